@@ -1,0 +1,193 @@
+/*
+ * tierkv_hip.h -- C ABI of the MI355X (gfx950) tiered paged KV-cache path.
+ *
+ * Plain pointers and sizes only: device pointers for tensors, a hipStream_t
+ * passed as void*, int status codes.  Every launch is asynchronous on the
+ * given stream and never synchronises.  The library keeps no pointer past a
+ * call.  Citations are file:line in xiaoMartintin/Paged_TierKV.
+ *
+ * Tier states: 0 HOT (fp16), 1 WARM (quantized), 2 COLD (evicted)
+ * (tierkv_policy.py:14-16, csrc/block_manager.cpp:9-13).
+ *
+ * Pool layouts (tierkv_policy.py:122-135, 828-841):
+ *   hot_k/hot_v   fp16  [hot_slots,  kv_heads, block_size, head_dim]
+ *   warm_k/warm_v       [warm_slots, kv_heads, block_size, head_dim]
+ *     TIERKV_WARM_REF_U8:    uint8 codes, k/v_scale and k/v_zero fp16
+ *                            [warm_slots, kv_heads, block_size, 1]
+ *                            (quantize_fp16_to_int8, tierkv_policy.py:21-36)
+ *     TIERKV_WARM_ABSMAX_I8: int8 codes, k/v_scale fp32 [warm_slots, kv_heads],
+ *                            k/v_zero unused (NULL)
+ *   block_table / block_states / block_lengths: int32 [batch, table_stride],
+ *     indexed by logical block; the table holds the slot of the block's
+ *     state-specific pool (compact layout) or a physical id that indexes both
+ *     pools (dense layout); COLD entries are never dereferenced.
+ */
+#ifndef TIERKV_HIP_H
+#define TIERKV_HIP_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define TIERKV_API __attribute__((visibility("default")))
+#else
+#define TIERKV_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes (the Python layer maps 1 -> ValueError, others -> RuntimeError). */
+#define TIERKV_OK 0
+#define TIERKV_ERR_INVALID 1     /* bad argument / shape */
+#define TIERKV_ERR_UNSUPPORTED 2 /* configuration outside the kernels' support */
+#define TIERKV_ERR_HIP 3         /* HIP launch/runtime error */
+#define TIERKV_ERR_WORKSPACE 4   /* workspace too small */
+#define TIERKV_ERR_STATE 5       /* BlockManager rule violation (RuntimeError) */
+
+#define TIERKV_DTYPE_F16 0
+#define TIERKV_DTYPE_BF16 1
+
+#define TIERKV_WARM_REF_U8 0
+#define TIERKV_WARM_ABSMAX_I8 1
+
+#define TIERKV_COLD_ZERO_LOGIT 0 /* reference: COLD tokens enter softmax with K=V=0 */
+#define TIERKV_COLD_MASKED 1     /* COLD blocks contribute nothing */
+
+/* Message of the last failing call on this thread ("" if none). */
+TIERKV_API const char* tierkv_last_error(void);
+
+/* Library/ABI version, for the Python loader's compatibility check. */
+TIERKV_API int32_t tierkv_abi_version(void);
+
+/* ---------------------------------------------------------------------- */
+/* Decode attention.  Replaces the launch in tierkv_decode_attention
+ * (tierkv_triton.py:272-465) of _tierkv_decode_attention_kernel
+ * (tierkv_triton.py:45-145) and the split/reduce pair (147-264).
+ *
+ * query  [batch, num_heads, head_dim] (== [B, H, 1, D] contiguous), f16/bf16.
+ * out    [batch, num_heads, head_dim] (== [B, 1, H, D]), same dtype as query.
+ * score_sums  NULL, or fp32 [batch, num_heads, table_stride]: per (head,
+ *   block) sum of softmax probabilities (tierkv_triton.py:121-145), zero for
+ *   blocks >= the sequence's block count.
+ * seq_num_blocks  NULL (every sequence has num_blocks blocks) or device
+ *   int32 [batch] (each clamped to num_blocks).
+ * workspace  device scratch of at least tierkv_decode_workspace_bytes(...)
+ *   bytes; its first 4 bytes are an error word the kernels set non-zero when
+ *   they skip a block whose slot or state is out of range.
+ * scaling  softmax scale (head_dim ** -0.5 in modeling_llama.py:315).
+ */
+TIERKV_API int32_t tierkv_decode_attention(
+    const void* query, int32_t query_dtype, void* out, float* score_sums,
+    const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
+    int64_t table_stride, const int32_t* seq_num_blocks, int32_t num_blocks,
+    const void* hot_k, const void* hot_v, int64_t hot_slots,
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    int32_t warm_format, int32_t cold_mode,
+    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    float scaling, int32_t splits_hint,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes tierkv_decode_attention needs for this shape. */
+TIERKV_API int64_t tierkv_decode_workspace_bytes(
+    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t num_blocks,
+    int32_t block_size, int32_t head_dim, int32_t with_scores, int32_t splits_hint);
+
+/* ---------------------------------------------------------------------- */
+/* Demotion HOT -> WARM.  Replaces CompactTieredKVTensorPool.demote_to_warm
+ * (tierkv_policy.py:1042-1068) / TieredKVTensorPool.demote_to_warm (329-361)
+ * and quantize_fp16_to_int8 (21-36), batched: job i quantizes tiles
+ * src_k/src_v[src_index[i]] (fp16 [kv_heads, block_size, head_dim], first
+ * lengths[i] tokens) into warm slot dst_slot[i].  Jobs whose indices are out
+ * of range are skipped (the Python layer validates them before launch).
+ *   REF_U8: per (token, head) codes/scale/zero bit-exact with the
+ *     reference's fp16 op sequence; tokens >= length are left untouched
+ *     (pad_tail = 0, compact demote_to_warm) or zero-padded with scale 1 /
+ *     zero 0 (pad_tail = 1, write_warm_block 989-995 / dense 350-356).
+ *   ABSMAX_I8: scale = max|x| / 127 over the valid tokens of the (block,
+ *     head) tile, codes rint(x / scale) clamped to [-127, 127]; tail codes 0.
+ * table_pos  NULL, or int32 [n]: flat indices into block_table/block_states
+ *   whose entries become (dst_slot[i], WARM) -- the _set_metadata rewrite
+ *   (tierkv_policy.py:917-926); negative entries are skipped.
+ */
+TIERKV_API int32_t tierkv_demote_to_warm(
+    const void* src_k, const void* src_v, int64_t src_tiles,
+    const int32_t* src_index, const int32_t* dst_slot, const int32_t* lengths, int32_t n,
+    void* warm_k, void* warm_v, int64_t warm_slots,
+    void* k_scale, void* k_zero, void* v_scale, void* v_zero,
+    int32_t warm_format, int32_t pad_tail,
+    int32_t* block_table, int32_t* block_states, const int32_t* table_pos,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
+/* Promotion WARM -> HOT.  Replaces promote_to_hot (tierkv_policy.py:1087-1115,
+ * 375-402) with dequantize_int8_to_fp16 (39-44): job i dequantizes the first
+ * lengths[i] tokens of warm slot src_slot[i] into hot slot dst_slot[i]
+ * (REF_U8: fp16 per-op rounding; ABSMAX_I8: fp16(fp32(q) * scale)).
+ * table_pos as in tierkv_demote_to_warm, entries become (dst_slot[i], HOT). */
+TIERKV_API int32_t tierkv_promote_to_hot(
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    const int32_t* src_slot, const int32_t* dst_slot, const int32_t* lengths, int32_t n,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t warm_format,
+    int32_t* block_table, int32_t* block_states, const int32_t* table_pos,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Block scores.  Per-block probability mass from softmax probabilities
+ * probs fp32 [batch, num_heads, tokens] -> out fp32 [batch, tokens/block_size]:
+ * sequential sum over heads, pairwise tree over the block's tokens, / heads,
+ * / max(len, 1).  lengths NULL (full blocks) or int32 [batch, n_blocks].
+ * The quantity of compute_block_scores (tierkv_policy.py:1380-1389) and
+ * block_scores_from_probability_sums (1905-1912) for a batch of sequences. */
+TIERKV_API int32_t tierkv_block_mass_from_probs(
+    const float* probs, const int32_t* lengths, float* out,
+    int32_t batch, int32_t num_heads, int32_t tokens, int32_t block_size, void* stream);
+
+/* block_scores_from_probability_sums (tierkv_policy.py:1905-1912), batched:
+ * score_sums fp32 [batch, num_heads, sums_stride], lengths int32
+ * [batch, len_stride] -> out fp32 [batch, num_blocks]. */
+TIERKV_API int32_t tierkv_block_scores_from_sums(
+    const float* score_sums, int64_t sums_stride, const int32_t* lengths, int64_t len_stride,
+    float* out, int32_t batch, int32_t num_heads, int32_t num_blocks, void* stream);
+
+/* Tier labels.  TierKVPolicyEngine.enforce_tiered_budget (mode 2,
+ * tierkv_policy.py:1434-1477) and enforce_budget (mode 1 with
+ * demoted_state, 1391-1432) for a batch of sequences: reserved HOT
+ * {0, n-1}, stable descending rank of the remaining scores, COLD sticky.
+ * mode 0 (hot_only) copies cur_states.  scores fp32 [batch, n]; cur_states
+ * and new_states int32 [batch, states_stride]. */
+TIERKV_API int32_t tierkv_tier_labels(
+    const float* scores, const int32_t* cur_states, int32_t* new_states, int64_t states_stride,
+    int32_t batch, int32_t num_blocks, int32_t hot_budget, int32_t warm_budget,
+    int32_t mode, int32_t demoted_state, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* BlockManager (host).  Replaces the pybind11 class of
+ * csrc/block_manager.cpp:22-134 with identical allocation order and errors:
+ * TIERKV_ERR_STATE carries the reference's message in tierkv_last_error(). */
+typedef struct tierkv_block_manager tierkv_block_manager;
+
+TIERKV_API int32_t tierkv_bm_create(int32_t total_blocks, tierkv_block_manager** out);   /* :24-34 */
+TIERKV_API void tierkv_bm_destroy(tierkv_block_manager* bm);
+TIERKV_API int32_t tierkv_bm_allocate_block(tierkv_block_manager* bm, int32_t seq_id, int32_t* physical_idx); /* :36-49 */
+TIERKV_API int32_t tierkv_bm_free_sequence(tierkv_block_manager* bm, int32_t seq_id);   /* :51-62 */
+TIERKV_API int32_t tierkv_bm_update_block_state(tierkv_block_manager* bm, int32_t seq_id,
+                                     int32_t logical_id, int32_t state);     /* :64-77 */
+/* Batched state write for logical ids [0, n) (a device policy tick's result);
+ * same checks as update_block_state, applied to every entry before any write. */
+TIERKV_API int32_t tierkv_bm_set_block_states(tierkv_block_manager* bm, int32_t seq_id,
+                                   const int32_t* states, int32_t n);
+TIERKV_API int32_t tierkv_bm_num_blocks(const tierkv_block_manager* bm, int32_t seq_id, int32_t* n);
+/* Copy up to capacity entries; *n receives the full count (:79-105). */
+TIERKV_API int32_t tierkv_bm_get_physical_indices(const tierkv_block_manager* bm, int32_t seq_id,
+                                       int32_t* out, int32_t capacity, int32_t* n);
+TIERKV_API int32_t tierkv_bm_get_states(const tierkv_block_manager* bm, int32_t seq_id,
+                             int32_t* out, int32_t capacity, int32_t* n);
+TIERKV_API int32_t tierkv_bm_num_free(const tierkv_block_manager* bm, int32_t* n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TIERKV_HIP_H */

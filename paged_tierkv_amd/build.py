@@ -1,0 +1,81 @@
+"""Build the gfx950 HIP library ``libtierkv_hip.so`` in-tree.
+
+``python -m paged_tierkv_amd.build`` (or ``__graft_entry__.build()``)
+compiles every HIP source for gfx950 with hipcc and the host-only C++ with
+g++, then links one shared library next to this file.  Objects go to
+``paged_tierkv_amd/_build``.  The library exports only the C ABI declared in
+``include/tierkv_hip.h``.
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = PKG / "_build"
+LIB = PKG / "libtierkv_hip.so"
+ARCH = os.environ.get("TIERKV_OFFLOAD_ARCH", "gfx950")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HIPCC = os.environ.get("HIPCC", os.path.join(ROCM, "bin", "hipcc"))
+
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    # Packed fp32 VALU ops are kept out of the generated code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
+]
+
+# Per-source extra flags: the codecs must not contract mul+add into FMA.
+HIP_SOURCES = {
+    "decode_attention.hip": [],
+    "quantize.hip": ["-ffp-contract=off"],
+    "block_score.hip": ["-ffp-contract=off"],
+}
+CXX_SOURCES = ["block_manager.cpp"]
+
+
+def _run(cmd):
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}\n{proc.stdout}")
+    return proc.stdout
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    include = ["-I", str(PKG.parent / "include")]
+    procs = []
+    objs = []
+    for src, extra in HIP_SOURCES.items():
+        obj = BUILD / (src + ".o")
+        cmd = [HIPCC, *HIP_FLAGS, *extra, *include, "-c", str(CSRC / src), "-o", str(obj)]
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs.append(obj)
+    for src in CXX_SOURCES:
+        obj = BUILD / (src + ".o")
+        cmd = ["g++", "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden", "-Wall", *include,
+               "-c", str(CSRC / src), "-o", str(obj)]
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
+        objs.append(obj)
+    errors = []
+    for cmd, proc in procs:
+        out, _ = proc.communicate()
+        if proc.returncode != 0:
+            errors.append(f"$ {' '.join(cmd)}\n{out}")
+        elif verbose and out.strip():
+            print(out)
+    if errors:
+        raise RuntimeError("HIP build failed:\n" + "\n".join(errors))
+    tmp = LIB.with_suffix(".so.tmp")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

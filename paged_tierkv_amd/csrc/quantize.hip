@@ -1,0 +1,384 @@
+// WARM-tier codecs on gfx950: demotion (HOT -> WARM quantize + table
+// rewrite) and promotion (WARM -> HOT dequantize + table rewrite).
+//
+// Replaces, batched over blocks, CompactTieredKVTensorPool.demote_to_warm /
+// promote_to_hot (tierkv_policy.py:1042-1115), the dense pool's versions
+// (329-402), write_warm_block (969-1002) and the codec pair
+// quantize_fp16_to_int8 / dequantize_int8_to_fp16 (tierkv_policy.py:21-44).
+//
+// Bit-exactness: the reference codec is a chain of ATen half ops, each
+// computed in fp32 and rounded to fp16; the kernels round after every op
+// with __float2half_rn, divide with IEEE __fdiv_rn and round with rintf
+// (half to even).  This file is compiled with -ffp-contract=off.
+
+#include "tierkv_common.h"
+
+namespace tierkv {
+
+constexpr int QT = 256;   // threads per quantize workgroup
+
+__device__ __forceinline__ float r16(float x) { return __half2float(__float2half_rn(x)); }
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int i = 1; i < QT / 64; ++i) r = fmaxf(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
+struct QuantJobs {
+  const __half* src[2];      // K, V source tiles [src_tiles, H_kv, bs, D]
+  int64_t src_tiles;
+  const int32_t* src_index;
+  const int32_t* dst_slot;
+  const int32_t* lengths;
+  void* warm[2];
+  int64_t warm_slots;
+  void* scale[2];
+  void* zero[2];
+  int32_t* table;
+  int32_t* states;
+  const int32_t* table_pos;
+  int32_t kv_heads, bs, D, pad_tail;
+};
+
+// ABSMAX_I8: one workgroup per (job, kv head, K|V) tile.
+__global__ __launch_bounds__(QT) void demote_absmax_kernel(QuantJobs q) {
+  __shared__ float red[QT / 64];
+  const int job = blockIdx.x;
+  const int h = blockIdx.y;
+  const int kv = blockIdx.z;
+  const int64_t si = q.src_index[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.src_tiles || di < 0 || di >= q.warm_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int64_t E = int64_t(q.bs) * q.D;
+  const int64_t valid = int64_t(len) * q.D;
+  const __half* src = q.src[kv] + (si * q.kv_heads + h) * E;
+  int8_t* dst = reinterpret_cast<int8_t*>(q.warm[kv]) + (di * q.kv_heads + h) * E;
+
+  float amax = 0.f;
+  for (int64_t e = threadIdx.x; e < valid; e += QT) amax = fmaxf(amax, fabsf(__half2float(src[e])));
+  amax = block_max(amax, red);
+  const float s = __fdiv_rn(amax, 127.f);
+  for (int64_t e = threadIdx.x; e < E; e += QT) {
+    int8_t c = 0;
+    if (e < valid && s != 0.f) {
+      float r = rintf(__fdiv_rn(__half2float(src[e]), s));
+      r = fminf(fmaxf(r, -127.f), 127.f);
+      c = static_cast<int8_t>(static_cast<int>(r));
+    }
+    dst[e] = c;
+  }
+  if (threadIdx.x == 0) {
+    reinterpret_cast<float*>(q.scale[kv])[di * q.kv_heads + h] = s;
+    if (q.table_pos && h == 0 && kv == 0) {
+      const int32_t pos = q.table_pos[job];
+      if (pos >= 0) {
+        q.table[pos] = static_cast<int32_t>(di);
+        q.states[pos] = WARM;
+      }
+    }
+  }
+}
+
+// Vectorised ABSMAX_I8 for head_dim % 8 == 0: each thread owns 8 halves.
+__global__ __launch_bounds__(QT) void demote_absmax_vec_kernel(QuantJobs q) {
+  __shared__ float red[QT / 64];
+  const int job = blockIdx.x;
+  const int h = blockIdx.y;
+  const int kv = blockIdx.z;
+  const int64_t si = q.src_index[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.src_tiles || di < 0 || di >= q.warm_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int64_t E = int64_t(q.bs) * q.D;
+  const int64_t valid = int64_t(len) * q.D;
+  const uint4* src = reinterpret_cast<const uint4*>(q.src[kv] + (si * q.kv_heads + h) * E);
+  uint2* dst = reinterpret_cast<uint2*>(reinterpret_cast<int8_t*>(q.warm[kv]) + (di * q.kv_heads + h) * E);
+  const int64_t nvec = E / 8;
+
+  // Tiles are at most 64 x 256 halves, i.e. <= 8 vectors per thread.
+  constexpr int MAXV = 8;
+  uint4 x[MAXV];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int64_t vi = threadIdx.x + int64_t(i) * QT;
+    if (vi < nvec) {
+      x[i] = src[vi];
+      if (vi * 8 < valid) {
+        const uint32_t w4[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          amax = fmaxf(amax, fabsf(half_lo(w4[k])));
+          amax = fmaxf(amax, fabsf(half_hi(w4[k])));
+        }
+      }
+    }
+  }
+  amax = block_max(amax, red);
+  const float s = __fdiv_rn(amax, 127.f);
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int64_t vi = threadIdx.x + int64_t(i) * QT;
+    if (vi < nvec) {
+      uint32_t out[2] = {0u, 0u};
+      if (vi * 8 < valid && s != 0.f) {
+        const uint32_t w4[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          float a = rintf(__fdiv_rn(half_lo(w4[k]), s));
+          float b = rintf(__fdiv_rn(half_hi(w4[k]), s));
+          a = fminf(fmaxf(a, -127.f), 127.f);
+          b = fminf(fmaxf(b, -127.f), 127.f);
+          const uint32_t ua = static_cast<uint32_t>(static_cast<int>(a)) & 0xffu;
+          const uint32_t ub = static_cast<uint32_t>(static_cast<int>(b)) & 0xffu;
+          out[k >> 1] |= (ua | (ub << 8)) << (16 * (k & 1));
+        }
+      }
+      dst[vi] = make_uint2(out[0], out[1]);
+    }
+  }
+  if (threadIdx.x == 0) {
+    reinterpret_cast<float*>(q.scale[kv])[di * q.kv_heads + h] = s;
+    if (q.table_pos && h == 0 && kv == 0) {
+      const int32_t pos = q.table_pos[job];
+      if (pos >= 0) {
+        q.table[pos] = static_cast<int32_t>(di);
+        q.states[pos] = WARM;
+      }
+    }
+  }
+}
+
+// REF_U8 (quantize_fp16_to_int8, tierkv_policy.py:21-36): one 16-lane group
+// per (token, head) row; one workgroup per (job, kv head, K|V) tile.
+__global__ __launch_bounds__(QT) void demote_ref_kernel(QuantJobs q) {
+  const int job = blockIdx.x;
+  const int h = blockIdx.y;
+  const int kv = blockIdx.z;
+  const int64_t si = q.src_index[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.src_tiles || di < 0 || di >= q.warm_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int D = q.D;
+  const int64_t tile_src = (si * q.kv_heads + h) * int64_t(q.bs);
+  const int64_t tile_dst = (di * q.kv_heads + h) * int64_t(q.bs);
+  uint8_t* codes = reinterpret_cast<uint8_t*>(q.warm[kv]);
+  __half* scale = reinterpret_cast<__half*>(q.scale[kv]);
+  __half* zero = reinterpret_cast<__half*>(q.zero[kv]);
+  const int sub = threadIdx.x & 15;
+  const int rows_per_pass = QT / 16;
+  for (int r0 = 0; r0 < q.bs; r0 += rows_per_pass) {
+    const int r = r0 + (threadIdx.x >> 4);
+    const bool row_ok = r < q.bs;
+    const __half* x = q.src[kv] + (tile_src + r) * D;
+    float mn = INFINITY, mx = -INFINITY;
+    if (row_ok && r < len) {
+      for (int d = sub; d < D; d += 16) {
+        const float v = __half2float(x[d]);
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+      }
+    }
+#pragma unroll
+    for (int m = 8; m >= 1; m >>= 1) {
+      mn = fminf(mn, __shfl_xor(mn, m, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, m, 16));
+    }
+    if (!row_ok) continue;
+    uint8_t* out = codes + (tile_dst + r) * D;
+    if (r < len) {
+      float sc = r16(__fdiv_rn(r16(mx - mn), 255.f));   // (max - min) / 255.0
+      if (sc == 0.f) sc = 1.f;                            // torch.where(scale == 0, 1, scale)
+      const float zp = r16(-rintf(r16(__fdiv_rn(mn, sc))));   // -round(min / scale)
+      for (int d = sub; d < D; d += 16) {
+        const float t = rintf(r16(__fdiv_rn(__half2float(x[d]), sc)));   // round(x / scale)
+        const float v = fminf(fmaxf(r16(t + zp), 0.f), 255.f);            // + zp, clamp(0, 255)
+        out[d] = static_cast<uint8_t>(v);
+      }
+      if (sub == 0) {
+        scale[tile_dst + r] = __float2half_rn(sc);
+        zero[tile_dst + r] = __float2half_rn(zp);
+      }
+    } else if (q.pad_tail) {
+      for (int d = sub; d < D; d += 16) out[d] = 0;
+      if (sub == 0) {
+        scale[tile_dst + r] = __float2half_rn(1.f);
+        zero[tile_dst + r] = __float2half_rn(0.f);
+      }
+    }
+  }
+  if (threadIdx.x == 0 && q.table_pos && h == 0 && kv == 0) {
+    const int32_t pos = q.table_pos[job];
+    if (pos >= 0) {
+      q.table[pos] = static_cast<int32_t>(di);
+      q.states[pos] = WARM;
+    }
+  }
+}
+
+struct DequantJobs {
+  const void* warm[2];
+  int64_t warm_slots;
+  const void* scale[2];
+  const void* zero[2];
+  const int32_t* src_slot;
+  const int32_t* dst_slot;
+  const int32_t* lengths;
+  __half* hot[2];
+  int64_t hot_slots;
+  int32_t* table;
+  int32_t* states;
+  const int32_t* table_pos;
+  int32_t kv_heads, bs, D, warm_format;
+};
+
+// promote_to_hot: dequantize the first `length` tokens of a WARM slot into
+// a HOT slot (dequantize_int8_to_fp16, tierkv_policy.py:39-44).
+__global__ __launch_bounds__(QT) void promote_kernel(DequantJobs q) {
+  const int job = blockIdx.x;
+  const int h = blockIdx.y;
+  const int kv = blockIdx.z;
+  const int64_t si = q.src_slot[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.warm_slots || di < 0 || di >= q.hot_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int D = q.D;
+  const int64_t E = int64_t(len) * D;
+  const int64_t src0 = (si * q.kv_heads + h) * int64_t(q.bs);
+  const int64_t dst0 = (di * q.kv_heads + h) * int64_t(q.bs);
+  __half* out = q.hot[kv] + dst0 * D;
+  if (q.warm_format == TIERKV_WARM_ABSMAX_I8) {
+    const int8_t* c = reinterpret_cast<const int8_t*>(q.warm[kv]) + src0 * D;
+    const float s = reinterpret_cast<const float*>(q.scale[kv])[si * q.kv_heads + h];
+    for (int64_t e = threadIdx.x; e < E; e += QT) out[e] = __float2half_rn(float(c[e]) * s);
+  } else {
+    const uint8_t* c = reinterpret_cast<const uint8_t*>(q.warm[kv]) + src0 * D;
+    const __half* sc = reinterpret_cast<const __half*>(q.scale[kv]) + src0;
+    const __half* zp = reinterpret_cast<const __half*>(q.zero[kv]) + src0;
+    for (int64_t e = threadIdx.x; e < E; e += QT) {
+      const int64_t r = e / D;
+      const float d = r16(float(c[e]) - __half2float(zp[r]));     // q.to(f16) - zero_point
+      out[e] = __float2half_rn(d * __half2float(sc[r]));           // * scale
+    }
+  }
+  if (threadIdx.x == 0 && q.table_pos && h == 0 && kv == 0) {
+    const int32_t pos = q.table_pos[job];
+    if (pos >= 0) {
+      q.table[pos] = static_cast<int32_t>(di);
+      q.states[pos] = HOT;
+    }
+  }
+}
+
+}  // namespace tierkv
+
+using namespace tierkv;
+
+extern "C" int32_t tierkv_demote_to_warm(
+    const void* src_k, const void* src_v, int64_t src_tiles,
+    const int32_t* src_index, const int32_t* dst_slot, const int32_t* lengths, int32_t n,
+    void* warm_k, void* warm_v, int64_t warm_slots,
+    void* k_scale, void* k_zero, void* v_scale, void* v_zero,
+    int32_t warm_format, int32_t pad_tail,
+    int32_t* block_table, int32_t* block_states, const int32_t* table_pos,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream_) {
+  clear_error();
+  if (n < 0) return fail(TIERKV_ERR_INVALID, "negative job count");
+  if (n == 0) return TIERKV_OK;
+  if (!src_k || !src_v || !src_index || !dst_slot || !lengths || !warm_k || !warm_v || !k_scale || !v_scale)
+    return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (table_pos && (!block_table || !block_states)) return fail(TIERKV_ERR_INVALID, "table_pos needs block_table and block_states");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim in [1, 256]");
+  if (n > 65535 * 64) return fail(TIERKV_ERR_UNSUPPORTED, "too many demotion jobs in one call");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  QuantJobs q{};
+  q.src[0] = reinterpret_cast<const __half*>(src_k);
+  q.src[1] = reinterpret_cast<const __half*>(src_v);
+  q.src_tiles = src_tiles;
+  q.src_index = src_index;
+  q.dst_slot = dst_slot;
+  q.lengths = lengths;
+  q.warm[0] = warm_k;
+  q.warm[1] = warm_v;
+  q.warm_slots = warm_slots;
+  q.scale[0] = k_scale;
+  q.scale[1] = v_scale;
+  q.zero[0] = k_zero;
+  q.zero[1] = v_zero;
+  q.table = block_table;
+  q.states = block_states;
+  q.table_pos = table_pos;
+  q.kv_heads = num_kv_heads;
+  q.bs = block_size;
+  q.D = head_dim;
+  q.pad_tail = pad_tail;
+  dim3 grid(n, num_kv_heads, 2);
+  if (warm_format == TIERKV_WARM_ABSMAX_I8) {
+    const bool vec = (head_dim % 8 == 0) && aligned16(src_k) && aligned16(src_v) &&
+                     (reinterpret_cast<uintptr_t>(warm_k) % 8 == 0) && (reinterpret_cast<uintptr_t>(warm_v) % 8 == 0);
+    if (vec) hipLaunchKernelGGL(demote_absmax_vec_kernel, grid, dim3(QT), 0, stream, q);
+    else hipLaunchKernelGGL(demote_absmax_kernel, grid, dim3(QT), 0, stream, q);
+    return check_launch("demote_absmax_kernel");
+  }
+  if (warm_format == TIERKV_WARM_REF_U8) {
+    if (!k_zero || !v_zero) return fail(TIERKV_ERR_INVALID, "reference format needs zero-point pools");
+    hipLaunchKernelGGL(demote_ref_kernel, grid, dim3(QT), 0, stream, q);
+    return check_launch("demote_ref_kernel");
+  }
+  return fail(TIERKV_ERR_INVALID, "unknown warm format");
+}
+
+extern "C" int32_t tierkv_promote_to_hot(
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    const int32_t* src_slot, const int32_t* dst_slot, const int32_t* lengths, int32_t n,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t warm_format,
+    int32_t* block_table, int32_t* block_states, const int32_t* table_pos,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream_) {
+  clear_error();
+  if (n < 0) return fail(TIERKV_ERR_INVALID, "negative job count");
+  if (n == 0) return TIERKV_OK;
+  if (!warm_k || !warm_v || !k_scale || !v_scale || !src_slot || !dst_slot || !lengths || !hot_k || !hot_v)
+    return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (warm_format == TIERKV_WARM_REF_U8 && (!k_zero || !v_zero))
+    return fail(TIERKV_ERR_INVALID, "reference format needs zero-point pools");
+  if (warm_format != TIERKV_WARM_REF_U8 && warm_format != TIERKV_WARM_ABSMAX_I8)
+    return fail(TIERKV_ERR_INVALID, "unknown warm format");
+  if (table_pos && (!block_table || !block_states)) return fail(TIERKV_ERR_INVALID, "table_pos needs block_table and block_states");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim in [1, 256]");
+  if (n > 65535 * 64) return fail(TIERKV_ERR_UNSUPPORTED, "too many promotion jobs in one call");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  DequantJobs q{};
+  q.warm[0] = warm_k;
+  q.warm[1] = warm_v;
+  q.warm_slots = warm_slots;
+  q.scale[0] = k_scale;
+  q.scale[1] = v_scale;
+  q.zero[0] = k_zero;
+  q.zero[1] = v_zero;
+  q.src_slot = src_slot;
+  q.dst_slot = dst_slot;
+  q.lengths = lengths;
+  q.hot[0] = reinterpret_cast<__half*>(hot_k);
+  q.hot[1] = reinterpret_cast<__half*>(hot_v);
+  q.hot_slots = hot_slots;
+  q.table = block_table;
+  q.states = block_states;
+  q.table_pos = table_pos;
+  q.kv_heads = num_kv_heads;
+  q.bs = block_size;
+  q.D = head_dim;
+  q.warm_format = warm_format;
+  hipLaunchKernelGGL(promote_kernel, dim3(n, num_kv_heads, 2), dim3(QT), 0, stream, q);
+  return check_launch("promote_kernel");
+}

@@ -1,0 +1,197 @@
+"""Tiered paged decode attention on MI355X -- drop-in for tierkv_triton.
+
+``tierkv_decode_attention`` keeps the signature, argument meaning, return
+contract and exceptions of the reference wrapper (tierkv_triton.py:272-465):
+
+* ValueError for a query that is not 4-D, batch != 1 with a 1-D table,
+  query_len != 1, non-GPU tensors, dtypes other than fp16/bf16,
+  ``num_blocks <= 0`` or ``num_blocks > block_table.shape[-1]``
+  (tierkv_triton.py:291-304);
+* RuntimeError when the HIP library is missing (tierkv_triton.py:267-269);
+* returns ``(out [B, 1, H, D], None)`` or, with ``return_scores``,
+  ``(out, score_sums)`` where ``score_sums`` is fp32 ``[H, max_blocks]``
+  (``[B, H, max_blocks]`` for batched tables), zero past ``num_blocks``
+  (tierkv_triton.py:371-377, .kiro bugfix contract).
+
+Additive, keyword-only extensions:
+
+* batched tables ``[B, max_blocks]`` with ``query [B, H, 1, D]`` and an
+  optional per-sequence ``seq_num_blocks``;
+* the WARM format is taken from the pools: uint8 codes + fp16 per-token
+  scale/zero (the reference codec) or int8 codes + fp32 per-(slot, head)
+  absmax scales (``k_zero``/``v_zero`` may be None);
+* ``cold_mode``: ``"zero_logit"`` (reference: COLD tokens enter the softmax
+  with K = V = 0) or ``"masked"`` (COLD blocks contribute nothing);
+* ``splits``: split-K factor (default: chosen from the launch size).  The
+  reference's ``TIERKV_SPLIT_DECODE`` switch is not needed: the kernel always
+  splits when it pays, and the result equals the single pass up to fp32
+  re-association.
+
+Set ``TIERKV_CHECK_ERRORS=1`` to make every call synchronise and raise if
+the kernel skipped a block whose slot or state was out of range.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_workspaces: dict = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Cached per-device scratch (the reference caches its score placeholder
+    the same way, tierkv_triton.py:24-40).  Zero-filled once: its first word
+    is the kernels' error flag."""
+    key = (device.type, device.index)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def workspace_error_word(device) -> int:
+    """Read (and clear) the kernels' error flag for ``device`` (synchronises)."""
+    device = torch.device(device)
+    ws = _workspaces.get((device.type, device.index))
+    if ws is None:
+        return 0
+    word = int(ws[:4].view(torch.int32).item())
+    if word:
+        ws[:4].zero_()
+    return word
+
+
+def warm_format_of(warm_k_pool: torch.Tensor, k_scale: torch.Tensor) -> int:
+    if warm_k_pool.dtype == torch.uint8 and k_scale.dtype == torch.float16:
+        return _lib.WARM_REF_U8
+    if warm_k_pool.dtype == torch.int8 and k_scale.dtype == torch.float32:
+        return _lib.WARM_ABSMAX_I8
+    raise ValueError(
+        "WARM pools must be uint8 codes with fp16 scales (reference format) or int8 codes "
+        "with fp32 per-(slot, head) scales (absmax format).")
+
+
+_COLD_MODES = {"zero_logit": _lib.COLD_ZERO_LOGIT, "masked": _lib.COLD_MASKED}
+
+
+def tierkv_decode_attention(
+    query_states: torch.Tensor,
+    block_table: torch.Tensor,
+    block_states: torch.Tensor,
+    block_lengths: torch.Tensor,
+    hot_k_pool: torch.Tensor,
+    hot_v_pool: torch.Tensor,
+    warm_k_pool: torch.Tensor,
+    warm_v_pool: torch.Tensor,
+    k_scale: torch.Tensor,
+    k_zero: torch.Tensor | None,
+    v_scale: torch.Tensor,
+    v_zero: torch.Tensor | None,
+    num_blocks: int,
+    num_key_value_groups: int,
+    scaling: float,
+    return_scores: bool = False,
+    *,
+    cold_mode: str = "zero_logit",
+    seq_num_blocks=None,
+    splits: int | None = None,
+):
+    """Decode attention over a tiered paged KV cache (see module docstring)."""
+    lib = _lib.lib()  # RuntimeError if the HIP library is not built
+    if query_states.ndim != 4:
+        raise ValueError("query_states must have shape [batch, num_heads, query_len, head_dim].")
+    batched = block_table.ndim == 2
+    if not batched and query_states.shape[0] != 1:
+        raise ValueError("TierKV decode supports batch size 1 only with a 1-D block table.")
+    if query_states.shape[-2] != 1:
+        raise ValueError("TierKV decode supports query_len == 1 only.")
+    if not query_states.is_cuda:
+        raise ValueError("TierKV decode requires GPU (HIP) tensors.")
+    if query_states.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("TierKV decode supports fp16/bf16 query tensors only.")
+    if int(num_blocks) <= 0:
+        raise ValueError("num_blocks must be positive.")
+    if int(num_blocks) > block_table.shape[-1]:
+        raise ValueError("num_blocks exceeds the provided block table length.")
+    if cold_mode not in _COLD_MODES:
+        raise ValueError('cold_mode must be "zero_logit" or "masked".')
+
+    batch, num_heads, _, head_dim = query_states.shape
+    if batched and block_table.shape[0] != batch:
+        raise ValueError("batched block tables must have one row per query batch entry.")
+    for name, t in (("block_table", block_table), ("block_states", block_states),
+                    ("block_lengths", block_lengths)):
+        _lib.require_gpu_tensor(t, name)
+        if t.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32.")
+        if t.shape != block_table.shape:
+            raise ValueError(f"{name} must have the block table's shape.")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous.")
+    pools = (hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool)
+    for name, t in zip(("hot_k_pool", "hot_v_pool", "warm_k_pool", "warm_v_pool"), pools):
+        _lib.require_gpu_tensor(t, name)
+        if t.ndim != 4 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous [slots, kv_heads, block_size, head_dim] tensor.")
+    if hot_k_pool.dtype != torch.float16 or hot_v_pool.dtype != torch.float16:
+        raise ValueError("HOT pools must be fp16.")
+    kv_heads, block_size, pool_dim = (int(x) for x in hot_k_pool.shape[1:])
+    if pool_dim != head_dim or tuple(warm_k_pool.shape[1:]) != (kv_heads, block_size, head_dim):
+        raise ValueError("pool geometry does not match the query head_dim.")
+    if hot_v_pool.shape != hot_k_pool.shape or warm_v_pool.shape != warm_k_pool.shape:
+        raise ValueError("K and V pools must have identical shapes.")
+    if kv_heads * int(num_key_value_groups) != num_heads:
+        raise ValueError("num_heads must equal kv_heads * num_key_value_groups.")
+    fmt = warm_format_of(warm_k_pool, k_scale)
+    metas = (k_scale, v_scale) if fmt == _lib.WARM_ABSMAX_I8 else (k_scale, k_zero, v_scale, v_zero)
+    for t in metas:
+        if t is None:
+            raise ValueError("reference-format WARM pools need k_zero and v_zero.")
+        _lib.require_gpu_tensor(t, "warm metadata")
+        if not t.is_contiguous() or t.shape[0] != warm_k_pool.shape[0]:
+            raise ValueError("warm scale/zero tensors must be contiguous with one entry per WARM slot.")
+
+    query = query_states.contiguous()
+    table_stride = int(block_table.shape[-1])
+    device = query.device
+    out = torch.empty((batch, 1, num_heads, head_dim), device=device, dtype=query.dtype)
+    score_sums = None
+    if return_scores:
+        score_sums = torch.empty((batch, num_heads, table_stride), device=device, dtype=torch.float32)
+
+    snb = None
+    if seq_num_blocks is not None:
+        snb = torch.as_tensor(seq_num_blocks, dtype=torch.int32, device=device).contiguous()
+        if snb.numel() != batch:
+            raise ValueError("seq_num_blocks needs one entry per sequence.")
+
+    splits_hint = int(splits) if splits else 0
+    need = lib.tierkv_decode_workspace_bytes(batch, num_heads, kv_heads, int(num_blocks), block_size,
+                                             head_dim, int(return_scores), splits_hint)
+    if need < 0:
+        raise ValueError("invalid decode geometry.")
+    ws = _workspace(device, need)
+    rc = lib.tierkv_decode_attention(
+        _lib.ptr(query), _lib.DTYPE_BF16 if query.dtype == torch.bfloat16 else _lib.DTYPE_F16,
+        _lib.ptr(out), _lib.ptr(score_sums),
+        _lib.ptr(block_table), _lib.ptr(block_states), _lib.ptr(block_lengths), table_stride,
+        _lib.ptr(snb), int(num_blocks),
+        _lib.ptr(hot_k_pool), _lib.ptr(hot_v_pool), int(hot_k_pool.shape[0]),
+        _lib.ptr(warm_k_pool), _lib.ptr(warm_v_pool), int(warm_k_pool.shape[0]),
+        _lib.ptr(k_scale), _lib.ptr(k_zero) if fmt == _lib.WARM_REF_U8 else None,
+        _lib.ptr(v_scale), _lib.ptr(v_zero) if fmt == _lib.WARM_REF_U8 else None,
+        fmt, _COLD_MODES[cold_mode],
+        batch, num_heads, kv_heads, block_size, head_dim,
+        float(scaling), splits_hint,
+        _lib.ptr(ws), int(ws.numel()), _lib.stream_of(device))
+    _lib.check(rc, "tierkv_decode_attention")
+    if _lib.env_flag("TIERKV_CHECK_ERRORS"):
+        word = workspace_error_word(device)
+        if word:
+            raise RuntimeError(f"TierKV decode skipped blocks with out-of-range slot/state (flag {word}).")
+    if score_sums is not None and not batched:
+        score_sums = score_sums[0]
+    return out, score_sums

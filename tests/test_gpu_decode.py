@@ -1,0 +1,182 @@
+"""GPU parity of the tiered decode-attention kernels against the CPU oracle
+(oracle.decode restates _eager_reference_decode, tierkv_triton.py:708-820).
+
+Tolerance: BASELINE's 2e-3 absolute / 1e-2 relative vs the fp32 reference
+for outputs; the same for per-block probability sums."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from paged_tierkv_amd import workloads as W
+from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention, workspace_error_word
+
+from helpers import assert_close, oracle_decode, oracle_warm, to_gpu_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(case, fmt, device, cold_mode=None, return_scores=False, query_dtype=torch.float16, **kw):
+    warm = oracle_warm(case, fmt)
+    args = to_gpu_inputs(case, warm, device, query_dtype)
+    out, scores = tierkv_decode_attention(**args, return_scores=return_scores,
+                                          cold_mode=cold_mode or case.cold_mode, **kw)
+    torch.cuda.synchronize()
+    return warm, out, scores
+
+
+def _check(case, fmt, device, cold_mode=None, return_scores=False, seqs=None, query_dtype=torch.float16, **kw):
+    print(f"[decode] case={case.name} fmt={fmt} cold={cold_mode or case.cold_mode} scores={return_scores} "
+          f"dtype={query_dtype} kw={kw}", flush=True)
+    warm, out, scores = _run(case, fmt, device, cold_mode, return_scores, query_dtype, **kw)
+    seqs = list(range(case.batch)) if seqs is None else seqs
+    res = oracle_decode(case, warm, fmt, cold_mode, return_scores, seqs=seqs)
+    exp_out, exp_sc = (res if return_scores else (res, None))
+    got = out[seqs, 0].float().cpu().numpy()
+    assert_close(got, exp_out, what=f"{case.name} output")
+    if return_scores:
+        sc = scores.cpu().numpy()
+        if sc.ndim == 2:
+            sc = sc[None]
+        assert_close(sc[seqs], exp_sc, what=f"{case.name} score_sums")
+    assert workspace_error_word(device) == 0
+    return out, scores
+
+
+# -- BASELINE configs -------------------------------------------------------
+
+def test_c1_absmax_masked(device):
+    _check(W.config1(), "absmax_i8", device, return_scores=True)
+
+
+def test_c1_reference_format_zero_logit(device):
+    _check(W.config1(), "ref_u8", device, cold_mode="zero_logit", return_scores=True)
+
+
+def test_c1_bf16_query(device):
+    case = W.config1()
+    case.query = case.query.to(torch.bfloat16).to(torch.float16)   # the oracle sees the bf16 values
+    _check(case, "absmax_i8", device, query_dtype=torch.bfloat16)
+
+
+def test_c3_llama3_subset(device):
+    _check(W.config3(), "absmax_i8", device, seqs=[0, 13, 31])
+
+
+def test_c3_scores_subset(device):
+    _check(W.config3(batch=4), "absmax_i8", device, return_scores=True)
+
+
+def test_c4_long_context_subset(device):
+    _check(W.config4(), "absmax_i8", device, seqs=[0, 3])
+
+
+# -- shapes, formats and modes ------------------------------------------------
+
+@pytest.mark.parametrize("groups", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize("fmt", ["absmax_i8", "ref_u8"])
+def test_gqa_dims_formats(device, groups, head_dim, fmt):
+    kv = 2
+    nb = 37
+    gen = torch.Generator().manual_seed(groups * 1000 + head_dim)
+    lengths = torch.randint(1, 17, (3, nb), generator=gen)
+    lengths[:, :-1] = torch.where(torch.rand((3, nb - 1), generator=gen) < 0.8, 16, lengths[:, :-1])
+    case = W.make_tiered_case(f"gqa{groups}_d{head_dim}", 3, kv * groups, kv, head_dim, nb, 9, 17,
+                              seed=groups + head_dim, lengths=lengths, max_blocks=nb + 5)
+    for cold in ("masked", "zero_logit"):
+        _check(case, fmt, device, cold_mode=cold, return_scores=True)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7])
+def test_split_invariance(device, splits):
+    case = W.make_tiered_case("splits", 2, 32, 8, 128, 100, 12, 60, seed=7)
+    out_auto = _check(case, "absmax_i8", device)[0]
+    out_s = _check(case, "absmax_i8", device, splits=splits)[0]
+    assert_close(out_s.float().cpu().numpy(), out_auto.float().cpu().numpy(), atol=1e-3, rtol=1e-3,
+                 what="split vs auto")
+
+
+def test_seq_num_blocks_ragged(device):
+    case = W.make_tiered_case("ragged", 4, 16, 4, 64, 48, 8, 24, seed=11)
+    snb = [48, 1, 17, 30]
+    warm = oracle_warm(case, "absmax_i8")
+    args = to_gpu_inputs(case, warm, device)
+    out, sc = tierkv_decode_attention(**args, return_scores=True, cold_mode="masked", seq_num_blocks=snb)
+    torch.cuda.synchronize()
+    for b, n in enumerate(snb):
+        sub = W.make_tiered_case("ragged", 4, 16, 4, 64, 48, 8, 24, seed=11)
+        sub.num_blocks = n
+        exp_out, exp_sc = oracle_decode(sub, warm, "absmax_i8", "masked", True, seqs=[b])
+        assert_close(out[b, 0].float().cpu().numpy(), exp_out[0], what=f"seq {b} out")
+        assert_close(sc[b].cpu().numpy(), exp_sc[0], what=f"seq {b} scores")
+        assert float(sc[b, :, n:].abs().sum()) == 0.0
+
+
+def test_all_cold(device):
+    case = W.make_tiered_case("allcold", 2, 8, 4, 64, 6, 0, 0, seed=3)
+    case.block_states[:, :6] = W.COLD
+    for cold in ("masked", "zero_logit"):
+        _, out, sc = _run(case, "absmax_i8", device, cold_mode=cold, return_scores=True)
+        assert float(out.float().abs().max()) == 0.0
+        if cold == "zero_logit":
+            s = sc.cpu().numpy()[:, :, :6].sum(-1)
+            np.testing.assert_allclose(s, 1.0, atol=1e-5)
+
+
+def test_invalid_slot_is_skipped_and_flagged(device, monkeypatch):
+    case = W.make_tiered_case("badslot", 1, 8, 4, 64, 4, 4, 0, seed=5)
+    case.block_table[0, 2] = 10_000   # out of range HOT slot: never dereferenced
+    warm = oracle_warm(case, "absmax_i8")
+    args = to_gpu_inputs(case, warm, device)
+    monkeypatch.setenv("TIERKV_CHECK_ERRORS", "1")
+    with pytest.raises(RuntimeError, match="out-of-range"):
+        tierkv_decode_attention(**args, cold_mode="masked")
+
+
+# -- the reference's own decode tests (main.py:452-634; tierkv_triton.py:823-1097)
+
+def _ref_geometry_case(states, lengths, kv_heads, q_heads, head_dim, seed):
+    nb = len(states)
+    case = W.make_tiered_case("refgeom", 1, q_heads, kv_heads, head_dim, nb, nb, 0, seed=seed,
+                              lengths=[lengths], max_blocks=nb + 4, layout="dense",
+                              dense_pool_blocks=nb + 4)
+    case.block_states[0, :nb] = torch.tensor(states, dtype=torch.int32)
+    return case
+
+
+@pytest.mark.parametrize("states,lengths", [
+    ([0, 0], [16, 5]),                       # 21 tokens all HOT (main.py:498-535)
+    ([1, 1], [16, 5]),                       # all WARM (main.py:545-566)
+    ([0, 1, 2], [16, 16, 9]),                # mixed H/W/C (main.py:568-598)
+    ([0, 1, 0, 1, 0, 0], [16] * 5 + [1]),   # > 4 blocks (main.py:600-624)
+])
+def test_reference_main_geometry(device, states, lengths):
+    # kv_heads 2, q heads 4, head_dim 16: generic kernel path.
+    case = _ref_geometry_case(states, lengths, 2, 4, 16, seed=len(states))
+    _check(case, "ref_u8", device, cold_mode="zero_logit", return_scores=True)
+
+
+@pytest.mark.parametrize("states", [
+    [0] * 6,                                 # 2.1 all-HOT with scores (tierkv_triton.py:901-938)
+    [0, 1, 2, 0, 1],                         # 2.2 HOT/WARM/COLD/HOT/WARM (943-989)
+    [0, 1, 0, 0, 1, 0, 0, 1],                # 2.3 split path, 8 blocks (994-1050)
+])
+def test_reference_preservation_geometry(device, states):
+    # kv_heads 4, q heads 8, head_dim 64, block 16: fast path.
+    case = _ref_geometry_case(states, [16] * len(states), 4, 8, 64, seed=10 + len(states))
+    _check(case, "ref_u8", device, cold_mode="zero_logit", return_scores=True)
+    # The reference API: 1-D tables, scores [H, max_blocks], (out, None) without scores.
+    args = to_gpu_inputs(case, oracle_warm(case, "ref_u8"), device)
+    for k in ("block_table", "block_states", "block_lengths"):
+        args[k] = args[k][0].contiguous()
+    out, sc = tierkv_decode_attention(**args, return_scores=True)
+    assert sc.shape == (8, len(states) + 4)
+    np.testing.assert_allclose(sc[:, : len(states)].sum(-1).cpu().numpy(), 1.0, atol=2e-2)
+    exp_out, exp_sc = oracle_decode(case, oracle_warm(case, "ref_u8"), "ref_u8", "zero_logit", True)
+    assert_close(out[:, 0].float().cpu().numpy(), exp_out, what="1-D table output")
+    assert_close(sc.cpu().numpy()[None], exp_sc, what="1-D table scores")
+    out2, none = tierkv_decode_attention(**args, return_scores=False)
+    assert none is None and out2.shape == (1, 1, 8, 64)
