@@ -20,6 +20,23 @@ def _i32(x, device) -> torch.Tensor:
     return t.to(device).contiguous()
 
 
+def _table_positions(table_pos, block_table, block_states, n, device):
+    """Validate (on the host, where the positions usually come from) and
+    upload the flat table positions of a migration batch."""
+    if table_pos is None:
+        return None
+    if block_table is None or block_states is None:
+        raise ValueError("table_pos needs block_table and block_states.")
+    host = torch.as_tensor(table_pos, dtype=torch.int32)
+    if host.numel() != n:
+        raise ValueError("table_pos needs one entry per job.")
+    if host.device.type == "cpu" and host.numel():
+        hi = int(host.max())
+        if hi >= min(block_table.numel(), block_states.numel()):
+            raise ValueError("table_pos entry outside the block table.")
+    return host.to(device).contiguous()
+
+
 def _check_tiles(t: torch.Tensor, name: str, dtype) -> None:
     _lib.require_gpu_tensor(t, name)
     if t.dtype != dtype or t.ndim != 4 or not t.is_contiguous():
@@ -50,11 +67,7 @@ def demote_to_warm(src_k, src_v, src_index, dst_slot, lengths, warm_k, warm_v, k
     n = int(src_index.numel())
     if dst_slot.numel() != n or lengths.numel() != n:
         raise ValueError("src_index, dst_slot and lengths must have the same length.")
-    tp = None
-    if table_pos is not None:
-        tp = _i32(table_pos, device)
-        if tp.numel() != n or block_table is None or block_states is None:
-            raise ValueError("table_pos needs block_table/block_states and one entry per job.")
+    tp = _table_positions(table_pos, block_table, block_states, n, device)
     rc = lib.tierkv_demote_to_warm(
         _lib.ptr(src_k), _lib.ptr(src_v), int(src_k.shape[0]),
         _lib.ptr(src_index), _lib.ptr(dst_slot), _lib.ptr(lengths), n,
@@ -82,7 +95,7 @@ def promote_to_hot(warm_k, warm_v, k_scale, k_zero, v_scale, v_zero, src_slot, d
     dst_slot = _i32(dst_slot, device)
     lengths = _i32(lengths, device)
     n = int(src_slot.numel())
-    tp = _i32(table_pos, device) if table_pos is not None else None
+    tp = _table_positions(table_pos, block_table, block_states, n, device)
     rc = lib.tierkv_promote_to_hot(
         _lib.ptr(warm_k), _lib.ptr(warm_v), int(warm_k.shape[0]),
         _lib.ptr(k_scale), _lib.ptr(k_zero), _lib.ptr(v_scale), _lib.ptr(v_zero),

@@ -1,0 +1,78 @@
+"""The C ABI library (CPU): it loads, exports every entry point that
+include/tierkv_hip.h declares, and rejects bad arguments before any launch;
+the Python wrappers raise the reference's exception types."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from paged_tierkv_amd import _lib
+from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tierkv_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"TIERKV_API\s+[\w\s\*]+?\b(tierkv_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = _declared()
+    assert len(names) >= 19
+    lib = _lib.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (tierkv_\w+)", out))
+    assert exported == set(names), exported ^ set(names)
+
+
+def test_abi_version_and_errors_without_gpu():
+    lib = _lib.lib()
+    assert lib.tierkv_abi_version() == _lib.ABI_VERSION
+    rc = lib.tierkv_decode_attention(
+        None, 0, None, None,            # query, dtype, out, score_sums
+        None, None, None, 0, None, 0,   # table, states, lengths, stride, seq_num_blocks, num_blocks
+        None, None, 0, None, None, 0,   # hot pools + slots, warm pools + slots
+        None, None, None, None, 0, 0,   # scales / zeros, warm format, cold mode
+        0, 0, 0, 0, 0,                  # batch, heads, kv heads, block size, head dim
+        ctypes.c_float(1.0), 0, None, 0, None)
+    assert rc == _lib.TIERKV_ERR_INVALID
+    assert "null" in _lib.last_error()
+    assert lib.tierkv_decode_workspace_bytes(0, 1, 1, 1, 16, 64, 0, 0) < 0
+    assert lib.tierkv_decode_workspace_bytes(32, 32, 8, 256, 16, 128, 1, 0) > 0
+    assert lib.tierkv_tier_labels(None, None, None, 4, 1, 4, 2, 1, 7, 1, None) == _lib.TIERKV_ERR_INVALID
+    assert lib.tierkv_block_mass_from_probs(None, None, None, 1, 1, 16, 16, None) == _lib.TIERKV_ERR_INVALID
+
+
+def test_decode_wrapper_contract_on_cpu_tensors():
+    q = torch.zeros((1, 8, 1, 64), dtype=torch.float16)
+    table = torch.zeros(4, dtype=torch.int32)
+    pool = torch.zeros((2, 4, 16, 64), dtype=torch.float16)
+    wpool = torch.zeros((2, 4, 16, 64), dtype=torch.uint8)
+    meta = torch.ones((2, 4, 16, 1), dtype=torch.float16)
+    args = [table, table, table, pool, pool, wpool, wpool, meta, meta, meta, meta]
+    with pytest.raises(ValueError, match="shape"):
+        tierkv_decode_attention(q[0], *args, num_blocks=2, num_key_value_groups=2, scaling=0.125)
+    with pytest.raises(ValueError, match="batch size 1"):
+        tierkv_decode_attention(q.repeat(2, 1, 1, 1), *args, num_blocks=2, num_key_value_groups=2, scaling=0.125)
+    with pytest.raises(ValueError, match="query_len"):
+        tierkv_decode_attention(q.repeat(1, 1, 2, 1), *args, num_blocks=2, num_key_value_groups=2, scaling=0.125)
+    with pytest.raises(ValueError, match="GPU"):
+        tierkv_decode_attention(q, *args, num_blocks=2, num_key_value_groups=2, scaling=0.125)
+
+
+def test_missing_library_raises_runtime_error(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libtierkv_hip.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.lib()

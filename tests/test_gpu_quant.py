@@ -1,0 +1,173 @@
+"""GPU parity of the demotion (quantize) and promotion (dequantize) kernels:
+codes, scales, zero points and table rewrites bit-exact against the oracle
+codec, which is itself pinned to golden vectors written by the reference's
+quantize_fp16_to_int8 (tierkv_policy.py:21-36)."""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec
+from paged_tierkv_amd import kernels, workloads as W
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def _eq(a, b, what):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} != {b.shape}"
+    if a.dtype in (np.float16, np.float32):
+        a = a.view(np.uint16 if a.dtype == np.float16 else np.uint32)
+        b = b.view(a.dtype)
+    bad = a != b
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {a.size} differ; first {np.argwhere(bad)[:3].tolist()}"
+
+
+@pytest.mark.parametrize("bs,dim", [(16, 128), (16, 64), (4, 16), (8, 12)])
+def test_absmax_demote_bit_exact(device, bs, dim):
+    print(f"[quant] absmax bs={bs} dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(bs * 100 + dim)
+    tiles, heads = 23, 3
+    src_k = (torch.randn((tiles, heads, bs, dim), generator=g) * 2).half()
+    src_v = torch.randn((tiles, heads, bs, dim), generator=g).half()
+    src_k[5] = 0                                        # zero tile -> scale 0, codes 0
+    jobs = torch.tensor([3, 5, 0, 22, 11, 7], dtype=torch.int32)
+    dst = torch.tensor([4, 0, 9, 2, 7, 1], dtype=torch.int32)
+    lens = torch.tensor([bs, bs, 1, bs - 1, bs, 2], dtype=torch.int32)
+    warm_k = torch.full((10, heads, bs, dim), 77, dtype=torch.int8, device=device)
+    warm_v = warm_k.clone()
+    ks = torch.full((10, heads), -1.0, device=device)
+    vs = ks.clone()
+    table = torch.full((2, 8), -1, dtype=torch.int32, device=device)
+    states = torch.zeros((2, 8), dtype=torch.int32, device=device)
+    pos = torch.tensor([0, 3, 8, 15, -1, 9], dtype=torch.int32)
+    kernels.demote_to_warm(src_k.to(device), src_v.to(device), jobs, dst, lens, warm_k, warm_v, ks, None, vs, None,
+                           warm_format="absmax_i8", block_table=table, block_states=states, table_pos=pos)
+    torch.cuda.synchronize()
+    for i in range(len(jobs)):
+        s, d, n = int(jobs[i]), int(dst[i]), int(lens[i])
+        for name, src, codes, sc in (("k", src_k, warm_k, ks), ("v", src_v, warm_v, vs)):
+            q, scale = codec.quantize_absmax_i8(src[s, :, :n].numpy())
+            _eq(codes[d, :, :n].cpu().numpy(), q, f"{name} codes job {i}")
+            _eq(sc[d].cpu().numpy(), scale, f"{name} scale job {i}")
+            assert int(codes[d, :, n:].abs().sum()) == 0, "tail codes must be 0"
+    t = table.view(-1).cpu().numpy()
+    st = states.view(-1).cpu().numpy()
+    for i, p in enumerate(pos.tolist()):
+        if p >= 0:
+            assert t[p] == int(dst[i]) and st[p] == 1
+    assert (t[[1, 2, 4]] == -1).all()
+
+
+def test_c2a_demotion_full_size_bit_exact(device):
+    case = W.config2a()
+    print(f"[quant] C2(a) demote {len(case.demote_logical)} of {case.hot_k.shape[0]} blocks", flush=True)
+    n = len(case.demote_logical)
+    warm_k = torch.empty((n, 8, 16, 128), dtype=torch.int8, device=device)
+    warm_v = torch.empty_like(warm_k)
+    ks = torch.empty((n, 8), device=device)
+    vs = torch.empty_like(ks)
+    table = case.table.to(device)
+    states = case.states.to(device)
+    src = case.table[0, case.demote_logical]
+    kernels.demote_to_warm(case.hot_k.to(device), case.hot_v.to(device), src, case.warm_slots,
+                           torch.full((n,), 16, dtype=torch.int32), warm_k, warm_v, ks, None, vs, None,
+                           warm_format="absmax_i8", block_table=table, block_states=states,
+                           table_pos=case.demote_logical.to(torch.int32))
+    torch.cuda.synchronize()
+    qk, sk = codec.quantize_absmax_i8(case.hot_k[src.long()].numpy())
+    qv, sv = codec.quantize_absmax_i8(case.hot_v[src.long()].numpy())
+    _eq(warm_k.cpu().numpy(), qk, "C2a K codes")
+    _eq(warm_v.cpu().numpy(), qv, "C2a V codes")
+    _eq(ks.cpu().numpy(), sk, "C2a K scales")
+    _eq(vs.cpu().numpy(), sv, "C2a V scales")
+    exp_table = case.table.clone()
+    exp_states = case.states.clone()
+    exp_table[0, case.demote_logical] = case.warm_slots
+    exp_states[0, case.demote_logical] = 1
+    _eq(table.cpu().numpy(), exp_table.numpy(), "C2a table")
+    _eq(states.cpu().numpy(), exp_states.numpy(), "C2a states")
+
+
+def test_reference_codec_demote_matches_golden(device):
+    g = np.load(os.path.join(GOLDEN, "codec_ref_u8.npz"))
+    x = torch.from_numpy(g["x"])                      # [7, 4, 16, 64] fp16
+    tiles, heads, bs, dim = x.shape
+    idx = torch.arange(tiles, dtype=torch.int32)
+    warm_k = torch.zeros((tiles, heads, bs, dim), dtype=torch.uint8, device=device)
+    warm_v = warm_k.clone()
+    sc = lambda: torch.zeros((tiles, heads, bs, 1), dtype=torch.float16, device=device)
+    ks, kz, vs, vz = sc(), sc(), sc(), sc()
+    xd = x.to(device)
+    kernels.demote_to_warm(xd, xd, idx, idx, torch.full((tiles,), bs, dtype=torch.int32), warm_k, warm_v,
+                           ks, kz, vs, vz, warm_format="ref_u8")
+    torch.cuda.synchronize()
+    _eq(warm_k.cpu().numpy(), g["q"], "codes vs reference golden")
+    _eq(ks.cpu().numpy(), g["scale"], "scale vs reference golden")
+    _eq(kz.cpu().numpy(), g["zero"], "zero vs reference golden")
+    # promotion back to fp16 == dequantize_int8_to_fp16 of the golden codes
+    hot = torch.zeros((tiles, heads, bs, dim), dtype=torch.float16, device=device)
+    hot_v = hot.clone()
+    kernels.promote_to_hot(warm_k, warm_v, ks, kz, vs, vz, idx, idx, torch.full((tiles,), bs, dtype=torch.int32),
+                           hot, hot_v, warm_format="ref_u8")
+    torch.cuda.synchronize()
+    _eq(hot.cpu().numpy(), g["deq"], "promote vs reference dequant golden")
+
+
+@pytest.mark.parametrize("pad_tail", [False, True])
+def test_reference_codec_partial_blocks(device, pad_tail):
+    g = torch.Generator().manual_seed(9)
+    heads, bs, dim = 2, 16, 64
+    src = torch.randn((4, heads, bs, dim), generator=g).half()
+    lens = torch.tensor([16, 5, 1, 9], dtype=torch.int32)
+    idx = torch.arange(4, dtype=torch.int32)
+    warm = torch.full((4, heads, bs, dim), 200, dtype=torch.uint8, device=device)
+    warm_v = warm.clone()
+    ks = torch.full((4, heads, bs, 1), 7.0, dtype=torch.float16, device=device)
+    kz, vs, vz = ks.clone(), ks.clone(), ks.clone()
+    kernels.demote_to_warm(src.to(device), src.to(device), idx, idx, lens, warm, warm_v, ks, kz, vs, vz,
+                           warm_format="ref_u8", pad_tail=pad_tail)
+    torch.cuda.synchronize()
+    for i in range(4):
+        n = int(lens[i])
+        q, s, z = codec.quantize_ref_u8(src[i, :, :n].numpy())
+        _eq(warm[i, :, :n].cpu().numpy(), q, f"codes {i}")
+        _eq(ks[i, :, :n].cpu().numpy(), s, f"scale {i}")
+        _eq(kz[i, :, :n].cpu().numpy(), z, f"zero {i}")
+        tail_codes = warm[i, :, n:].cpu().numpy()
+        if pad_tail:   # write_warm_block (tierkv_policy.py:989-995)
+            assert (tail_codes == 0).all() and (ks[i, :, n:].cpu().numpy() == 1).all()
+            assert (kz[i, :, n:].cpu().numpy() == 0).all()
+        else:          # compact demote_to_warm leaves the tail untouched
+            assert (tail_codes == 200).all() and (ks[i, :, n:].cpu().numpy() == 7).all()
+
+
+def test_absmax_promote_bit_exact(device):
+    g = torch.Generator().manual_seed(4)
+    codes = torch.randint(-127, 128, (5, 2, 16, 128), generator=g, dtype=torch.int8)
+    scales = torch.rand((5, 2), generator=g) * 0.1
+    lens = torch.tensor([16, 3, 16, 7, 1], dtype=torch.int32)
+    src = torch.tensor([4, 0, 2, 1, 3], dtype=torch.int32)
+    dst = torch.tensor([0, 1, 2, 3, 4], dtype=torch.int32)
+    hot = torch.full((5, 2, 16, 128), 9.0, dtype=torch.float16, device=device)
+    hot_v = hot.clone()
+    cd = codes.to(device)
+    sd = scales.to(device)
+    table = torch.zeros(16, dtype=torch.int32, device=device)
+    states = torch.ones(16, dtype=torch.int32, device=device)
+    kernels.promote_to_hot(cd, cd, sd, None, sd, None, src, dst, lens, hot, hot_v, warm_format="absmax_i8",
+                           block_table=table, block_states=states, table_pos=[1, 2, 3, 4, 5])
+    torch.cuda.synchronize()
+    for i in range(5):
+        n = int(lens[i])
+        exp = (codes[int(src[i]), :, :n].float() * scales[int(src[i])][:, None, None]).half()
+        _eq(hot[i, :, :n].cpu().numpy(), exp.numpy(), f"promote {i}")
+        assert (hot[i, :, n:].cpu() == 9.0).all()
+    assert table[1:6].tolist() == [0, 1, 2, 3, 4] and states[1:6].tolist() == [0] * 5
