@@ -31,7 +31,10 @@ HIP_FLAGS = [
 
 # Per-source extra flags: the codecs must not contract mul+add into FMA.
 HIP_SOURCES = {
-    "decode_attention.hip": [],
+    # The tier branches of the tile loader store to different elements of the
+    # same register arrays; LLVM's common-store sinking would merge them into
+    # one dynamically indexed store and push the tiles to scratch memory.
+    "decode_attention.hip": ["-mllvm", "-simplifycfg-sink-common=false"],
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
 }

@@ -4,35 +4,50 @@
 // split/reduce pair (147-264) behind tierkv_decode_attention
 // (tierkv_triton.py:272-465).
 //
-// Fast path (block_size 16, head_dim 64 or 128, GQA group <= 16):
-//   * one workgroup = (sequence, kv head, split of logical blocks), 4 waves;
-//     the whole GQA group is served by one pass over each K/V byte;
-//   * the split's HOT/WARM blocks are compacted into an LDS list at start,
-//     so COLD blocks cost no bytes and waves get a balanced round-robin share;
-//   * one wave handles one 16-token block at a time with MFMA 16x16x16 f16:
-//       S^T = K * Q^T   (A = K rows straight from HBM, B = Q^T, N = heads)
-//       O^T += V^T * P^T (B = P^T is exactly S^T's accumulator layout)
-//     WARM int8 codes are turned into fp16 in registers; absmax scales are
-//     folded into the logits (s_k) and into P (s_v);
-//   * online softmax in base 2 with wave-local state, merged across waves in
-//     LDS and across splits in tierkv_decode_merge_kernel;
-//   * the next block's tile is loaded while the current one is computed.
+// Fast path (block_size 16, head_dim 64 or 128, GQA group <= 16), one kernel:
+//   * workgroup = (sequence, kv head, split), 8 waves (4 when the GQA group
+//     exceeds 8); the whole GQA group is served by one pass over each K/V
+//     byte;
+//   * every workgroup scans its sequence's table row and keeps the resident
+//     (HOT first, then WARM) blocks whose rank is congruent to its split, so
+//     splits and waves get the same number of tiles and a similar HOT/WARM
+//     mix; COLD blocks cost no bytes;
+//   * one wave handles one 16-token block (tile) at a time with MFMA
+//     16x16x16 f16:  S^T = K Q^T  (A = K rows as loaded, B = Q^T), then
+//     O^T += V^T P^T  (B = P^T is exactly S^T's accumulator layout);
+//   * WARM int8 codes become fp16 by a byte permute under the exponent of
+//     1024 (codes + 1152 exactly); the constant offset is removed once per
+//     head (q . 1152 from the logits, 1152 * sum(P) from the output), and the
+//     absmax scales are folded into the logits (s_k) and into P (s_v);
+//   * the next tile is prefetched into a second register buffer (ping-pong),
+//     the tier branch is wave-uniform;
+//   * online softmax in base 2 whose running maximum is re-based only when a
+//     logit exceeds it by more than LAZY_T (P stays <= 2^LAZY_T);
+//   * waves merge in LDS; when a sequence is split over several workgroups
+//     the last one to finish (an atomic counter per (sequence, kv head))
+//     merges the partials (log-sum-exp combine, tierkv_triton.py:231-264)
+//     and finalises the per-block probability sums.
 // Generic path (any block_size <= 64, head_dim <= 256, any group): one wave
-// per (sequence, q head), the reference's two-pass structure.
+// per (sequence, q head), the reference kernel's structure.
 
 #include "tierkv_common.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cfloat>
 #include <cmath>
 
 namespace tierkv {
 
-constexpr int FBS = 16;          // tokens per block on the fast path
-constexpr int NW = 4;            // waves per fast-path workgroup
-constexpr int MAX_CHUNK = 256;   // logical blocks per split (LDS list capacity)
-constexpr float PBOOST = 64.f;   // P is scaled by 2^6 before its fp16 cast
+constexpr int FBS = 16;            // tokens per block on the fast path
+constexpr int MAX_LIST = 512;      // resident blocks per workgroup (LDS list)
+constexpr int MAX_WAVES = 8;
+constexpr float PBOOST = 64.f;     // P is scaled by 2^6 before its fp16 cast
+constexpr float LAZY_T = 8.f;      // log2 headroom of the running maximum
+constexpr float FOLD_MAX = 2.f;    // WARM V scales above this are applied to V
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr float BIAS_I8 = 1152.f;  // fp16 value of an int8 code c is 1152 + c
+constexpr float BIAS_U8 = 1024.f;  // fp16 value of a uint8 code u is 1024 + u
 
 struct DecodeParams {
   const void* q;
@@ -56,13 +71,13 @@ struct DecodeParams {
   int32_t batch, num_heads, kv_heads, block_size, head_dim, groups;
   float scale_log2;   // scaling * log2(e)
   float scaling;
-  int32_t splits, blocks_per_split;
+  int32_t splits;
   float* ws_acc;      // [units][splits][G][D]
   float* ws_ml;       // [units][splits][G][2]
-  float* ws_stage;    // [B][H][num_blocks][2]  (block max, block sum)
+  float* ws_stage;    // [B][H][num_blocks][2]  (block reference max, block sum)
+  int32_t* ws_cnt;    // [units] arrival counters (zero between launches)
   int32_t* ws_err;
   float* score_sums;  // [B][H][table_stride] or null
-  int32_t direct_out;
 };
 
 __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
@@ -71,401 +86,309 @@ __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
   return nb;
 }
 
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// Device-coherent (agent scope) relaxed stores and loads: the store is
+// written through to the level shared by all XCDs, the load does not hit a
+// stale copy.  Workgroups of one split exchange partials and per-block
+// statistics with them; ordering comes from waiting for the stores to
+// complete before the arrival counter is incremented.
+__device__ __forceinline__ void store_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_dev(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // --------------------------------------------------------------------------
 // Fast path
 // --------------------------------------------------------------------------
 
-template <int D, int WF>
+// One tile in registers.  Lane (n = lane & 15, g = lane >> 4):
+//   k: token n, dims g*D/4 .. +D/4 (HOT: D/8 dwords of halves; WARM: D/16
+//      dwords of codes);
+//   v: tokens 4g + j (j = 0..3), dims n*D/16 .. +D/16, row j at v[j*D/32]
+//      (HOT: D/32 dwords of halves; WARM: D/64 dwords of codes);
+//   m: WARM metadata (absmax: s_k, s_v; reference format: fp16 pairs of the
+//      per-token k scale, k zero, v scale, v zero of tokens 4g .. 4g+3).
+template <int D>
 struct Tile {
-  // HOT: lane's K slice (D/4 halves) and 4 tokens x D/16 halves of V.
-  // WARM: the same bytes as 1-byte codes (first half of the arrays).
   uint32_t k[D / 8];
-  uint32_t v[4][D / 32];
-  float kmeta[2];        // REF_U8: this lane's token K scale / zero; ABSMAX: s_k
-  float vmeta[4][2];     // REF_U8: per-token V scale / zero; ABSMAX: [0][0] = s_v
+  uint32_t v[D / 8];
+  uint32_t m[8];
 };
 
 template <int D, int WF>
-__device__ __forceinline__ void load_tile(const DecodeParams& p, int kvh, int4 e, int lane,
-                                          Tile<D, WF>& t) {
-  const int n = lane & 15;   // token row for K, dim group for V
-  const int g = lane >> 4;   // dim quarter for K, token quad for V
-  const int64_t slot = e.y;
-  const int64_t tile0 = (slot * p.kv_heads + kvh) * FBS;   // first token row of the tile
-  if (e.w == HOT) {
-    const uint4* kp = reinterpret_cast<const uint4*>(p.hot_k + (tile0 + n) * D + g * (D / 4));
+__device__ __forceinline__ void load_tile(const DecodeParams& p, int kvh, int state, int slot, int lane,
+                                          Tile<D>& t) {
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;   // first token row of the tile
+  if (state == HOT) {
+    const uint4* kp = reinterpret_cast<const uint4*>(p.hot_k + tile0 * D) + n * (D / 8) + g * (D / 32);
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
-      uint4 x = kp[i];
+      const uint4 x = kp[i];
       t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const __half* vp = p.hot_v + (tile0 + 4 * g + j) * D + n * (D / 16);
       if constexpr (D == 128) {
-        uint4 x = *reinterpret_cast<const uint4*>(vp);
-        t.v[j][0] = x.x; t.v[j][1] = x.y; t.v[j][2] = x.z; t.v[j][3] = x.w;
+        const uint4 x = *reinterpret_cast<const uint4*>(vp);
+        t.v[4 * j + 0] = x.x; t.v[4 * j + 1] = x.y; t.v[4 * j + 2] = x.z; t.v[4 * j + 3] = x.w;
       } else {
-        uint2 x = *reinterpret_cast<const uint2*>(vp);
-        t.v[j][0] = x.x; t.v[j][1] = x.y;
+        const uint2 x = *reinterpret_cast<const uint2*>(vp);
+        t.v[2 * j + 0] = x.x; t.v[2 * j + 1] = x.y;
       }
     }
   } else {
-    const uint8_t* wk = reinterpret_cast<const uint8_t*>(p.warm_k);
-    const uint8_t* wv = reinterpret_cast<const uint8_t*>(p.warm_v);
-    const uint4* kp = reinterpret_cast<const uint4*>(wk + (tile0 + n) * D + g * (D / 4));
+    const uint8_t* wk = reinterpret_cast<const uint8_t*>(p.warm_k) + tile0 * D;
+    const uint8_t* wv = reinterpret_cast<const uint8_t*>(p.warm_v) + tile0 * D;
+    const uint4* kp = reinterpret_cast<const uint4*>(wk + n * D + g * (D / 4));
 #pragma unroll
     for (int i = 0; i < D / 64; ++i) {
-      uint4 x = kp[i];
+      const uint4 x = kp[i];
       t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint8_t* vp = wv + (tile0 + 4 * g + j) * D + n * (D / 16);
+      const uint8_t* vp = wv + (4 * g + j) * D + n * (D / 16);
+      // Same row stride as the HOT layout (D/32 dwords), first D/64 used:
+      // both tiers then write the same registers at the same indices.
       if constexpr (D == 128) {
-        uint2 x = *reinterpret_cast<const uint2*>(vp);
-        t.v[j][0] = x.x; t.v[j][1] = x.y;
+        const uint2 x = *reinterpret_cast<const uint2*>(vp);
+        t.v[4 * j + 0] = x.x; t.v[4 * j + 1] = x.y;
       } else {
-        t.v[j][0] = *reinterpret_cast<const uint32_t*>(vp);
+        t.v[2 * j] = *reinterpret_cast<const uint32_t*>(vp);
       }
     }
     if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-      const float* ks = reinterpret_cast<const float*>(p.k_scale);
-      const float* vs = reinterpret_cast<const float*>(p.v_scale);
-      t.kmeta[0] = ks[slot * p.kv_heads + kvh];
-      t.vmeta[0][0] = vs[slot * p.kv_heads + kvh];
+      const int64_t si = int64_t(slot) * p.kv_heads + kvh;
+      t.m[0] = __float_as_uint(reinterpret_cast<const float*>(p.k_scale)[si]);
+      t.m[1] = __float_as_uint(reinterpret_cast<const float*>(p.v_scale)[si]);
     } else {
-      const __half* ks = reinterpret_cast<const __half*>(p.k_scale);
-      const __half* kz = reinterpret_cast<const __half*>(p.k_zero);
-      const __half* vs = reinterpret_cast<const __half*>(p.v_scale);
-      const __half* vz = reinterpret_cast<const __half*>(p.v_zero);
-      t.kmeta[0] = __half2float(ks[tile0 + n]);
-      t.kmeta[1] = __half2float(kz[tile0 + n]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        t.vmeta[j][0] = __half2float(vs[tile0 + 4 * g + j]);
-        t.vmeta[j][1] = __half2float(vz[tile0 + 4 * g + j]);
-      }
+      const int64_t mi = tile0 + 4 * g;   // halves; 8-byte aligned
+      const uint2 ks = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_scale) + mi);
+      const uint2 kz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_zero) + mi);
+      const uint2 vs = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_scale) + mi);
+      const uint2 vz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_zero) + mi);
+      t.m[0] = ks.x; t.m[1] = ks.y; t.m[2] = kz.x; t.m[3] = kz.y;
+      t.m[4] = vs.x; t.m[5] = vs.y; t.m[6] = vz.x; t.m[7] = vz.y;
     }
   }
 }
 
-// K operand (A of S^T = K Q^T) for MFMA step s: dims g*D/4 + 4s .. +3 of
-// token n.
-template <int D, int WF>
-__device__ __forceinline__ f16x4 k_operand(const Tile<D, WF>& t, int state, int s) {
-  if (state == HOT) return as_f16x4(t.k[2 * s], t.k[2 * s + 1]);
-  const uint32_t w = t.k[s];
-  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-    uint32_t lo, hi;
-    i8x4_to_f16x4(w, lo, hi);
-    return as_f16x4(lo, hi);
-  } else {
-    const float sc = t.kmeta[0], zp = t.kmeta[1];
-    const float a0 = (float(w & 0xffu) - zp) * sc;
-    const float a1 = (float((w >> 8) & 0xffu) - zp) * sc;
-    const float a2 = (float((w >> 16) & 0xffu) - zp) * sc;
-    const float a3 = (float(w >> 24) - zp) * sc;
-    return as_f16x4(pack_f16x2(a0, a1), pack_f16x2(a2, a3));
-  }
+__device__ __forceinline__ float half_of(const uint32_t* pair, int r) {
+  const uint32_t w = pair[r >> 1];
+  return (r & 1) ? half_hi(w) : half_lo(w);
 }
 
-// V operand (A of O^T += V^T P^T) for step s: {V[4g+j][n*D/16 + s]}_{j=0..3}.
-template <int D, int WF>
-__device__ __forceinline__ f16x4 v_operand(const Tile<D, WF>& t, int state, int s) {
-  if (state == HOT) {
-    const int dw = s >> 1;
-    if (s & 1) {
-      return as_f16x4((t.v[0][dw] >> 16) | (t.v[1][dw] & 0xffff0000u),
-                      (t.v[2][dw] >> 16) | (t.v[3][dw] & 0xffff0000u));
-    }
-    return as_f16x4((t.v[0][dw] & 0xffffu) | (t.v[1][dw] << 16),
-                    (t.v[2][dw] & 0xffffu) | (t.v[3][dw] << 16));
-  }
-  const int dw = s >> 2, sh = (s & 3) * 8;
-  const uint32_t b0 = (t.v[0][dw] >> sh) & 0xffu;
-  const uint32_t b1 = (t.v[1][dw] >> sh) & 0xffu;
-  const uint32_t b2 = (t.v[2][dw] >> sh) & 0xffu;
-  const uint32_t b3 = (t.v[3][dw] >> sh) & 0xffu;
-  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-    uint32_t lo, hi;
-    i8x4_to_f16x4(b0 | (b1 << 8) | (b2 << 16) | (b3 << 24), lo, hi);
-    return as_f16x4(lo, hi);
-  } else {
-    const float v0 = (float(b0) - t.vmeta[0][1]) * t.vmeta[0][0];
-    const float v1 = (float(b1) - t.vmeta[1][1]) * t.vmeta[1][0];
-    const float v2 = (float(b2) - t.vmeta[2][1]) * t.vmeta[2][0];
-    const float v3 = (float(b3) - t.vmeta[3][1]) * t.vmeta[3][0];
-    return as_f16x4(pack_f16x2(v0, v1), pack_f16x2(v2, v3));
-  }
-}
+// Per-wave softmax state.  acc holds O^T: acc[s][r] = O[head n][(4g + r) * DS + s]
+// scaled by PBOOST and 2^-m_run; l and corr are this lane's partial sums
+// over its four tokens (reduced over g at the end).
+template <int D>
+struct WaveState {
+  f32x4 acc[D / 16];
+  float m_run;
+  float l_part;
+  float corr;
+};
 
-template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT>
-__global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeParams p) {
-  constexpr int DS = D / 16;   // MFMA steps per block for each product
-  extern __shared__ float s_dyn[];               // [NW][G][D] partial accumulators
-  __shared__ int4 s_list[MAX_CHUNK];             // (block, slot, len, state)
-  __shared__ int s_wave_cnt[NW];
-  __shared__ int s_cold_tokens;
-  __shared__ float s_m[NW][16];
-  __shared__ float s_l[NW][16];
-
-  const int G = p.groups;
-  const int splits = p.splits;
-  const int wg = blockIdx.x;
-  const int split = wg % splits;
-  const int unit = wg / splits;
-  const int b = unit / p.kv_heads;
-  const int kvh = unit % p.kv_heads;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int nb = seq_blocks(p, b);
-  const int c0 = split * p.blocks_per_split;
-  const int c1 = min(c0 + p.blocks_per_split, nb);
-
-  if (tid == 0) s_cold_tokens = 0;
-
-  // ---- compact this split's resident (HOT/WARM) blocks into LDS ----------
-  bool res = false;
-  int4 ent = make_int4(0, 0, 0, COLD);
-  const int idx = c0 + tid;
-  if (tid < p.blocks_per_split && idx < c1) {
-    const int64_t o = int64_t(b) * p.table_stride + idx;
-    const int st = p.states[o];
-    const int slot = p.table[o];
-    const int len = min(max(p.lengths[o], 0), FBS);
-    ent = make_int4(idx, slot, len, st);
-    if (st == HOT || st == WARM) {
-      const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-      const bool slot_ok = slot >= 0 && slot < cap;
-      if (!slot_ok && len > 0) atomicOr(p.ws_err, 1);
-      res = slot_ok && len > 0;
-      if (SCORES && !res) {
-        for (int h = 0; h < G; ++h) {
-          float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + kvh * G + h) * p.num_blocks + idx) * 2;
-          sp[0] = -INFINITY;
-          sp[1] = 0.f;
-        }
-      }
-    } else if (st != COLD) {
-      atomicOr(p.ws_err, 2);
-    }
-  }
-  __syncthreads();
-  if (COLD_ZERO && ent.w == COLD && ent.z > 0) atomicAdd(&s_cold_tokens, ent.z);
-  const uint64_t mask = __ballot(res);
-  if (lane == 0) s_wave_cnt[w] = __popcll(mask);
-  __syncthreads();
-  int base = 0, nres = 0;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    base += (i < w) ? s_wave_cnt[i] : 0;
-    nres += s_wave_cnt[i];
-  }
-  if (res) s_list[base + __popcll(mask & ((1ull << lane) - 1ull))] = ent;
-  __syncthreads();
-
-  // ---- per-wave online softmax over the list ------------------------------
-  const int n = lane & 15;
+template <int D, int WF, bool SCORES>
+__device__ __forceinline__ void process_tile(const DecodeParams& p, const Tile<D>& t, int state, int blk, int len,
+                                             int lane, bool head_ok, int b, int qh, const uint32_t* qv,
+                                             float qsum, WaveState<D>& ws) {
+  constexpr int DS = D / 16;
   const int g = lane >> 4;
-  const bool head_ok = n < G;
-  const int qh = kvh * G + n;
 
-  uint32_t qv[D / 8];
-  {
-    const QT* qp = reinterpret_cast<const QT*>(p.q) + (int64_t(b) * p.num_heads + (head_ok ? qh : 0)) * D + g * (D / 4);
+  // ---- S^T = K Q^T ------------------------------------------------------
+  f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (state == HOT) {
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) {
-      float a = head_ok ? to_f32<QT>(qp[2 * i]) : 0.f;
-      float c = head_ok ? to_f32<QT>(qp[2 * i + 1]) : 0.f;
-      qv[i] = pack_f16x2(a, c);
+    for (int s = 0; s < DS; ++s)
+      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(t.k[2 * s], t.k[2 * s + 1]),
+                                                   as_f16x4(qv[2 * s], qv[2 * s + 1]), sacc, 0, 0, 0);
+  } else {
+#pragma unroll
+    for (int s = 0; s < DS; ++s) {
+      const f16x4 a = (WF == TIERKV_WARM_ABSMAX_I8) ? i8x4_plus1152(t.k[s]) : u8x4_plus1024(t.k[s]);
+      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, as_f16x4(qv[2 * s], qv[2 * s + 1]), sacc, 0, 0, 0);
     }
   }
 
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  f32x4 acc[DS];
+  // ---- logits (base 2) for tokens 4g + r ----------------------------------
+  float x[4];
+  if (state == HOT) {
 #pragma unroll
-  for (int s = 0; s < DS; ++s) acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < 4; ++r) x[r] = sacc[r] * p.scale_log2;
+  } else if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
+    const float c1 = p.scale_log2 * __uint_as_float(t.m[0]);
+    const float c0 = -BIAS_I8 * qsum * c1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = fmaf(sacc[r], c1, c0);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float c1 = p.scale_log2 * half_of(&t.m[0], r);
+      const float c0 = -(BIAS_U8 + half_of(&t.m[2], r)) * qsum * c1;
+      x[r] = fmaf(sacc[r], c1, c0);
+    }
+  }
+  if (len < FBS) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (4 * g + r >= len) x[r] = -INFINITY;
+  }
 
-  Tile<D, WF> cur, nxt;
-  int k = w;
-  if (k < nres) load_tile<D, WF>(p, kvh, s_list[k], lane, cur);
-  while (k < nres) {
-    const int4 e = s_list[k];
-    const int kn = k + NW;
-    if (kn < nres) load_tile<D, WF>(p, kvh, s_list[kn], lane, nxt);
-    const int state = e.w;
-
-    // S^T = K Q^T: lane holds S[head n][token 4g + j].
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+  // ---- lazy online softmax ---------------------------------------------------
+  const float lm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  if (__any(head_ok && lm > ws.m_run + LAZY_T)) {
+    float tm = fmaxf(lm, shfl_xor_f(lm, 16));
+    tm = fmaxf(tm, shfl_xor_f(tm, 32));
+    const float m_new = fmaxf(ws.m_run, tm);
+    const float alpha = (ws.m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ws.m_run - m_new);
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      const f16x4 a = k_operand<D, WF>(cur, state, s);
-      const f16x4 bq = as_f16x4(qv[2 * s], qv[2 * s + 1]);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bq, sacc, 0, 0, 0);
-    }
-    float coef = p.scale_log2;
-    float vcoef = PBOOST;
-    if (state == WARM && WF == TIERKV_WARM_ABSMAX_I8) {
-      coef *= cur.kmeta[0];
-      vcoef *= cur.vmeta[0][0];
-    }
-    float x[4];
-    float bm = -INFINITY;
+    for (int s = 0; s < DS; ++s) ws.acc[s] *= alpha;
+    ws.l_part *= alpha;
+    ws.corr *= alpha;
+    ws.m_run = m_new;
+  }
+  float pr[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const bool valid = (4 * g + j) < e.z;
-      x[j] = valid ? sacc[j] * coef : -INFINITY;
-      bm = fmaxf(bm, x[j]);
-    }
-    bm = fmaxf(bm, shfl_xor_f(bm, 16));
-    bm = fmaxf(bm, shfl_xor_f(bm, 32));
-    float ex[4];
-    float ls = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      ex[j] = (x[j] == -INFINITY) ? 0.f : exp2f(x[j] - bm);
-      ls += ex[j];
-    }
-    ls += shfl_xor_f(ls, 16);
+  for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(x[r] - ws.m_run);
+  const float psum = (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  ws.l_part += psum;
+  if constexpr (SCORES) {
+    float ls = psum + shfl_xor_f(psum, 16);
     ls += shfl_xor_f(ls, 32);
-    if (SCORES && g == 0 && head_ok) {
-      float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + e.x) * 2;
-      sp[0] = bm;
-      sp[1] = ls;
+    if (g == 0 && head_ok) {
+      float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
+      store_dev(sp, ws.m_run);
+      store_dev(sp + 1, ls);
     }
-    const float m_new = fmaxf(m_run, bm);
-    const float alpha = (m_run == -INFINITY) ? 0.f : exp2f(m_run - m_new);
-    const float beta = exp2f(bm - m_new);
-    l_run = l_run * alpha + ls * beta;
-    m_run = m_new;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int s = 0; s < DS; ++s) acc[s] *= alpha;
-    }
-    const float pscale = beta * vcoef;
-    const f16x4 pf = as_f16x4(pack_f16x2(ex[0] * pscale, ex[1] * pscale),
-                              pack_f16x2(ex[2] * pscale, ex[3] * pscale));
-    if (e.z < FBS) {
-      // Partial block: zero the V rows past the length so stale tail data
-      // (weighted by p == 0) cannot inject Inf/NaN through 0 * x.
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (4 * g + j >= e.z) {
-#pragma unroll
-          for (int i = 0; i < D / 32; ++i) cur.v[j][i] = 0u;
-          cur.vmeta[j][0] = 0.f;
-          cur.vmeta[j][1] = 0.f;
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      const f16x4 av = v_operand<D, WF>(cur, state, s);
-      acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pf, acc[s], 0, 0, 0);
-    }
-    cur = nxt;
-    k = kn;
   }
 
-  // ---- merge the NW waves in LDS -------------------------------------------
-  float* s_acc = s_dyn;   // [NW][G][D]
-  if (head_ok) {
-    if (g == 0) {
-      s_m[w][n] = m_run;
-      s_l[w][n] = l_run;
-    }
-    // acc[s][j] holds O[head n][(4g + j) * DS + s].
+  // ---- O^T += V^T P^T ----------------------------------------------------------
+  if (state == HOT) {
+    const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int s = 0; s < DS; ++s) {
+      constexpr int RW = D / 32;   // dwords per V row
+      const int dw = s >> 1;
+      const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
+      const f16x4 av = as_f16x4(perm_b32(t.v[1 * RW + dw], t.v[0 * RW + dw], sel),
+                                perm_b32(t.v[3 * RW + dw], t.v[2 * RW + dw], sel));
+      ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pf, ws.acc[s], 0, 0, 0);
+    }
+    return;
+  }
+  // WARM: transpose the four rows' codes so that vt[s] holds the four tokens
+  // of dim n*DS + s.
+  constexpr int RS = D / 32;   // row stride in t.v
+  uint32_t vt[DS];
+#pragma unroll
+  for (int w4 = 0; w4 < D / 64; ++w4)
+    transpose_bytes4x4(t.v[0 * RS + w4], t.v[1 * RS + w4], t.v[2 * RS + w4], t.v[3 * RS + w4], &vt[4 * w4]);
+  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
+    const float sv = __uint_as_float(t.m[1]);
+    if (sv <= FOLD_MAX) {
+      const float f = PBOOST * sv;
+      const uint32_t p01 = pack_f16x2(pr[0] * f, pr[1] * f);
+      const uint32_t p23 = pack_f16x2(pr[2] * f, pr[3] * f);
+      // The offset is removed with the same fp16 P values the MFMA multiplies.
+      ws.corr += BIAS_I8 * ((half_lo(p01) + half_hi(p01)) + (half_lo(p23) + half_hi(p23)));
+      const f16x4 pf = as_f16x4(p01, p23);
+#pragma unroll
+      for (int s = 0; s < DS; ++s)
+        ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_plus1152(vt[s]), pf, ws.acc[s], 0, 0, 0);
+    } else {
+      // Large V scale: apply it to V (fp16(c * s_v)) so that P stays in range.
+      const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
-        s_acc[(w * G + n) * D + (4 * g + j) * DS + s] = acc[s][j];
+        const uint32_t w = vt[s];
+        const float a0 = float(int8_t(w & 0xffu)) * sv;
+        const float a1 = float(int8_t((w >> 8) & 0xffu)) * sv;
+        const float a2 = float(int8_t((w >> 16) & 0xffu)) * sv;
+        const float a3 = float(int8_t(w >> 24)) * sv;
+        ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(pack_f16x2(a0, a1), pack_f16x2(a2, a3)), pf,
+                                                          ws.acc[s], 0, 0, 0);
       }
     }
-  }
-  __syncthreads();
-  const float cold_tokens = COLD_ZERO ? float(s_cold_tokens) : 0.f;
-  for (int i = tid; i < G * D; i += NW * 64) {
-    const int h = i / D;
-    const int d = i - h * D;
-    float M = -INFINITY;
+  } else {
+    float sv[4], zv[4];
+    bool big = false;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, s_m[ww][h]);
-    float L = 0.f, A = 0.f;
+    for (int r = 0; r < 4; ++r) {
+      sv[r] = half_of(&t.m[4], r);
+      zv[r] = half_of(&t.m[6], r);
+      big = big || (sv[r] > FOLD_MAX);
+    }
+    if (!__any(big)) {
+      const uint32_t p01 = pack_f16x2(pr[0] * (PBOOST * sv[0]), pr[1] * (PBOOST * sv[1]));
+      const uint32_t p23 = pack_f16x2(pr[2] * (PBOOST * sv[2]), pr[3] * (PBOOST * sv[3]));
+      // The offset (1024 + zero) is removed with the fp16 P values the MFMA uses.
+      ws.corr += half_lo(p01) * (BIAS_U8 + zv[0]) + half_hi(p01) * (BIAS_U8 + zv[1]) +
+                 half_lo(p23) * (BIAS_U8 + zv[2]) + half_hi(p23) * (BIAS_U8 + zv[3]);
+      const f16x4 pf = as_f16x4(p01, p23);
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) {
-      const float mw = s_m[ww][h];
-      const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - M);
-      L += s_l[ww][h] * f;
-      A += s_acc[(ww * G + h) * D + d] * f;
-    }
-    if (COLD_ZERO && cold_tokens > 0.f) {
-      // COLD tokens: logit 0, V = 0 (tierkv_triton.py:92-102 masked loads).
-      const float M2 = fmaxf(M, 0.f);
-      const float f = (M == -INFINITY) ? 0.f : exp2f(M - M2);
-      L = L * f + cold_tokens * exp2f(-M2);
-      A *= f;
-      M = M2;
-    }
-    if (p.direct_out) {
-      const float o = (L > 0.f) ? A / (L * PBOOST) : 0.f;
-      reinterpret_cast<QT*>(p.out)[(int64_t(b) * p.num_heads + kvh * G + h) * D + d] = from_f32<QT>(o);
+      for (int s = 0; s < DS; ++s)
+        ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(u8x4_plus1024(vt[s]), pf, ws.acc[s], 0, 0, 0);
     } else {
-      const int64_t pi = (int64_t(unit) * splits + split) * G + h;
-      p.ws_acc[pi * D + d] = A;
-      if (d == 0) {
-        p.ws_ml[pi * 2 + 0] = M;
-        p.ws_ml[pi * 2 + 1] = L;
+      // (u - zero) * scale per token in fp32, as the reference kernel does.
+      const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
+#pragma unroll
+      for (int s = 0; s < DS; ++s) {
+        const uint32_t w = vt[s];
+        const float a0 = (float(w & 0xffu) - zv[0]) * sv[0];
+        const float a1 = (float((w >> 8) & 0xffu) - zv[1]) * sv[1];
+        const float a2 = (float((w >> 16) & 0xffu) - zv[2]) * sv[2];
+        const float a3 = (float(w >> 24) - zv[3]) * sv[3];
+        ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(pack_f16x2(a0, a1), pack_f16x2(a2, a3)), pf,
+                                                          ws.acc[s], 0, 0, 0);
       }
     }
   }
 }
 
-// Merge of the splits (LSE combine, tierkv_triton.py:231-264) and the score
-// finalisation: score = l_b * 2^(m_b - M) / L for HOT/WARM blocks,
-// len * 2^(-M) / L for COLD blocks in zero-logit mode, 0 otherwise.
+// Final softmax normalisation of one (sequence, kv head): out[h][d] and, if
+// requested, the per-block probability sums.  M, L are the combined base-2
+// maximum and denominator of the resident tokens (the accumulator is in
+// PBOOST units, L is not); COLD
+// tokens of the zero-logit mode enter with logit 0 (tierkv_triton.py:92-102).
 template <typename QT, bool COLD_ZERO>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
-  __shared__ float s_M[64];
-  __shared__ float s_L[64];
-  const int unit = blockIdx.x;
-  const int b = unit / p.kv_heads;
-  const int kvh = unit % p.kv_heads;
-  const int G = p.groups;
-  const int D = p.head_dim;
-  const int splits = p.splits;
-  for (int h = threadIdx.x; h < G; h += blockDim.x) {
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, p.ws_ml[((int64_t(unit) * splits + s) * G + h) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const float* ml = p.ws_ml + ((int64_t(unit) * splits + s) * G + h) * 2;
-      L += (ml[0] == -INFINITY) ? 0.f : ml[1] * exp2f(ml[0] - M);
+__device__ __forceinline__ void finalize_unit(const DecodeParams& p, int b, int kvh, float cold_tokens,
+                                              const float* A_of, float* s_M, float* s_L, int G, int D,
+                                              int tid, int nthreads) {
+  // A_of(h, d) is read from LDS by the caller-provided buffer [G][D]; s_M/s_L
+  // hold the resident (M, L) per head and receive the final ones.
+  __syncthreads();
+  if (tid < G) {
+    float M = s_M[tid], L = s_L[tid];
+    if (COLD_ZERO && cold_tokens > 0.f) {
+      const float M2 = fmaxf(M, 0.f);
+      const float f = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - M2);
+      L = L * f + cold_tokens * __builtin_amdgcn_exp2f(-M2);
+      s_L[G + tid] = f;   // rescale of the resident accumulator
+      M = M2;
+    } else {
+      s_L[G + tid] = 1.f;
     }
-    s_M[h] = M;
-    s_L[h] = L;
+    s_M[tid] = M;
+    s_L[tid] = L;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < G * D; i += blockDim.x) {
+  for (int i = tid; i < G * D; i += nthreads) {
     const int h = i / D;
-    const int d = i - h * D;
-    const float M = s_M[h], L = s_L[h];
-    float A = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const int64_t pi = (int64_t(unit) * splits + s) * G + h;
-      const float ms = p.ws_ml[pi * 2];
-      if (ms != -INFINITY) A += p.ws_acc[pi * D + d] * exp2f(ms - M);
-    }
-    const float o = (L > 0.f) ? A / (L * PBOOST) : 0.f;
-    reinterpret_cast<QT*>(p.out)[(int64_t(b) * p.num_heads + kvh * G + h) * D + d] = from_f32<QT>(o);
+    const float L = s_L[h];
+    const float o = (L > 0.f) ? A_of[i] * s_L[G + h] / (L * PBOOST) : 0.f;
+    reinterpret_cast<QT*>(p.out)[(int64_t(b) * p.num_heads + kvh * G + h) * D + (i - h * D)] = from_f32<QT>(o);
   }
   if (p.score_sums) {
     const int nb = seq_blocks(p, b);
     const int stride = int(p.table_stride);
-    for (int i = threadIdx.x; i < G * stride; i += blockDim.x) {
+    for (int i = tid; i < G * stride; i += nthreads) {
       const int h = i / stride;
       const int blk = i - h * stride;
       const int qh = kvh * G + h;
@@ -474,16 +397,253 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(DecodeParams p) {
       if (blk < nb && L > 0.f) {
         const int64_t o = int64_t(b) * p.table_stride + blk;
         const int st = p.states[o];
+        const int len = min(max(p.lengths[o], 0), FBS);
         if (st == COLD) {
-          if (COLD_ZERO) sc = float(min(max(p.lengths[o], 0), p.block_size)) * exp2f(-M) / L;
-        } else if (st == HOT || st == WARM) {
-          const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
-          if (sp[0] != -INFINITY) sc = sp[1] * exp2f(sp[0] - M) / L;
+          if (COLD_ZERO) sc = float(len) * __builtin_amdgcn_exp2f(-M) / L;
+        } else if ((st == HOT || st == WARM) && len > 0) {
+          const int64_t slot = p.table[o];
+          const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
+          if (slot >= 0 && slot < cap) {
+            const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
+            sc = load_dev(sp + 1) * __builtin_amdgcn_exp2f(load_dev(sp) - M) / L;
+          }
         }
       }
       p.score_sums[(int64_t(b) * p.num_heads + qh) * p.table_stride + blk] = sc;
     }
   }
+}
+
+template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT>
+__global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodeParams p) {
+  constexpr int DS = D / 16;
+  extern __shared__ float s_dyn[];               // [nw][G][D] wave accumulators
+  __shared__ int4 s_list[MAX_LIST];              // (block, slot, len, state)
+  __shared__ int s_wcnt[MAX_WAVES];
+  __shared__ int s_cold;
+  __shared__ int s_last;
+  __shared__ float s_m[MAX_WAVES][16];
+  __shared__ float s_l[MAX_WAVES][16];
+  __shared__ float s_M[32];
+  __shared__ float s_L[32];
+
+  const int G = p.groups;
+  const int splits = p.splits;
+  const int split = blockIdx.x % splits;
+  const int unit = blockIdx.x / splits;
+  const int b = unit / p.kv_heads;
+  const int kvh = unit % p.kv_heads;
+  const int tid = threadIdx.x;
+  const int nthreads = blockDim.x;
+  const int nw = nthreads >> 6;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int nb = seq_blocks(p, b);
+
+  // ---- this workgroup's share of the resident blocks ------------------------
+  // Ranks count HOT blocks first, then WARM, in logical order; the workgroup
+  // keeps rank % splits == split at list position rank / splits.
+  if (tid == 0) s_cold = 0;
+  int total = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    const int want = pass == 0 ? HOT : WARM;
+    for (int c0 = 0; c0 < nb; c0 += nthreads) {
+      const int idx = c0 + tid;
+      bool res = false;
+      int4 ent = make_int4(idx, 0, 0, want);
+      if (idx < nb) {
+        const int64_t o = int64_t(b) * p.table_stride + idx;
+        const int st = p.states[o];
+        const int len = min(max(p.lengths[o], 0), FBS);
+        if (st == want) {
+          const int slot = p.table[o];
+          const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
+          const bool slot_ok = slot >= 0 && slot < cap;
+          if (!slot_ok && len > 0) atomicOr(p.ws_err, 1);
+          res = slot_ok && len > 0;
+          ent = make_int4(idx, slot, len, st);
+        } else if (pass == 0) {
+          if (st == COLD) {
+            if (COLD_ZERO && len > 0) atomicAdd(&s_cold, len);
+          } else if (st != WARM) {
+            atomicOr(p.ws_err, 2);
+          }
+        }
+      }
+      const uint64_t mask = __ballot(res);
+      if (lane == 0) s_wcnt[w] = __popcll(mask);
+      __syncthreads();
+      int before = total, chunk = 0;
+      for (int i = 0; i < nw; ++i) {
+        const int c = s_wcnt[i];
+        before += (i < w) ? c : 0;
+        chunk += c;
+      }
+      const int rank = before + __popcll(mask & ((1ull << lane) - 1ull));
+      if (res && rank % splits == split) s_list[rank / splits] = ent;
+      total += chunk;
+      __syncthreads();
+    }
+  }
+  const int nlist = (total > split) ? (total - split + splits - 1) / splits : 0;
+
+  // ---- query (fp16) and its per-head sum ------------------------------------
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const bool head_ok = n < G;
+  const int qh = kvh * G + (head_ok ? n : 0);
+  uint32_t qv[D / 8];
+  float qsum = 0.f;
+  {
+    const QT* qp = reinterpret_cast<const QT*>(p.q) + (int64_t(b) * p.num_heads + qh) * D + g * (D / 4);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) {
+      const uint4 x = reinterpret_cast<const uint4*>(qp)[i];
+      const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t h2;
+        if constexpr (std::is_same<QT, __half>::value) {
+          h2 = wd[k];
+        } else {
+          const float a = __uint_as_float(wd[k] << 16);
+          const float c = __uint_as_float(wd[k] & 0xffff0000u);
+          h2 = pack_f16x2(a, c);
+        }
+        h2 = head_ok ? h2 : 0u;
+        qv[4 * i + k] = h2;
+        qsum += half_lo(h2) + half_hi(h2);
+      }
+    }
+    qsum += shfl_xor_f(qsum, 16);
+    qsum += shfl_xor_f(qsum, 32);
+  }
+
+  // ---- per-wave tile loop (ping-pong prefetch) -------------------------------
+  WaveState<D> st;
+#pragma unroll
+  for (int s = 0; s < DS; ++s) st.acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m_run = -INFINITY;
+  st.l_part = 0.f;
+  st.corr = 0.f;
+
+  const int mine = (nlist > w) ? (nlist - w + nw - 1) / nw : 0;
+  if (mine > 0) {
+    Tile<D> t0, t1;
+    int4 e0 = s_list[w];
+    int e0s = uniform(e0.w), e0slot = uniform(e0.y);
+    load_tile<D, WF>(p, kvh, e0s, e0slot, lane, t0);
+    for (int i = 0; i < mine; i += 2) {
+      // Prefetch the next tile (the last one again when there is none, so that
+      // every iteration issues the same loads).
+      const int4 e1 = s_list[w + min(i + 1, mine - 1) * nw];
+      const int e1s = uniform(e1.w), e1slot = uniform(e1.y);
+      load_tile<D, WF>(p, kvh, e1s, e1slot, lane, t1);
+      process_tile<D, WF, SCORES>(p, t0, e0s, uniform(e0.x), uniform(e0.z), lane, head_ok, b, qh, qv, qsum, st);
+      if (i + 1 >= mine) break;
+      const int4 e2 = s_list[w + min(i + 2, mine - 1) * nw];
+      const int e2s = uniform(e2.w), e2slot = uniform(e2.y);
+      load_tile<D, WF>(p, kvh, e2s, e2slot, lane, t0);
+      process_tile<D, WF, SCORES>(p, t1, e1s, uniform(e1.x), uniform(e1.z), lane, head_ok, b, qh, qv, qsum, st);
+      e0 = e2;
+      e0s = e2s;
+    }
+  }
+
+  // ---- merge the waves in LDS ------------------------------------------------
+  float l = st.l_part + shfl_xor_f(st.l_part, 16);
+  l += shfl_xor_f(l, 32);
+  float corr = st.corr + shfl_xor_f(st.corr, 16);
+  corr += shfl_xor_f(corr, 32);
+  float* s_acc = s_dyn;   // [nw][G][D]
+  if (head_ok) {
+    if (g == 0) {
+      s_m[w][n] = st.m_run;
+      s_l[w][n] = l;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int s = 0; s < DS; ++s) s_acc[(w * G + n) * D + (4 * g + r) * DS + s] = st.acc[s][r] - corr;
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][tid]);
+    float L = 0.f;
+    for (int ww = 0; ww < nw; ++ww) {
+      const float mw = s_m[ww][tid];
+      L += (mw == -INFINITY) ? 0.f : s_l[ww][tid] * __builtin_amdgcn_exp2f(mw - M);
+    }
+    s_M[tid] = M;
+    s_L[tid] = L;
+  }
+  __syncthreads();
+  // Combined accumulator of this workgroup into wave 0's LDS slice.
+  for (int i = tid; i < G * D; i += nthreads) {
+    const int h = i / D;
+    const float M = s_M[h];
+    float A = 0.f;
+    for (int ww = 0; ww < nw; ++ww) {
+      const float mw = s_m[ww][h];
+      if (mw != -INFINITY) A += s_acc[ww * G * D + i] * __builtin_amdgcn_exp2f(mw - M);
+    }
+    if (splits == 1) {
+      s_acc[i] = A;   // row i of wave 0 is read only by this thread
+    } else {
+      const int64_t pi = (int64_t(unit) * splits + split) * G + h;
+      store_dev(p.ws_acc + pi * D + (i - h * D), A);
+    }
+  }
+  const float cold_tokens = COLD_ZERO ? float(s_cold) : 0.f;
+  if (splits == 1) {
+    if (SCORES) __builtin_amdgcn_s_waitcnt(0);   // per-block statistics stored
+    finalize_unit<QT, COLD_ZERO>(p, b, kvh, cold_tokens, s_acc, s_M, s_L, G, D, tid, nthreads);
+    return;
+  }
+
+  // ---- splits: publish the partial, the last workgroup merges -----------------
+  if (tid < G) {
+    const int64_t pi = (int64_t(unit) * splits + split) * G + tid;
+    store_dev(p.ws_ml + pi * 2 + 0, s_M[tid]);
+    store_dev(p.ws_ml + pi * 2 + 1, s_L[tid]);
+  }
+  // Every wave's device-coherent stores complete before the arrival is counted.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(p.ws_cnt + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (prev == splits - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int s = 0; s < splits; ++s) M = fmaxf(M, load_dev(p.ws_ml + ((int64_t(unit) * splits + s) * G + tid) * 2));
+    float L = 0.f;
+    for (int s = 0; s < splits; ++s) {
+      const float* ml = p.ws_ml + ((int64_t(unit) * splits + s) * G + tid) * 2;
+      const float ms = load_dev(ml);
+      const float ls = load_dev(ml + 1);
+      L += (ms == -INFINITY) ? 0.f : ls * __builtin_amdgcn_exp2f(ms - M);
+    }
+    s_M[tid] = M;
+    s_L[tid] = L;
+  }
+  __syncthreads();
+  for (int i = tid; i < G * D; i += nthreads) {
+    const int h = i / D;
+    const float M = s_M[h];
+    float A = 0.f;
+    for (int s = 0; s < splits; ++s) {
+      const int64_t pi = (int64_t(unit) * splits + s) * G + h;
+      const float ms = load_dev(p.ws_ml + pi * 2);
+      if (ms != -INFINITY) A += load_dev(p.ws_acc + pi * D + (i - h * D)) * __builtin_amdgcn_exp2f(ms - M);
+    }
+    s_acc[i] = A;
+  }
+  if (tid == 0) __hip_atomic_store(p.ws_cnt + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  finalize_unit<QT, COLD_ZERO>(p, b, kvh, cold_tokens, s_acc, s_M, s_L, G, D, tid, nthreads);
 }
 
 // --------------------------------------------------------------------------
@@ -626,40 +786,42 @@ __global__ __launch_bounds__(64) void decode_generic_kernel(DecodeParams p) {
     }
   }
 }
-
 // --------------------------------------------------------------------------
 // Host side
 // --------------------------------------------------------------------------
 
-struct SplitPlan {
+struct Plan {
+  int nw;
   int splits;
-  int blocks_per_split;
 };
-
-static SplitPlan plan_splits(int batch, int kv_heads, int num_blocks, int splits_hint) {
-  const int units = std::max(1, batch * kv_heads);
-  int splits;
-  if (splits_hint > 0) {
-    splits = splits_hint;
-  } else {
-    // Aim for about 4 workgroups per CU on 256 CUs.
-    const int target = 1024;
-    splits = std::max(1, (target + units - 1) / units);
-    // Keep at least 8 logical blocks per split.
-    splits = std::min(splits, std::max(1, num_blocks / 8));
-  }
-  int bps = (num_blocks + splits - 1) / splits;
-  bps = std::max(1, std::min(bps, MAX_CHUNK));
-  splits = (num_blocks + bps - 1) / bps;
-  return {std::max(1, splits), bps};
-}
 
 static bool fast_path_ok(int block_size, int head_dim, int groups) {
   return block_size == FBS && (head_dim == 64 || head_dim == 128) && groups >= 1 && groups <= 16;
 }
 
+// Eight waves per workgroup (four for GQA groups above 8, to bound the LDS
+// accumulators); enough splits to put about 2048 waves (two per SIMD) on the
+// chip, at least 2*nw list entries per split, and at most MAX_LIST.
+static Plan plan_launch(int batch, int kv_heads, int num_blocks, int groups, int splits_hint) {
+  Plan pl;
+  pl.nw = groups <= 8 ? 8 : 4;
+  const int64_t units = std::max<int64_t>(1, int64_t(batch) * kv_heads);
+  int splits;
+  if (splits_hint > 0) {
+    splits = splits_hint;
+  } else {
+    const int64_t target_waves = 2048;
+    splits = int(std::max<int64_t>(1, (target_waves + units * pl.nw - 1) / (units * pl.nw)));
+    splits = std::min(splits, std::max(1, num_blocks / (2 * pl.nw)));
+  }
+  splits = std::max(splits, (num_blocks + MAX_LIST - 1) / MAX_LIST);
+  splits = std::min(splits, std::max(1, num_blocks));
+  pl.splits = std::max(1, splits);
+  return pl;
+}
+
 struct WsLayout {
-  int64_t err, acc, ml, stage, total;
+  int64_t err, cnt, acc, ml, stage, total;
 };
 
 static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks, int block_size,
@@ -670,53 +832,49 @@ static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks
   l.err = 0;
   int64_t off = 256;
   if (fast_path_ok(block_size, head_dim, groups)) {
-    const SplitPlan sp = plan_splits(batch, kv_heads, num_blocks, splits_hint);
+    const Plan pl = plan_launch(batch, kv_heads, num_blocks, groups, splits_hint);
     const int64_t units = int64_t(batch) * kv_heads;
+    l.cnt = off;
+    off = up(off + units * 4);
     l.acc = off;
-    off = up(off + units * sp.splits * groups * head_dim * 4);
+    if (pl.splits > 1) off = up(off + units * pl.splits * groups * head_dim * 4);
     l.ml = off;
-    off = up(off + units * sp.splits * groups * 2 * 4);
+    if (pl.splits > 1) off = up(off + units * pl.splits * groups * 2 * 4);
     l.stage = off;
     if (scores) off = up(off + int64_t(batch) * num_heads * num_blocks * 2 * 4);
   } else {
-    l.acc = l.ml = l.stage = off;
+    l.cnt = l.acc = l.ml = l.stage = off;
   }
   l.total = off;
   return l;
 }
 
 template <int D, int WF, bool SC, bool CZ, typename QT>
-static void launch_fast(const DecodeParams& p, int grid, hipStream_t stream) {
-  const size_t shmem = size_t(NW) * p.groups * D * sizeof(float);
-  hipLaunchKernelGGL((decode_split_kernel<D, WF, SC, CZ, QT>), dim3(grid), dim3(NW * 64), shmem, stream, p);
+static void launch_fast(const DecodeParams& p, int nw, int grid, hipStream_t stream) {
+  const size_t shmem = size_t(nw) * p.groups * D * sizeof(float);
+  hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT>), dim3(grid), dim3(nw * 64), shmem, stream, p);
 }
 
 template <int D, int WF, typename QT>
-static void dispatch_sc_cz(const DecodeParams& p, bool sc, bool cz, int grid, hipStream_t stream) {
+static void dispatch_sc_cz(const DecodeParams& p, bool sc, bool cz, int nw, int grid, hipStream_t stream) {
   if (sc) {
-    if (cz) launch_fast<D, WF, true, true, QT>(p, grid, stream);
-    else launch_fast<D, WF, true, false, QT>(p, grid, stream);
+    if (cz) launch_fast<D, WF, true, true, QT>(p, nw, grid, stream);
+    else launch_fast<D, WF, true, false, QT>(p, nw, grid, stream);
   } else {
-    if (cz) launch_fast<D, WF, false, true, QT>(p, grid, stream);
-    else launch_fast<D, WF, false, false, QT>(p, grid, stream);
+    if (cz) launch_fast<D, WF, false, true, QT>(p, nw, grid, stream);
+    else launch_fast<D, WF, false, false, QT>(p, nw, grid, stream);
   }
 }
 
 template <typename QT>
-static void dispatch_fast(const DecodeParams& p, int wf, bool sc, bool cz, int grid, hipStream_t stream) {
+static void dispatch_fast(const DecodeParams& p, int wf, bool sc, bool cz, int nw, int grid, hipStream_t stream) {
   if (p.head_dim == 128) {
-    if (wf == TIERKV_WARM_ABSMAX_I8) dispatch_sc_cz<128, TIERKV_WARM_ABSMAX_I8, QT>(p, sc, cz, grid, stream);
-    else dispatch_sc_cz<128, TIERKV_WARM_REF_U8, QT>(p, sc, cz, grid, stream);
+    if (wf == TIERKV_WARM_ABSMAX_I8) dispatch_sc_cz<128, TIERKV_WARM_ABSMAX_I8, QT>(p, sc, cz, nw, grid, stream);
+    else dispatch_sc_cz<128, TIERKV_WARM_REF_U8, QT>(p, sc, cz, nw, grid, stream);
   } else {
-    if (wf == TIERKV_WARM_ABSMAX_I8) dispatch_sc_cz<64, TIERKV_WARM_ABSMAX_I8, QT>(p, sc, cz, grid, stream);
-    else dispatch_sc_cz<64, TIERKV_WARM_REF_U8, QT>(p, sc, cz, grid, stream);
+    if (wf == TIERKV_WARM_ABSMAX_I8) dispatch_sc_cz<64, TIERKV_WARM_ABSMAX_I8, QT>(p, sc, cz, nw, grid, stream);
+    else dispatch_sc_cz<64, TIERKV_WARM_REF_U8, QT>(p, sc, cz, nw, grid, stream);
   }
-}
-
-template <typename QT>
-static void launch_merge(const DecodeParams& p, bool cz, int units, hipStream_t stream) {
-  if (cz) hipLaunchKernelGGL((decode_merge_kernel<QT, true>), dim3(units), dim3(256), 0, stream, p);
-  else hipLaunchKernelGGL((decode_merge_kernel<QT, false>), dim3(units), dim3(256), 0, stream, p);
 }
 
 template <typename QT>
@@ -775,6 +933,8 @@ extern "C" int32_t tierkv_decode_attention(
     return fail(TIERKV_ERR_INVALID, "WARM pools and scales are required (pass 1-slot placeholders when empty)");
   if (warm_format == TIERKV_WARM_REF_U8 && (!k_zero || !v_zero))
     return fail(TIERKV_ERR_INVALID, "reference-format WARM pools need zero points");
+  if (int64_t(batch) * num_kv_heads > (int64_t(1) << 24))
+    return fail(TIERKV_ERR_UNSUPPORTED, "batch * kv_heads too large");
   const bool scores = score_sums != nullptr;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, num_blocks, block_size, head_dim, scores, splits_hint);
   if (workspace_bytes < wl.total) return fail(TIERKV_ERR_WORKSPACE, "workspace too small");
@@ -808,6 +968,7 @@ extern "C" int32_t tierkv_decode_attention(
   p.scale_log2 = scaling * LOG2E;
   char* ws = reinterpret_cast<char*>(workspace);
   p.ws_err = reinterpret_cast<int32_t*>(ws + wl.err);
+  p.ws_cnt = reinterpret_cast<int32_t*>(ws + wl.cnt);
   p.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
   p.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   p.ws_stage = reinterpret_cast<float*>(ws + wl.stage);
@@ -816,28 +977,23 @@ extern "C" int32_t tierkv_decode_attention(
   const bool bf16 = query_dtype == TIERKV_DTYPE_BF16;
 
   if (fast_path_ok(block_size, head_dim, p.groups)) {
-    const bool aligned = aligned16(hot_k) && aligned16(hot_v) && aligned16(warm_k) && aligned16(warm_v);
-    if (!aligned) return fail(TIERKV_ERR_INVALID, "pool base pointers must be 16-byte aligned");
-    const SplitPlan sp = plan_splits(batch, num_kv_heads, num_blocks, splits_hint);
-    p.splits = sp.splits;
-    p.blocks_per_split = sp.blocks_per_split;
-    p.direct_out = (sp.splits == 1 && !scores) ? 1 : 0;
-    const int units = batch * num_kv_heads;
-    const int grid = units * sp.splits;
-    if (bf16) dispatch_fast<__hip_bfloat16>(p, warm_format, scores, cz, grid, stream);
-    else dispatch_fast<__half>(p, warm_format, scores, cz, grid, stream);
-    int32_t rc = check_launch("decode_split_kernel");
-    if (rc) return rc;
-    if (!p.direct_out) {
-      if (bf16) launch_merge<__hip_bfloat16>(p, cz, units, stream);
-      else launch_merge<__half>(p, cz, units, stream);
-      rc = check_launch("decode_merge_kernel");
-      if (rc) return rc;
+    const bool aligned = aligned16(hot_k) && aligned16(hot_v) && aligned16(warm_k) && aligned16(warm_v) &&
+                         aligned16(query);
+    if (!aligned) return fail(TIERKV_ERR_INVALID, "query and pool base pointers must be 16-byte aligned");
+    if (warm_format == TIERKV_WARM_REF_U8) {
+      const uintptr_t m = reinterpret_cast<uintptr_t>(k_scale) | reinterpret_cast<uintptr_t>(k_zero) |
+                          reinterpret_cast<uintptr_t>(v_scale) | reinterpret_cast<uintptr_t>(v_zero);
+      if (m & 7u) return fail(TIERKV_ERR_INVALID, "reference-format scale/zero pools must be 8-byte aligned");
     }
-    return TIERKV_OK;
+    const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, p.groups, splits_hint);
+    p.splits = pl.splits;
+    const int64_t grid = int64_t(batch) * num_kv_heads * pl.splits;
+    if (grid > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
+    if (bf16) dispatch_fast<__hip_bfloat16>(p, warm_format, scores, cz, pl.nw, int(grid), stream);
+    else dispatch_fast<__half>(p, warm_format, scores, cz, pl.nw, int(grid), stream);
+    return check_launch("tiered_decode_kernel");
   }
   p.splits = 1;
-  p.blocks_per_split = num_blocks;
   if (bf16) launch_generic<__hip_bfloat16>(p, warm_format, cz, stream);
   else launch_generic<__half>(p, warm_format, cz, stream);
   return check_launch("decode_generic_kernel");

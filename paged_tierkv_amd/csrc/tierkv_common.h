@@ -55,21 +55,36 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Four int8 codes packed in a dword -> four exact fp16 values.  The biased
-// byte u = c ^ 0x80 = c + 128 is placed under the fp16 exponent of 1024
-// (0x6400 | u == 1024 + u exactly), then 1152 is subtracted: exact for every
-// code in [-128, 127].
-__device__ __forceinline__ void i8x4_to_f16x4(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  const uint32_t u = w ^ 0x80808080u;
-  lo = (u & 0xffu) | ((u & 0xff00u) << 8) | 0x64006400u;
-  hi = ((u >> 16) & 0xffu) | ((u >> 8) & 0xff0000u) | 0x64006400u;
-  const __half2 bias = __halves2half2(__float2half(1152.f), __float2half(1152.f));
-  __half2 l2 = *reinterpret_cast<__half2*>(&lo);
-  __half2 h2 = *reinterpret_cast<__half2*>(&hi);
-  l2 = __hsub2(l2, bias);
-  h2 = __hsub2(h2, bias);
-  lo = *reinterpret_cast<uint32_t*>(&l2);
-  hi = *reinterpret_cast<uint32_t*>(&h2);
+__device__ __forceinline__ f16x4 as_f16x4(uint32_t lo, uint32_t hi);
+
+// v_perm_b32: byte i of the result is byte sel_i of the 8-byte value
+// {hi (bytes 4-7), lo (bytes 0-3)}.
+__device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Four unsigned bytes u -> four exact fp16 values 1024 + u: each byte is
+// placed under the fp16 exponent byte 0x64 (0x6400 | u == 1024 + u).
+__device__ __forceinline__ f16x4 u8x4_plus1024(uint32_t w) {
+  return as_f16x4(perm_b32(0x64646464u, w, 0x04010400u), perm_b32(0x64646464u, w, 0x04030402u));
+}
+
+// Four int8 codes c -> four exact fp16 values 1152 + c (c + 128 == c ^ 0x80).
+__device__ __forceinline__ f16x4 i8x4_plus1152(uint32_t w) {
+  return u8x4_plus1024(w ^ 0x80808080u);
+}
+
+// 4x4 byte transpose: out[s] = {r0.byte s, r1.byte s, r2.byte s, r3.byte s}.
+__device__ __forceinline__ void transpose_bytes4x4(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
+                                                   uint32_t* out) {
+  const uint32_t t01l = perm_b32(r1, r0, 0x05010400u);   // r0.b0 r1.b0 r0.b1 r1.b1
+  const uint32_t t01h = perm_b32(r1, r0, 0x07030602u);   // r0.b2 r1.b2 r0.b3 r1.b3
+  const uint32_t t23l = perm_b32(r3, r2, 0x05010400u);
+  const uint32_t t23h = perm_b32(r3, r2, 0x07030602u);
+  out[0] = perm_b32(t23l, t01l, 0x05040100u);
+  out[1] = perm_b32(t23l, t01l, 0x07060302u);
+  out[2] = perm_b32(t23h, t01h, 0x05040100u);
+  out[3] = perm_b32(t23h, t01h, 0x07060302u);
 }
 
 __device__ __forceinline__ f16x4 as_f16x4(uint32_t lo, uint32_t hi) {
