@@ -104,78 +104,88 @@ __device__ __forceinline__ float load_dev(const float* p) {
 // Fast path
 // --------------------------------------------------------------------------
 
-// One tile in registers.  Lane (n = lane & 15, g = lane >> 4):
-//   k: token n, dims g*D/4 .. +D/4 (HOT: D/8 dwords of halves; WARM: D/16
-//      dwords of codes);
-//   v: tokens 4g + j (j = 0..3), dims n*D/16 .. +D/16, row j at v[j*D/32]
-//      (HOT: D/32 dwords of halves; WARM: D/64 dwords of codes);
-//   m: WARM metadata (absmax: s_k, s_v; reference format: fp16 pairs of the
-//      per-token k scale, k zero, v scale, v zero of tokens 4g .. 4g+3).
+// Tiles in registers.  Lane (n = lane & 15, g = lane >> 4) holds
+//   k: token n, dims g*D/4 .. +D/4;
+//   v: tokens 4g + j (j = 0..3), dims n*D/16 .. +D/16 (row j at v[j*RW]);
+// HOT tiles as fp16 pairs, WARM tiles as 8-bit codes plus metadata
+// (absmax: s_k, s_v; reference format: fp16 pairs of the per-token k scale,
+// k zero, v scale and v zero of tokens 4g .. 4g+3).  The two tiers have their
+// own registers: each tile loop is straight-line code for one tier.
 template <int D>
-struct Tile {
+struct HotTile {
+  static constexpr int RW = D / 32;   // dwords per V row
   uint32_t k[D / 8];
   uint32_t v[D / 8];
-  uint32_t m[8];
 };
 
 template <int D, int WF>
-__device__ __forceinline__ void load_tile(const DecodeParams& p, int kvh, int state, int slot, int lane,
-                                          Tile<D>& t) {
+struct WarmTile {
+  static constexpr int RW = D / 64;
+  static constexpr int NM = (WF == TIERKV_WARM_ABSMAX_I8) ? 2 : 8;
+  uint32_t k[D / 16];
+  uint32_t v[D / 16];
+  uint32_t m[NM];
+};
+
+template <int D>
+__device__ __forceinline__ void load_hot(const DecodeParams& p, int kvh, int slot, int lane, HotTile<D>& t) {
   const int n = lane & 15;
   const int g = lane >> 4;
   const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;   // first token row of the tile
-  if (state == HOT) {
-    const uint4* kp = reinterpret_cast<const uint4*>(p.hot_k + tile0 * D) + n * (D / 8) + g * (D / 32);
+  const uint4* kp = reinterpret_cast<const uint4*>(p.hot_k + tile0 * D) + n * (D / 8) + g * (D / 32);
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) {
-      const uint4 x = kp[i];
-      t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
-    }
+  for (int i = 0; i < D / 32; ++i) {
+    const uint4 x = kp[i];
+    t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const __half* vp = p.hot_v + (tile0 + 4 * g + j) * D + n * (D / 16);
-      if constexpr (D == 128) {
-        const uint4 x = *reinterpret_cast<const uint4*>(vp);
-        t.v[4 * j + 0] = x.x; t.v[4 * j + 1] = x.y; t.v[4 * j + 2] = x.z; t.v[4 * j + 3] = x.w;
-      } else {
-        const uint2 x = *reinterpret_cast<const uint2*>(vp);
-        t.v[2 * j + 0] = x.x; t.v[2 * j + 1] = x.y;
-      }
-    }
-  } else {
-    const uint8_t* wk = reinterpret_cast<const uint8_t*>(p.warm_k) + tile0 * D;
-    const uint8_t* wv = reinterpret_cast<const uint8_t*>(p.warm_v) + tile0 * D;
-    const uint4* kp = reinterpret_cast<const uint4*>(wk + n * D + g * (D / 4));
-#pragma unroll
-    for (int i = 0; i < D / 64; ++i) {
-      const uint4 x = kp[i];
-      t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint8_t* vp = wv + (4 * g + j) * D + n * (D / 16);
-      // Same row stride as the HOT layout (D/32 dwords), first D/64 used:
-      // both tiers then write the same registers at the same indices.
-      if constexpr (D == 128) {
-        const uint2 x = *reinterpret_cast<const uint2*>(vp);
-        t.v[4 * j + 0] = x.x; t.v[4 * j + 1] = x.y;
-      } else {
-        t.v[2 * j] = *reinterpret_cast<const uint32_t*>(vp);
-      }
-    }
-    if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-      const int64_t si = int64_t(slot) * p.kv_heads + kvh;
-      t.m[0] = __float_as_uint(reinterpret_cast<const float*>(p.k_scale)[si]);
-      t.m[1] = __float_as_uint(reinterpret_cast<const float*>(p.v_scale)[si]);
+  for (int j = 0; j < 4; ++j) {
+    const __half* vp = p.hot_v + (tile0 + 4 * g + j) * D + n * (D / 16);
+    if constexpr (D == 128) {
+      const uint4 x = *reinterpret_cast<const uint4*>(vp);
+      t.v[4 * j + 0] = x.x; t.v[4 * j + 1] = x.y; t.v[4 * j + 2] = x.z; t.v[4 * j + 3] = x.w;
     } else {
-      const int64_t mi = tile0 + 4 * g;   // halves; 8-byte aligned
-      const uint2 ks = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_scale) + mi);
-      const uint2 kz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_zero) + mi);
-      const uint2 vs = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_scale) + mi);
-      const uint2 vz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_zero) + mi);
-      t.m[0] = ks.x; t.m[1] = ks.y; t.m[2] = kz.x; t.m[3] = kz.y;
-      t.m[4] = vs.x; t.m[5] = vs.y; t.m[6] = vz.x; t.m[7] = vz.y;
+      const uint2 x = *reinterpret_cast<const uint2*>(vp);
+      t.v[2 * j + 0] = x.x; t.v[2 * j + 1] = x.y;
     }
+  }
+}
+
+template <int D, int WF>
+__device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int slot, int lane, WarmTile<D, WF>& t) {
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;
+  const uint8_t* wk = reinterpret_cast<const uint8_t*>(p.warm_k) + tile0 * D;
+  const uint8_t* wv = reinterpret_cast<const uint8_t*>(p.warm_v) + tile0 * D;
+  const uint4* kp = reinterpret_cast<const uint4*>(wk + n * D + g * (D / 4));
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    const uint4 x = kp[i];
+    t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint8_t* vp = wv + (4 * g + j) * D + n * (D / 16);
+    if constexpr (D == 128) {
+      const uint2 x = *reinterpret_cast<const uint2*>(vp);
+      t.v[2 * j + 0] = x.x; t.v[2 * j + 1] = x.y;
+    } else {
+      t.v[j] = *reinterpret_cast<const uint32_t*>(vp);
+    }
+  }
+  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
+    const int64_t si = int64_t(slot) * p.kv_heads + kvh;
+    t.m[0] = __float_as_uint(reinterpret_cast<const float*>(p.k_scale)[si]);
+    t.m[1] = __float_as_uint(reinterpret_cast<const float*>(p.v_scale)[si]);
+  } else {
+    const int64_t mi = tile0 + 4 * g;   // halves; 8-byte aligned
+    const uint2 ks = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_scale) + mi);
+    const uint2 kz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_zero) + mi);
+    const uint2 vs = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_scale) + mi);
+    const uint2 vz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_zero) + mi);
+    t.m[0] = ks.x; t.m[1] = ks.y; t.m[2] = kz.x; t.m[3] = kz.y;
+    t.m[4] = vs.x; t.m[5] = vs.y; t.m[6] = vz.x; t.m[7] = vz.y;
   }
 }
 
@@ -195,53 +205,14 @@ struct WaveState {
   float corr;
 };
 
-template <int D, int WF, bool SCORES>
-__device__ __forceinline__ void process_tile(const DecodeParams& p, const Tile<D>& t, int state, int blk, int len,
-                                             int lane, bool head_ok, int b, int qh, const uint32_t* qv,
-                                             float qsum, WaveState<D>& ws) {
+// Lazy online-softmax update for the four logits x[] of this lane; returns
+// p[r] = 2^(x[r] - m_run).  The running maximum is re-based (and the state
+// rescaled) only when a logit exceeds it by more than LAZY_T.
+template <int D, bool SCORES>
+__device__ __forceinline__ void softmax_step(const DecodeParams& p, const float* x, float* pr, int lane,
+                                             bool head_ok, int b, int qh, int blk, WaveState<D>& ws) {
   constexpr int DS = D / 16;
   const int g = lane >> 4;
-
-  // ---- S^T = K Q^T ------------------------------------------------------
-  f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (state == HOT) {
-#pragma unroll
-    for (int s = 0; s < DS; ++s)
-      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(t.k[2 * s], t.k[2 * s + 1]),
-                                                   as_f16x4(qv[2 * s], qv[2 * s + 1]), sacc, 0, 0, 0);
-  } else {
-#pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      const f16x4 a = (WF == TIERKV_WARM_ABSMAX_I8) ? i8x4_plus1152(t.k[s]) : u8x4_plus1024(t.k[s]);
-      sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, as_f16x4(qv[2 * s], qv[2 * s + 1]), sacc, 0, 0, 0);
-    }
-  }
-
-  // ---- logits (base 2) for tokens 4g + r ----------------------------------
-  float x[4];
-  if (state == HOT) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = sacc[r] * p.scale_log2;
-  } else if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-    const float c1 = p.scale_log2 * __uint_as_float(t.m[0]);
-    const float c0 = -BIAS_I8 * qsum * c1;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = fmaf(sacc[r], c1, c0);
-  } else {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float c1 = p.scale_log2 * half_of(&t.m[0], r);
-      const float c0 = -(BIAS_U8 + half_of(&t.m[2], r)) * qsum * c1;
-      x[r] = fmaf(sacc[r], c1, c0);
-    }
-  }
-  if (len < FBS) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (4 * g + r >= len) x[r] = -INFINITY;
-  }
-
-  // ---- lazy online softmax ---------------------------------------------------
   const float lm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
   if (__any(head_ok && lm > ws.m_run + LAZY_T)) {
     float tm = fmaxf(lm, shfl_xor_f(lm, 16));
@@ -254,7 +225,6 @@ __device__ __forceinline__ void process_tile(const DecodeParams& p, const Tile<D
     ws.corr *= alpha;
     ws.m_run = m_new;
   }
-  float pr[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(x[r] - ws.m_run);
   const float psum = (pr[0] + pr[1]) + (pr[2] + pr[3]);
@@ -268,28 +238,80 @@ __device__ __forceinline__ void process_tile(const DecodeParams& p, const Tile<D
       store_dev(sp + 1, ls);
     }
   }
+}
 
-  // ---- O^T += V^T P^T ----------------------------------------------------------
-  if (state == HOT) {
-    const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
+__device__ __forceinline__ void mask_tail(float* x, int g, int len) {
+  if (len < FBS) {
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      constexpr int RW = D / 32;   // dwords per V row
-      const int dw = s >> 1;
-      const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
-      const f16x4 av = as_f16x4(perm_b32(t.v[1 * RW + dw], t.v[0 * RW + dw], sel),
-                                perm_b32(t.v[3 * RW + dw], t.v[2 * RW + dw], sel));
-      ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pf, ws.acc[s], 0, 0, 0);
-    }
-    return;
+    for (int r = 0; r < 4; ++r)
+      if (4 * g + r >= len) x[r] = -INFINITY;
   }
-  // WARM: transpose the four rows' codes so that vt[s] holds the four tokens
-  // of dim n*DS + s.
-  constexpr int RS = D / 32;   // row stride in t.v
+}
+
+template <int D, bool SCORES>
+__device__ __forceinline__ void process_hot(const DecodeParams& p, const HotTile<D>& t, int blk, int len, int lane,
+                                            bool head_ok, int b, int qh, const uint32_t* qv, WaveState<D>& ws) {
+  constexpr int DS = D / 16;
+  constexpr int RW = HotTile<D>::RW;
+  // S^T = K Q^T
+  f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < DS; ++s)
+    sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(t.k[2 * s], t.k[2 * s + 1]),
+                                                 as_f16x4(qv[2 * s], qv[2 * s + 1]), sacc, 0, 0, 0);
+  float x[4], pr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) x[r] = sacc[r] * p.scale_log2;
+  mask_tail(x, lane >> 4, len);
+  softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, blk, ws);
+  // O^T += V^T P^T; the A operand of step s is {V[4g + j][n*DS + s]}_j.
+  const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
+#pragma unroll
+  for (int s = 0; s < DS; ++s) {
+    const int dw = s >> 1;
+    const uint32_t sel = (s & 1) ? 0x07060302u : 0x05040100u;
+    const f16x4 av = as_f16x4(perm_b32(t.v[1 * RW + dw], t.v[0 * RW + dw], sel),
+                              perm_b32(t.v[3 * RW + dw], t.v[2 * RW + dw], sel));
+    ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, pf, ws.acc[s], 0, 0, 0);
+  }
+}
+
+template <int D, int WF, bool SCORES>
+__device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTile<D, WF>& t, int blk, int len,
+                                             int lane, bool head_ok, int b, int qh, const uint32_t* qv, float qsum,
+                                             WaveState<D>& ws) {
+  constexpr int DS = D / 16;
+  constexpr int RW = WarmTile<D, WF>::RW;
+  // S^T = (K + offset) Q^T with the codes as exact fp16 integers.
+  f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < DS; ++s) {
+    const f16x4 a = (WF == TIERKV_WARM_ABSMAX_I8) ? i8x4_plus1152(t.k[s]) : u8x4_plus1024(t.k[s]);
+    sacc = __builtin_amdgcn_mfma_f32_16x16x16f16(a, as_f16x4(qv[2 * s], qv[2 * s + 1]), sacc, 0, 0, 0);
+  }
+  float x[4], pr[4];
+  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
+    const float c1 = p.scale_log2 * __uint_as_float(t.m[0]);
+    const float c0 = -BIAS_I8 * qsum * c1;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = fmaf(sacc[r], c1, c0);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float c1 = p.scale_log2 * half_of(&t.m[0], r);
+      const float c0 = -(BIAS_U8 + half_of(&t.m[2], r)) * qsum * c1;
+      x[r] = fmaf(sacc[r], c1, c0);
+    }
+  }
+  mask_tail(x, lane >> 4, len);
+  softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, blk, ws);
+
+  // O^T += V^T P^T: transpose the four rows' codes so that vt[s] holds the
+  // four tokens of dim n*DS + s.
   uint32_t vt[DS];
 #pragma unroll
-  for (int w4 = 0; w4 < D / 64; ++w4)
-    transpose_bytes4x4(t.v[0 * RS + w4], t.v[1 * RS + w4], t.v[2 * RS + w4], t.v[3 * RS + w4], &vt[4 * w4]);
+  for (int w4 = 0; w4 < RW; ++w4)
+    transpose_bytes4x4(t.v[0 * RW + w4], t.v[1 * RW + w4], t.v[2 * RW + w4], t.v[3 * RW + w4], &vt[4 * w4]);
   if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
     const float sv = __uint_as_float(t.m[1]);
     if (sv <= FOLD_MAX) {
@@ -352,66 +374,39 @@ __device__ __forceinline__ void process_tile(const DecodeParams& p, const Tile<D
   }
 }
 
-// Final softmax normalisation of one (sequence, kv head): out[h][d] and, if
-// requested, the per-block probability sums.  M, L are the combined base-2
-// maximum and denominator of the resident tokens (the accumulator is in
-// PBOOST units, L is not); COLD
-// tokens of the zero-logit mode enter with logit 0 (tierkv_triton.py:92-102).
-template <typename QT, bool COLD_ZERO>
-__device__ __forceinline__ void finalize_unit(const DecodeParams& p, int b, int kvh, float cold_tokens,
-                                              const float* A_of, float* s_M, float* s_L, int G, int D,
-                                              int tid, int nthreads) {
-  // A_of(h, d) is read from LDS by the caller-provided buffer [G][D]; s_M/s_L
-  // hold the resident (M, L) per head and receive the final ones.
-  __syncthreads();
-  if (tid < G) {
-    float M = s_M[tid], L = s_L[tid];
-    if (COLD_ZERO && cold_tokens > 0.f) {
-      const float M2 = fmaxf(M, 0.f);
-      const float f = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - M2);
-      L = L * f + cold_tokens * __builtin_amdgcn_exp2f(-M2);
-      s_L[G + tid] = f;   // rescale of the resident accumulator
-      M = M2;
-    } else {
-      s_L[G + tid] = 1.f;
-    }
-    s_M[tid] = M;
-    s_L[tid] = L;
+// Final softmax quantities of one head from the combined base-2 maximum M
+// and denominator L of the resident tokens (the accumulator is in PBOOST
+// units, L is not).  COLD tokens of the zero-logit mode enter with logit 0
+// (tierkv_triton.py:92-102); f rescales the resident accumulator.
+template <bool COLD_ZERO>
+__device__ __forceinline__ void cold_adjust(float& M, float& L, float& f, float cold_tokens) {
+  f = 1.f;
+  if (COLD_ZERO && cold_tokens > 0.f) {
+    const float M2 = fmaxf(M, 0.f);
+    f = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - M2);
+    L = L * f + cold_tokens * __builtin_amdgcn_exp2f(-M2);
+    M = M2;
   }
-  __syncthreads();
-  for (int i = tid; i < G * D; i += nthreads) {
-    const int h = i / D;
-    const float L = s_L[h];
-    const float o = (L > 0.f) ? A_of[i] * s_L[G + h] / (L * PBOOST) : 0.f;
-    reinterpret_cast<QT*>(p.out)[(int64_t(b) * p.num_heads + kvh * G + h) * D + (i - h * D)] = from_f32<QT>(o);
-  }
-  if (p.score_sums) {
-    const int nb = seq_blocks(p, b);
-    const int stride = int(p.table_stride);
-    for (int i = tid; i < G * stride; i += nthreads) {
-      const int h = i / stride;
-      const int blk = i - h * stride;
-      const int qh = kvh * G + h;
-      float sc = 0.f;
-      const float M = s_M[h], L = s_L[h];
-      if (blk < nb && L > 0.f) {
-        const int64_t o = int64_t(b) * p.table_stride + blk;
-        const int st = p.states[o];
-        const int len = min(max(p.lengths[o], 0), FBS);
-        if (st == COLD) {
-          if (COLD_ZERO) sc = float(len) * __builtin_amdgcn_exp2f(-M) / L;
-        } else if ((st == HOT || st == WARM) && len > 0) {
-          const int64_t slot = p.table[o];
-          const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-          if (slot >= 0 && slot < cap) {
-            const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
-            sc = load_dev(sp + 1) * __builtin_amdgcn_exp2f(load_dev(sp) - M) / L;
-          }
-        }
-      }
-      p.score_sums[(int64_t(b) * p.num_heads + qh) * p.table_stride + blk] = sc;
+}
+
+// Per-block probability sum of (head qh, block blk) of sequence b
+// (tierkv_triton.py:121-145) from the final M, L.
+template <bool COLD_ZERO>
+__device__ __forceinline__ float block_score(const DecodeParams& p, int b, int qh, int blk, int nb, float M, float L) {
+  if (blk >= nb || !(L > 0.f)) return 0.f;
+  const int64_t o = int64_t(b) * p.table_stride + blk;
+  const int st = p.states[o];
+  const int len = min(max(p.lengths[o], 0), FBS);
+  if (st == COLD) return COLD_ZERO ? float(len) * __builtin_amdgcn_exp2f(-M) / L : 0.f;
+  if ((st == HOT || st == WARM) && len > 0) {
+    const int64_t slot = p.table[o];
+    const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
+    if (slot >= 0 && slot < cap) {
+      const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
+      return load_dev(sp + 1) * __builtin_amdgcn_exp2f(load_dev(sp) - M) / L;
     }
   }
+  return 0.f;
 }
 
 template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT>
@@ -419,13 +414,11 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   constexpr int DS = D / 16;
   extern __shared__ float s_dyn[];               // [nw][G][D] wave accumulators
   __shared__ int4 s_list[MAX_LIST];              // (block, slot, len, state)
-  __shared__ int s_wcnt[MAX_WAVES];
-  __shared__ int s_cold;
+  __shared__ int s_wcnt[2 * MAX_WAVES];
+  __shared__ int s_wcold[MAX_WAVES];
   __shared__ int s_last;
   __shared__ float s_m[MAX_WAVES][16];
   __shared__ float s_l[MAX_WAVES][16];
-  __shared__ float s_M[32];
-  __shared__ float s_L[32];
 
   const int G = p.groups;
   const int splits = p.splits;
@@ -440,66 +433,110 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   const int w = tid >> 6;
   const int nb = seq_blocks(p, b);
 
-  // ---- this workgroup's share of the resident blocks ------------------------
-  // Ranks count HOT blocks first, then WARM, in logical order; the workgroup
-  // keeps rank % splits == split at list position rank / splits.
-  if (tid == 0) s_cold = 0;
-  int total = 0;
-  for (int pass = 0; pass < 2; ++pass) {
-    const int want = pass == 0 ? HOT : WARM;
-    for (int c0 = 0; c0 < nb; c0 += nthreads) {
-      const int idx = c0 + tid;
-      bool res = false;
-      int4 ent = make_int4(idx, 0, 0, want);
-      if (idx < nb) {
-        const int64_t o = int64_t(b) * p.table_stride + idx;
-        const int st = p.states[o];
-        const int len = min(max(p.lengths[o], 0), FBS);
-        if (st == want) {
-          const int slot = p.table[o];
-          const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-          const bool slot_ok = slot >= 0 && slot < cap;
-          if (!slot_ok && len > 0) atomicOr(p.ws_err, 1);
-          res = slot_ok && len > 0;
-          ent = make_int4(idx, slot, len, st);
-        } else if (pass == 0) {
-          if (st == COLD) {
-            if (COLD_ZERO && len > 0) atomicAdd(&s_cold, len);
-          } else if (st != WARM) {
-            atomicOr(p.ws_err, 2);
-          }
-        }
-      }
-      const uint64_t mask = __ballot(res);
-      if (lane == 0) s_wcnt[w] = __popcll(mask);
-      __syncthreads();
-      int before = total, chunk = 0;
-      for (int i = 0; i < nw; ++i) {
-        const int c = s_wcnt[i];
-        before += (i < w) ? c : 0;
-        chunk += c;
-      }
-      const int rank = before + __popcll(mask & ((1ull << lane) - 1ull));
-      if (res && rank % splits == split) s_list[rank / splits] = ent;
-      total += chunk;
-      __syncthreads();
-    }
-  }
-  const int nlist = (total > split) ? (total - split + splits - 1) / splits : 0;
-
-  // ---- query (fp16) and its per-head sum ------------------------------------
+  // ---- query: issued first, converted once the list is built ---------------
   const int n = lane & 15;
   const int g = lane >> 4;
   const bool head_ok = n < G;
   const int qh = kvh * G + (head_ok ? n : 0);
+  uint4 qraw[D / 32];
+  {
+    const uint4* qp = reinterpret_cast<const uint4*>(reinterpret_cast<const QT*>(p.q) +
+                                                     (int64_t(b) * p.num_heads + qh) * D + g * (D / 4));
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) qraw[i] = qp[i];
+  }
+
+  // ---- this workgroup's share of the resident blocks ------------------------
+  // Ranks count HOT blocks first, then WARM, in logical order; the workgroup
+  // keeps rank % splits == split at list position rank / splits.  COLD tokens
+  // (zero-logit mode) are counted per thread and reduced per wave.
+  int total = 0, total_hot = 0;
+  int cold_part = 0;
+  auto classify = [&](int idx, int want_mask, int4& ent, bool& hot, bool& warm) {
+    hot = warm = false;
+    ent = make_int4(idx, 0, 0, COLD);
+    if (idx >= nb) return;
+    const int64_t o = int64_t(b) * p.table_stride + idx;
+    const int st = p.states[o];
+    const int len = min(max(p.lengths[o], 0), FBS);
+    if (st == HOT || st == WARM) {
+      const int slot = p.table[o];
+      const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
+      const bool slot_ok = slot >= 0 && slot < cap;
+      const bool ok = slot_ok && len > 0;
+      if (!slot_ok && len > 0 && (want_mask & (1 << st))) atomicOr(p.ws_err, 1);   // flagged in st's pass
+      ent = make_int4(idx, slot, len, st);
+      hot = ok && st == HOT;
+      warm = ok && st == WARM;
+    } else if (want_mask & 1) {   // counted once, in the HOT (or single) pass
+      if (st == COLD) cold_part += COLD_ZERO ? len : 0;
+      else atomicOr(p.ws_err, 2);
+    }
+  };
+  if (nb <= nthreads) {
+    // One chunk: both ranks from one read of the row.
+    int4 ent;
+    bool hot, warm;
+    classify(tid, 3, ent, hot, warm);
+    const uint64_t mh = __ballot(hot);
+    const uint64_t mw = __ballot(warm);
+    if (lane == 0) {
+      s_wcnt[w] = __popcll(mh);
+      s_wcnt[MAX_WAVES + w] = __popcll(mw);
+    }
+    __syncthreads();
+    int hb = 0, wb = 0;
+    for (int i = 0; i < nw; ++i) {
+      const int ch = s_wcnt[i], cw = s_wcnt[MAX_WAVES + i];
+      hb += (i < w) ? ch : 0;
+      wb += (i < w) ? cw : 0;
+      total_hot += ch;
+      total += cw;
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    const int rank = hot ? hb + __popcll(mh & below) : total_hot + wb + __popcll(mw & below);
+    if ((hot || warm) && rank % splits == split) s_list[rank / splits] = ent;
+    total += total_hot;
+  } else {
+    for (int pass = 0; pass < 2; ++pass) {
+      for (int c0 = 0; c0 < nb; c0 += nthreads) {
+        int4 ent;
+        bool hot, warm;
+        classify(c0 + tid, pass == 0 ? 1 : 2, ent, hot, warm);
+        const bool res = pass == 0 ? hot : warm;
+        const uint64_t mask = __ballot(res);
+        if (lane == 0) s_wcnt[w] = __popcll(mask);
+        __syncthreads();
+        int before = total, chunk = 0;
+        for (int i = 0; i < nw; ++i) {
+          const int c = s_wcnt[i];
+          before += (i < w) ? c : 0;
+          chunk += c;
+        }
+        const int rank = before + __popcll(mask & ((1ull << lane) - 1ull));
+        if (res && rank % splits == split) s_list[rank / splits] = ent;
+        total += chunk;
+        __syncthreads();
+      }
+      if (pass == 0) total_hot = total;
+    }
+  }
+  if (COLD_ZERO) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) cold_part += __shfl_xor(cold_part, m, 64);
+    if (lane == 0) s_wcold[w] = cold_part;
+  }
+  __syncthreads();
+  const int nlist = (total > split) ? (total - split + splits - 1) / splits : 0;
+  const int nhot = (total_hot > split) ? (total_hot - split + splits - 1) / splits : 0;
+
+  // ---- query (fp16) and its per-head sum ------------------------------------
   uint32_t qv[D / 8];
   float qsum = 0.f;
   {
-    const QT* qp = reinterpret_cast<const QT*>(p.q) + (int64_t(b) * p.num_heads + qh) * D + g * (D / 4);
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
-      const uint4 x = reinterpret_cast<const uint4*>(qp)[i];
-      const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+      const uint32_t wd[4] = {qraw[i].x, qraw[i].y, qraw[i].z, qraw[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         uint32_t h2;
@@ -519,7 +556,13 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
     qsum += shfl_xor_f(qsum, 32);
   }
 
-  // ---- per-wave tile loop (ping-pong prefetch) -------------------------------
+  // ---- per-wave tile loops (ping-pong prefetch) ------------------------------
+  // The list holds this workgroup's HOT entries first (nhot of them), then
+  // its WARM ones; wave w takes positions w, w + nw, ...  The WARM tiles are
+  // processed first while the first HOT tile is already in flight.  List
+  // entries are read one step ahead so that each prefetch can be issued
+  // before the current tile's data is waited for; the scheduling barriers
+  // keep the compiler from moving that tile's compute above the prefetch.
   WaveState<D> st;
 #pragma unroll
   for (int s = 0; s < DS; ++s) st.acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -528,29 +571,53 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   st.corr = 0.f;
 
   const int mine = (nlist > w) ? (nlist - w + nw - 1) / nw : 0;
-  if (mine > 0) {
-    Tile<D> t0, t1;
-    int4 e0 = s_list[w];
-    int e0s = uniform(e0.w), e0slot = uniform(e0.y);
-    load_tile<D, WF>(p, kvh, e0s, e0slot, lane, t0);
-    for (int i = 0; i < mine; i += 2) {
+  const int mine_hot = (nhot > w) ? (nhot - w + nw - 1) / nw : 0;
+  const int mine_warm = mine - mine_hot;
+  const int warm0 = w + mine_hot * nw;   // list position of this wave's first WARM tile
+  HotTile<D> th0, th1;
+  if (mine_hot > 0) load_hot<D>(p, kvh, uniform(s_list[w].y), lane, th0);
+  if (mine_warm > 0) {
+    WarmTile<D, WF> tw0, tw1;
+    const int last = mine_warm - 1;
+    int4 e0 = s_list[warm0];
+    int4 e1 = s_list[warm0 + min(1, last) * nw];
+    load_warm<D, WF>(p, kvh, uniform(e0.y), lane, tw0);
+    for (int i = 0; i < mine_warm; i += 2) {
       // Prefetch the next tile (the last one again when there is none, so that
       // every iteration issues the same loads).
-      const int4 e1 = s_list[w + min(i + 1, mine - 1) * nw];
-      const int e1s = uniform(e1.w), e1slot = uniform(e1.y);
-      load_tile<D, WF>(p, kvh, e1s, e1slot, lane, t1);
-      process_tile<D, WF, SCORES>(p, t0, e0s, uniform(e0.x), uniform(e0.z), lane, head_ok, b, qh, qv, qsum, st);
-      if (i + 1 >= mine) break;
-      const int4 e2 = s_list[w + min(i + 2, mine - 1) * nw];
-      const int e2s = uniform(e2.w), e2slot = uniform(e2.y);
-      load_tile<D, WF>(p, kvh, e2s, e2slot, lane, t0);
-      process_tile<D, WF, SCORES>(p, t1, e1s, uniform(e1.x), uniform(e1.z), lane, head_ok, b, qh, qv, qsum, st);
+      load_warm<D, WF>(p, kvh, uniform(e1.y), lane, tw1);
+      __builtin_amdgcn_sched_barrier(0);
+      const int4 e2 = s_list[warm0 + min(i + 2, last) * nw];
+      process_warm<D, WF, SCORES>(p, tw0, uniform(e0.x), uniform(e0.z), lane, head_ok, b, qh, qv, qsum, st);
+      if (i + 1 >= mine_warm) break;
+      load_warm<D, WF>(p, kvh, uniform(e2.y), lane, tw0);
+      __builtin_amdgcn_sched_barrier(0);
+      const int4 e3 = s_list[warm0 + min(i + 3, last) * nw];
+      process_warm<D, WF, SCORES>(p, tw1, uniform(e1.x), uniform(e1.z), lane, head_ok, b, qh, qv, qsum, st);
       e0 = e2;
-      e0s = e2s;
+      e1 = e3;
+    }
+  }
+  if (mine_hot > 0) {
+    const int last = mine_hot - 1;
+    int4 e0 = s_list[w];
+    int4 e1 = s_list[w + min(1, last) * nw];
+    for (int i = 0; i < mine_hot; i += 2) {
+      load_hot<D>(p, kvh, uniform(e1.y), lane, th1);
+      __builtin_amdgcn_sched_barrier(0);
+      const int4 e2 = s_list[w + min(i + 2, last) * nw];
+      process_hot<D, SCORES>(p, th0, uniform(e0.x), uniform(e0.z), lane, head_ok, b, qh, qv, st);
+      if (i + 1 >= mine_hot) break;
+      load_hot<D>(p, kvh, uniform(e2.y), lane, th0);
+      __builtin_amdgcn_sched_barrier(0);
+      const int4 e3 = s_list[w + min(i + 3, last) * nw];
+      process_hot<D, SCORES>(p, th1, uniform(e1.x), uniform(e1.z), lane, head_ok, b, qh, qv, st);
+      e0 = e2;
+      e1 = e3;
     }
   }
 
-  // ---- merge the waves in LDS ------------------------------------------------
+  // ---- merge the waves in LDS (one barrier) ----------------------------------
   float l = st.l_part + shfl_xor_f(st.l_part, 16);
   l += shfl_xor_f(l, 32);
   float corr = st.corr + shfl_xor_f(st.corr, 16);
@@ -566,47 +633,66 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
 #pragma unroll
       for (int s = 0; s < DS; ++s) s_acc[(w * G + n) * D + (4 * g + r) * DS + s] = st.acc[s][r] - corr;
   }
+  if (SCORES) __builtin_amdgcn_s_waitcnt(0);   // this wave's per-block statistics are stored
   __syncthreads();
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][tid]);
-    float L = 0.f;
+  float cold_tokens = 0.f;
+  if (COLD_ZERO)
+    for (int i = 0; i < nw; ++i) cold_tokens += float(s_wcold[i]);
+  // (M, L) of head h over this workgroup's waves.
+  auto wave_ml = [&](int h, float& M, float& L) {
+    M = -INFINITY;
+    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][h]);
+    L = 0.f;
     for (int ww = 0; ww < nw; ++ww) {
-      const float mw = s_m[ww][tid];
-      L += (mw == -INFINITY) ? 0.f : s_l[ww][tid] * __builtin_amdgcn_exp2f(mw - M);
+      const float mw = s_m[ww][h];
+      L += (mw == -INFINITY) ? 0.f : s_l[ww][h] * __builtin_amdgcn_exp2f(mw - M);
     }
-    s_M[tid] = M;
-    s_L[tid] = L;
-  }
-  __syncthreads();
-  // Combined accumulator of this workgroup into wave 0's LDS slice.
-  for (int i = tid; i < G * D; i += nthreads) {
-    const int h = i / D;
-    const float M = s_M[h];
+  };
+  auto wave_acc = [&](int i, int h, float M) {
     float A = 0.f;
     for (int ww = 0; ww < nw; ++ww) {
       const float mw = s_m[ww][h];
       if (mw != -INFINITY) A += s_acc[ww * G * D + i] * __builtin_amdgcn_exp2f(mw - M);
     }
-    if (splits == 1) {
-      s_acc[i] = A;   // row i of wave 0 is read only by this thread
-    } else {
-      const int64_t pi = (int64_t(unit) * splits + split) * G + h;
-      store_dev(p.ws_acc + pi * D + (i - h * D), A);
-    }
-  }
-  const float cold_tokens = COLD_ZERO ? float(s_cold) : 0.f;
+    return A;
+  };
+  QT* out = reinterpret_cast<QT*>(p.out) + (int64_t(b) * p.num_heads + kvh * G) * D;
+
   if (splits == 1) {
-    if (SCORES) __builtin_amdgcn_s_waitcnt(0);   // per-block statistics stored
-    finalize_unit<QT, COLD_ZERO>(p, b, kvh, cold_tokens, s_acc, s_M, s_L, G, D, tid, nthreads);
+    for (int i = tid; i < G * D; i += nthreads) {
+      const int h = i / D;
+      float M, L, f;
+      wave_ml(h, M, L);
+      const float A = wave_acc(i, h, M);
+      cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
+      out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
+    }
+    if (SCORES) {
+      const int stride = int(p.table_stride);
+      for (int i = tid; i < G * stride; i += nthreads) {
+        const int h = i / stride;
+        const int blk = i - h * stride;
+        float M, L, f;
+        wave_ml(h, M, L);
+        cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
+        p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] =
+            block_score<COLD_ZERO>(p, b, kvh * G + h, blk, nb, M, L);
+      }
+    }
     return;
   }
 
   // ---- splits: publish the partial, the last workgroup merges -----------------
-  if (tid < G) {
-    const int64_t pi = (int64_t(unit) * splits + split) * G + tid;
-    store_dev(p.ws_ml + pi * 2 + 0, s_M[tid]);
-    store_dev(p.ws_ml + pi * 2 + 1, s_L[tid]);
+  for (int i = tid; i < G * D; i += nthreads) {
+    const int h = i / D;
+    float M, L;
+    wave_ml(h, M, L);
+    const int64_t pi = (int64_t(unit) * splits + split) * G + h;
+    store_dev(p.ws_acc + pi * D + (i - h * D), wave_acc(i, h, M));
+    if (i - h * D == 0) {
+      store_dev(p.ws_ml + pi * 2 + 0, M);
+      store_dev(p.ws_ml + pi * 2 + 1, L);
+    }
   }
   // Every wave's device-coherent stores complete before the arrival is counted.
   __builtin_amdgcn_s_waitcnt(0);
@@ -617,33 +703,42 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   }
   __syncthreads();
   if (!s_last) return;
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int s = 0; s < splits; ++s) M = fmaxf(M, load_dev(p.ws_ml + ((int64_t(unit) * splits + s) * G + tid) * 2));
-    float L = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const float* ml = p.ws_ml + ((int64_t(unit) * splits + s) * G + tid) * 2;
+  auto split_ml = [&](int h, float& M, float& L) {
+    M = -INFINITY;
+    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, load_dev(p.ws_ml + ((int64_t(unit) * splits + sp) * G + h) * 2));
+    L = 0.f;
+    for (int sp = 0; sp < splits; ++sp) {
+      const float* ml = p.ws_ml + ((int64_t(unit) * splits + sp) * G + h) * 2;
       const float ms = load_dev(ml);
-      const float ls = load_dev(ml + 1);
-      L += (ms == -INFINITY) ? 0.f : ls * __builtin_amdgcn_exp2f(ms - M);
+      L += (ms == -INFINITY) ? 0.f : load_dev(ml + 1) * __builtin_amdgcn_exp2f(ms - M);
     }
-    s_M[tid] = M;
-    s_L[tid] = L;
-  }
-  __syncthreads();
+  };
   for (int i = tid; i < G * D; i += nthreads) {
     const int h = i / D;
-    const float M = s_M[h];
+    float M, L, f;
+    split_ml(h, M, L);
     float A = 0.f;
-    for (int s = 0; s < splits; ++s) {
-      const int64_t pi = (int64_t(unit) * splits + s) * G + h;
+    for (int sp = 0; sp < splits; ++sp) {
+      const int64_t pi = (int64_t(unit) * splits + sp) * G + h;
       const float ms = load_dev(p.ws_ml + pi * 2);
       if (ms != -INFINITY) A += load_dev(p.ws_acc + pi * D + (i - h * D)) * __builtin_amdgcn_exp2f(ms - M);
     }
-    s_acc[i] = A;
+    cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
+    out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
+  }
+  if (SCORES) {
+    const int stride = int(p.table_stride);
+    for (int i = tid; i < G * stride; i += nthreads) {
+      const int h = i / stride;
+      const int blk = i - h * stride;
+      float M, L, f;
+      split_ml(h, M, L);
+      cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
+      p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] =
+          block_score<COLD_ZERO>(p, b, kvh * G + h, blk, nb, M, L);
+    }
   }
   if (tid == 0) __hip_atomic_store(p.ws_cnt + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  finalize_unit<QT, COLD_ZERO>(p, b, kvh, cold_tokens, s_acc, s_M, s_L, G, D, tid, nthreads);
 }
 
 // --------------------------------------------------------------------------
