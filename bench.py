@@ -172,8 +172,10 @@ def main():
     gbs = nbytes / sec / 1e9
     log(f"[bench] {sec * 1e6:.2f} us/layer-step, {gbs:.1f} GB/s algorithmic ({gbs / PEAK_HBM_GBS:.1%} of peak)")
 
+    # HBM bytes per launch of the decode kernel from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE summary of this workload (copy-calibrated).
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"{case.name}_decode_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"tiered_decode_kernel_{case.name}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
