@@ -34,7 +34,11 @@ HIP_SOURCES = {
     # The tier branches of the tile loader store to different elements of the
     # same register arrays; LLVM's common-store sinking would merge them into
     # one dynamically indexed store and push the tiles to scratch memory.
-    "decode_attention.hip": ["-mllvm", "-simplifycfg-sink-common=false"],
+    # The decode kernel's leading scalar arguments (table row pointers, query,
+    # geometry) are preloaded into SGPRs at wave launch, saving a kernarg
+    # round trip before the table row can be read.
+    "decode_attention.hip": ["-mllvm", "-simplifycfg-sink-common=false",
+                             "-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
 }

@@ -127,63 +127,98 @@ struct WarmTile {
   uint32_t m[NM];
 };
 
+// Tile loads go through buffer resources built per tile in scalar registers
+// (base = the tile's first byte, num_records = its size).  A dead load (a
+// pipeline step past the end of the list) gets num_records = 0: every lane is
+// out of range, the hardware returns zeros without a memory access, and the
+// load retires quickly, so a wave leaving its loop does not wait for a memory
+// round trip before its registers can be reused.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 buffer descriptor: raw 32-bit dwords
+// Cache policy of the tile loads: non-temporal.  Every tile byte is read once
+// per launch; the streaming hint keeps the tiles from displacing other lines
+// and measurably raises gather bandwidth on gfx950.
+#ifndef TIERKV_TILE_CPOL
+#define TIERKV_TILE_CPOL 2
+#endif
+constexpr int TILE_CPOL = TIERKV_TILE_CPOL;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, RSRC_WORD3);
+}
+
 template <int D>
-__device__ __forceinline__ void load_hot(const DecodeParams& p, int kvh, int slot, int lane, HotTile<D>& t) {
+__device__ __forceinline__ void load_hot(const DecodeParams& p, int kvh, int slot, int lane, HotTile<D>& t,
+                                         bool live) {
   const int n = lane & 15;
   const int g = lane >> 4;
+  constexpr uint32_t TILE = FBS * D * 2;
   const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;   // first token row of the tile
-  const uint4* kp = reinterpret_cast<const uint4*>(p.hot_k + tile0 * D) + n * (D / 8) + g * (D / 32);
+  const auto rk = tile_rsrc(p.hot_k + tile0 * D, live ? TILE : 0u);
+  const auto rv = tile_rsrc(p.hot_v + tile0 * D, live ? TILE : 0u);
+  const int ko = (n * (D / 8) + g * (D / 32)) * 16;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
-    const uint4 x = kp[i];
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * i, 0, TILE_CPOL);
     t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const __half* vp = p.hot_v + (tile0 + 4 * g + j) * D + n * (D / 16);
+    const int vo = ((4 * g + j) * D + n * (D / 16)) * 2;
     if constexpr (D == 128) {
-      const uint4 x = *reinterpret_cast<const uint4*>(vp);
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rv, vo, 0, TILE_CPOL);
       t.v[4 * j + 0] = x.x; t.v[4 * j + 1] = x.y; t.v[4 * j + 2] = x.z; t.v[4 * j + 3] = x.w;
     } else {
-      const uint2 x = *reinterpret_cast<const uint2*>(vp);
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, vo, 0, TILE_CPOL);
       t.v[2 * j + 0] = x.x; t.v[2 * j + 1] = x.y;
     }
   }
 }
 
 template <int D, int WF>
-__device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int slot, int lane, WarmTile<D, WF>& t) {
+__device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int slot, int lane, WarmTile<D, WF>& t,
+                                          bool live) {
   const int n = lane & 15;
   const int g = lane >> 4;
+  constexpr uint32_t TILE = FBS * D;
   const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;
-  const uint8_t* wk = reinterpret_cast<const uint8_t*>(p.warm_k) + tile0 * D;
-  const uint8_t* wv = reinterpret_cast<const uint8_t*>(p.warm_v) + tile0 * D;
-  const uint4* kp = reinterpret_cast<const uint4*>(wk + n * D + g * (D / 4));
+  const auto rk = tile_rsrc(reinterpret_cast<const uint8_t*>(p.warm_k) + tile0 * D, live ? TILE : 0u);
+  const auto rv = tile_rsrc(reinterpret_cast<const uint8_t*>(p.warm_v) + tile0 * D, live ? TILE : 0u);
+  const int ko = n * D + g * (D / 4);
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) {
-    const uint4 x = kp[i];
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * i, 0, TILE_CPOL);
     t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const uint8_t* vp = wv + (4 * g + j) * D + n * (D / 16);
+    const int vo = (4 * g + j) * D + n * (D / 16);
     if constexpr (D == 128) {
-      const uint2 x = *reinterpret_cast<const uint2*>(vp);
+      const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rv, vo, 0, TILE_CPOL);
       t.v[2 * j + 0] = x.x; t.v[2 * j + 1] = x.y;
     } else {
-      t.v[j] = *reinterpret_cast<const uint32_t*>(vp);
+      t.v[j] = __builtin_amdgcn_raw_buffer_load_b32(rv, vo, 0, TILE_CPOL);
     }
   }
   if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
     const int64_t si = int64_t(slot) * p.kv_heads + kvh;
-    t.m[0] = __float_as_uint(reinterpret_cast<const float*>(p.k_scale)[si]);
-    t.m[1] = __float_as_uint(reinterpret_cast<const float*>(p.v_scale)[si]);
+    const auto rs = tile_rsrc(reinterpret_cast<const float*>(p.k_scale) + si, live ? 4u : 0u);
+    const auto rz = tile_rsrc(reinterpret_cast<const float*>(p.v_scale) + si, live ? 4u : 0u);
+    t.m[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0);
+    t.m[1] = __builtin_amdgcn_raw_buffer_load_b32(rz, 0, 0, 0);
   } else {
-    const int64_t mi = tile0 + 4 * g;   // halves; 8-byte aligned
-    const uint2 ks = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_scale) + mi);
-    const uint2 kz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.k_zero) + mi);
-    const uint2 vs = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_scale) + mi);
-    const uint2 vz = *reinterpret_cast<const uint2*>(reinterpret_cast<const __half*>(p.v_zero) + mi);
+    // Per-token fp16 scale and zero of tokens 4g .. 4g+3 (8-byte aligned).
+    constexpr uint32_t META = FBS * 2;
+    const int mo = 8 * g;
+    const auto r0 = tile_rsrc(reinterpret_cast<const __half*>(p.k_scale) + tile0, live ? META : 0u);
+    const auto r1 = tile_rsrc(reinterpret_cast<const __half*>(p.k_zero) + tile0, live ? META : 0u);
+    const auto r2 = tile_rsrc(reinterpret_cast<const __half*>(p.v_scale) + tile0, live ? META : 0u);
+    const auto r3 = tile_rsrc(reinterpret_cast<const __half*>(p.v_zero) + tile0, live ? META : 0u);
+    const u32x2 ks = __builtin_amdgcn_raw_buffer_load_b64(r0, mo, 0, 0);
+    const u32x2 kz = __builtin_amdgcn_raw_buffer_load_b64(r1, mo, 0, 0);
+    const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(r2, mo, 0, 0);
+    const u32x2 vz = __builtin_amdgcn_raw_buffer_load_b64(r3, mo, 0, 0);
     t.m[0] = ks.x; t.m[1] = ks.y; t.m[2] = kz.x; t.m[3] = kz.y;
     t.m[4] = vs.x; t.m[5] = vs.y; t.m[6] = vz.x; t.m[7] = vz.y;
   }
@@ -409,29 +444,42 @@ __device__ __forceinline__ float block_score(const DecodeParams& p, int b, int q
   return 0.f;
 }
 
-template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT>
-__global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodeParams p) {
+// The arguments the list build needs first come ahead of the parameter block
+// so that they can be preloaded into scalar registers at wave launch.
+template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT, int NW>
+__global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
+    const int32_t* __restrict__ a_table, const int32_t* __restrict__ a_states,
+    const int32_t* __restrict__ a_lengths, const void* __restrict__ a_q,
+    const int32_t* __restrict__ a_seq_nblocks, int32_t a_stride, int32_t a_num_blocks,
+    int32_t a_kv_heads, int32_t a_splits, DecodeParams p) {
   constexpr int DS = D / 16;
-  extern __shared__ float s_dyn[];               // [nw][G][D] wave accumulators
+  extern __shared__ float s_dyn[];               // [NW][G][D] wave accumulators
   __shared__ int4 s_list[MAX_LIST];              // (block, slot, len, state)
   __shared__ int s_wcnt[2 * MAX_WAVES];
   __shared__ int s_wcold[MAX_WAVES];
   __shared__ int s_last;
+  __shared__ int s_next[2];                      // next WARM / HOT list position to hand out
   __shared__ float s_m[MAX_WAVES][16];
   __shared__ float s_l[MAX_WAVES][16];
 
   const int G = p.groups;
-  const int splits = p.splits;
+  const int splits = a_splits;
   const int split = blockIdx.x % splits;
   const int unit = blockIdx.x / splits;
-  const int b = unit / p.kv_heads;
-  const int kvh = unit % p.kv_heads;
+  const int b = unit / a_kv_heads;
+  const int kvh = unit % a_kv_heads;
   const int tid = threadIdx.x;
-  const int nthreads = blockDim.x;
-  const int nw = nthreads >> 6;
+  constexpr int nthreads = NW * 64;
+  constexpr int nw = NW;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int nb = seq_blocks(p, b);
+  // Blocks of this sequence: the per-sequence count is loaded together with
+  // the first row chunk and applied afterwards.
+  const int nb_ld = a_seq_nblocks ? a_seq_nblocks[b] : a_num_blocks;
+  if (tid == 0) {
+    s_next[0] = 0;
+    s_next[1] = 0;
+  }
 
   // ---- query: issued first, converted once the list is built ---------------
   const int n = lane & 15;
@@ -440,44 +488,49 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   const int qh = kvh * G + (head_ok ? n : 0);
   uint4 qraw[D / 32];
   {
-    const uint4* qp = reinterpret_cast<const uint4*>(reinterpret_cast<const QT*>(p.q) +
+    const uint4* qp = reinterpret_cast<const uint4*>(reinterpret_cast<const QT*>(a_q) +
                                                      (int64_t(b) * p.num_heads + qh) * D + g * (D / 4));
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) qraw[i] = qp[i];
   }
 
   // ---- this workgroup's share of the resident blocks ------------------------
-  // Ranks count HOT blocks first, then WARM, in logical order; the workgroup
-  // keeps rank % splits == split at list position rank / splits.  COLD tokens
-  // (zero-logit mode) are counted per thread and reduced per wave.
-  int total = 0, total_hot = 0;
+  // One pass over the table row.  HOT and WARM blocks are ranked separately in
+  // logical order; the workgroup keeps rank % splits == split, HOT entries at
+  // list positions [0, nhot) from the front, WARM entries from the back
+  // (position MAX_LIST - 1 - k for the k-th).  The three entries of a block
+  // (state, length, slot) are loaded together.  COLD tokens (zero-logit
+  // mode) are counted per thread and reduced per wave.
+  int nb = a_num_blocks;
+  int seen_hot = 0, seen_warm = 0;
   int cold_part = 0;
-  auto classify = [&](int idx, int want_mask, int4& ent, bool& hot, bool& warm) {
-    hot = warm = false;
-    ent = make_int4(idx, 0, 0, COLD);
-    if (idx >= nb) return;
-    const int64_t o = int64_t(b) * p.table_stride + idx;
-    const int st = p.states[o];
-    const int len = min(max(p.lengths[o], 0), FBS);
-    if (st == HOT || st == WARM) {
-      const int slot = p.table[o];
-      const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-      const bool slot_ok = slot >= 0 && slot < cap;
-      const bool ok = slot_ok && len > 0;
-      if (!slot_ok && len > 0 && (want_mask & (1 << st))) atomicOr(p.ws_err, 1);   // flagged in st's pass
-      ent = make_int4(idx, slot, len, st);
-      hot = ok && st == HOT;
-      warm = ok && st == WARM;
-    } else if (want_mask & 1) {   // counted once, in the HOT (or single) pass
-      if (st == COLD) cold_part += COLD_ZERO ? len : 0;
-      else atomicOr(p.ws_err, 2);
+  for (int c0 = 0; c0 < a_num_blocks; c0 += nthreads) {
+    const int idx = c0 + tid;
+    int st = COLD, len = 0, slot = -1;
+    if (idx < a_num_blocks) {
+      const int64_t o = int64_t(b) * a_stride + idx;
+      st = a_states[o];
+      len = a_lengths[o];
+      slot = a_table[o];
+      __builtin_amdgcn_sched_barrier(0);   // all three in flight before any use
     }
-  };
-  if (nb <= nthreads) {
-    // One chunk: both ranks from one read of the row.
-    int4 ent;
-    bool hot, warm;
-    classify(tid, 3, ent, hot, warm);
+    if (c0 == 0) nb = uniform(min(max(nb_ld, 0), a_num_blocks));
+    len = min(max(len, 0), FBS);
+    bool hot = false, warm = false;
+    const int4 ent = make_int4(idx, slot, len, st);
+    if (idx < nb) {
+      if (st == HOT || st == WARM) {
+        const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
+        const bool slot_ok = slot >= 0 && slot < cap;
+        if (!slot_ok && len > 0) atomicOr(p.ws_err, 1);
+        hot = slot_ok && len > 0 && st == HOT;
+        warm = slot_ok && len > 0 && st == WARM;
+      } else if (st == COLD) {
+        cold_part += COLD_ZERO ? len : 0;
+      } else {
+        atomicOr(p.ws_err, 2);
+      }
+    }
     const uint64_t mh = __ballot(hot);
     const uint64_t mw = __ballot(warm);
     if (lane == 0) {
@@ -485,41 +538,25 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
       s_wcnt[MAX_WAVES + w] = __popcll(mw);
     }
     __syncthreads();
-    int hb = 0, wb = 0;
+    int hb = seen_hot, wb = seen_warm;
+#pragma unroll
     for (int i = 0; i < nw; ++i) {
       const int ch = s_wcnt[i], cw = s_wcnt[MAX_WAVES + i];
       hb += (i < w) ? ch : 0;
       wb += (i < w) ? cw : 0;
-      total_hot += ch;
-      total += cw;
+      seen_hot += ch;
+      seen_warm += cw;
     }
     const uint64_t below = (1ull << lane) - 1ull;
-    const int rank = hot ? hb + __popcll(mh & below) : total_hot + wb + __popcll(mw & below);
-    if ((hot || warm) && rank % splits == split) s_list[rank / splits] = ent;
-    total += total_hot;
-  } else {
-    for (int pass = 0; pass < 2; ++pass) {
-      for (int c0 = 0; c0 < nb; c0 += nthreads) {
-        int4 ent;
-        bool hot, warm;
-        classify(c0 + tid, pass == 0 ? 1 : 2, ent, hot, warm);
-        const bool res = pass == 0 ? hot : warm;
-        const uint64_t mask = __ballot(res);
-        if (lane == 0) s_wcnt[w] = __popcll(mask);
-        __syncthreads();
-        int before = total, chunk = 0;
-        for (int i = 0; i < nw; ++i) {
-          const int c = s_wcnt[i];
-          before += (i < w) ? c : 0;
-          chunk += c;
-        }
-        const int rank = before + __popcll(mask & ((1ull << lane) - 1ull));
-        if (res && rank % splits == split) s_list[rank / splits] = ent;
-        total += chunk;
-        __syncthreads();
-      }
-      if (pass == 0) total_hot = total;
+    if (hot) {
+      const int r = hb + __popcll(mh & below);
+      if (r % splits == split) s_list[r / splits] = ent;
     }
+    if (warm) {
+      const int r = wb + __popcll(mw & below);
+      if (r % splits == split) s_list[MAX_LIST - 1 - r / splits] = ent;
+    }
+    if (c0 + nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
   }
   if (COLD_ZERO) {
 #pragma unroll
@@ -527,8 +564,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
     if (lane == 0) s_wcold[w] = cold_part;
   }
   __syncthreads();
-  const int nlist = (total > split) ? (total - split + splits - 1) / splits : 0;
-  const int nhot = (total_hot > split) ? (total_hot - split + splits - 1) / splits : 0;
+  const int nhot = uniform((seen_hot > split) ? (seen_hot - split + splits - 1) / splits : 0);
+  const int nwarm = uniform((seen_warm > split) ? (seen_warm - split + splits - 1) / splits : 0);
 
   // ---- query (fp16) and its per-head sum ------------------------------------
   uint32_t qv[D / 8];
@@ -556,13 +593,16 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
     qsum += shfl_xor_f(qsum, 32);
   }
 
-  // ---- per-wave tile loops (ping-pong prefetch) ------------------------------
-  // The list holds this workgroup's HOT entries first (nhot of them), then
-  // its WARM ones; wave w takes positions w, w + nw, ...  The WARM tiles are
-  // processed first while the first HOT tile is already in flight.  List
-  // entries are read one step ahead so that each prefetch can be issued
-  // before the current tile's data is waited for; the scheduling barriers
-  // keep the compiler from moving that tile's compute above the prefetch.
+  // ---- per-wave tile loops -------------------------------------------------
+  // The list holds this workgroup's HOT entries at positions [0, nhot) and its
+  // WARM entries at MAX_LIST - 1 - [0, nwarm).  Waves take positions from two LDS counters
+  // (WARM first, then HOT), one tile at a time: the SIMD arbiter favours the
+  // older of the two waves it hosts, so a static split would leave the younger
+  // waves finishing several tiles late.  Each wave keeps NBW (NBH) tiles of a
+  // register pipeline in flight.  Every step issues its load unconditionally
+  // (a position past the end reads one cache line for the whole wave and is
+  // never processed) and the loops leave only through their latch, so the
+  // compiler's wait counts stay exact across iterations.
   WaveState<D> st;
 #pragma unroll
   for (int s = 0; s < DS; ++s) st.acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -570,51 +610,82 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   st.l_part = 0.f;
   st.corr = 0.f;
 
-  const int mine = (nlist > w) ? (nlist - w + nw - 1) / nw : 0;
-  const int mine_hot = (nhot > w) ? (nhot - w + nw - 1) / nw : 0;
-  const int mine_warm = mine - mine_hot;
-  const int warm0 = w + mine_hot * nw;   // list position of this wave's first WARM tile
-  HotTile<D> th0, th1;
-  if (mine_hot > 0) load_hot<D>(p, kvh, uniform(s_list[w].y), lane, th0);
-  if (mine_warm > 0) {
-    WarmTile<D, WF> tw0, tw1;
-    const int last = mine_warm - 1;
-    int4 e0 = s_list[warm0];
-    int4 e1 = s_list[warm0 + min(1, last) * nw];
-    load_warm<D, WF>(p, kvh, uniform(e0.y), lane, tw0);
-    for (int i = 0; i < mine_warm; i += 2) {
-      // Prefetch the next tile (the last one again when there is none, so that
-      // every iteration issues the same loads).
-      load_warm<D, WF>(p, kvh, uniform(e1.y), lane, tw1);
+  auto grab = [&](int c) -> int {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(&s_next[c], 1);
+    return uniform(v);
+  };
+  constexpr int NBH = 2;
+  constexpr int NBW = 2;
+  HotTile<D> th[NBH];
+  int4 eh[NBH];
+  bool lh[NBH];
+  int4 hne = make_int4(0, 0, 0, 0);   // next HOT entry to load and whether it is live
+  bool hnl = false;
+  if (nhot > 0) {
+    int gi = grab(1);
+    hne = s_list[min(gi, nhot - 1)];
+    hnl = gi < nhot;
+#pragma unroll
+    for (int k = 0; k < NBH - 1; ++k) {
+      eh[k] = hne;
+      lh[k] = hnl;
+      load_hot<D>(p, kvh, uniform(hne.y), lane, th[k], hnl);
       __builtin_amdgcn_sched_barrier(0);
-      const int4 e2 = s_list[warm0 + min(i + 2, last) * nw];
-      process_warm<D, WF, SCORES>(p, tw0, uniform(e0.x), uniform(e0.z), lane, head_ok, b, qh, qv, qsum, st);
-      if (i + 1 >= mine_warm) break;
-      load_warm<D, WF>(p, kvh, uniform(e2.y), lane, tw0);
-      __builtin_amdgcn_sched_barrier(0);
-      const int4 e3 = s_list[warm0 + min(i + 3, last) * nw];
-      process_warm<D, WF, SCORES>(p, tw1, uniform(e1.x), uniform(e1.z), lane, head_ok, b, qh, qv, qsum, st);
-      e0 = e2;
-      e1 = e3;
+      gi = grab(1);
+      hne = s_list[min(gi, nhot - 1)];
+      hnl = gi < nhot;
     }
   }
-  if (mine_hot > 0) {
-    const int last = mine_hot - 1;
-    int4 e0 = s_list[w];
-    int4 e1 = s_list[w + min(1, last) * nw];
-    for (int i = 0; i < mine_hot; i += 2) {
-      load_hot<D>(p, kvh, uniform(e1.y), lane, th1);
+  if (nwarm > 0) {
+    WarmTile<D, WF> tw[NBW];
+    int4 ew[NBW];
+    bool lw[NBW];
+    int gi = grab(0);
+    int4 ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
+    bool nl = gi < nwarm;
+#pragma unroll
+    for (int k = 0; k < NBW - 1; ++k) {
+      ew[k] = ne;
+      lw[k] = nl;
+      load_warm<D, WF>(p, kvh, uniform(ne.y), lane, tw[k], nl);
       __builtin_amdgcn_sched_barrier(0);
-      const int4 e2 = s_list[w + min(i + 2, last) * nw];
-      process_hot<D, SCORES>(p, th0, uniform(e0.x), uniform(e0.z), lane, head_ok, b, qh, qv, st);
-      if (i + 1 >= mine_hot) break;
-      load_hot<D>(p, kvh, uniform(e2.y), lane, th0);
-      __builtin_amdgcn_sched_barrier(0);
-      const int4 e3 = s_list[w + min(i + 3, last) * nw];
-      process_hot<D, SCORES>(p, th1, uniform(e1.x), uniform(e1.z), lane, head_ok, b, qh, qv, st);
-      e0 = e2;
-      e1 = e3;
+      gi = grab(0);
+      ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
+      nl = gi < nwarm;
     }
+    do {
+#pragma unroll
+      for (int k = 0; k < NBW; ++k) {
+        const int kn = (k + NBW - 1) % NBW;
+        ew[kn] = ne;
+        lw[kn] = nl;
+        load_warm<D, WF>(p, kvh, uniform(ne.y), lane, tw[kn], nl);
+        __builtin_amdgcn_sched_barrier(0);
+        gi = grab(0);
+        ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
+        nl = gi < nwarm;
+        if (lw[k])
+          process_warm<D, WF, SCORES>(p, tw[k], uniform(ew[k].x), uniform(ew[k].z), lane, head_ok, b, qh, qv, qsum, st);
+      }
+    } while (lw[0]);   // buffer 0 holds the next tile; positions are handed out in order
+  }
+  if (nhot > 0) {
+    do {
+#pragma unroll
+      for (int k = 0; k < NBH; ++k) {
+        const int kn = (k + NBH - 1) % NBH;
+        eh[kn] = hne;
+        lh[kn] = hnl;
+        load_hot<D>(p, kvh, uniform(hne.y), lane, th[kn], hnl);
+        __builtin_amdgcn_sched_barrier(0);
+        const int gi = grab(1);
+        hne = s_list[min(gi, nhot - 1)];
+        hnl = gi < nhot;
+        if (lh[k])
+          process_hot<D, SCORES>(p, th[k], uniform(eh[k].x), uniform(eh[k].z), lane, head_ok, b, qh, qv, st);
+      }
+    } while (lh[0]);
   }
 
   // ---- merge the waves in LDS (one barrier) ----------------------------------
@@ -636,24 +707,31 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   if (SCORES) __builtin_amdgcn_s_waitcnt(0);   // this wave's per-block statistics are stored
   __syncthreads();
   float cold_tokens = 0.f;
-  if (COLD_ZERO)
+  if (COLD_ZERO) {
+#pragma unroll
     for (int i = 0; i < nw; ++i) cold_tokens += float(s_wcold[i]);
-  // (M, L) of head h over this workgroup's waves.
-  auto wave_ml = [&](int h, float& M, float& L) {
+  }
+  // (M, L) of head h over this workgroup's waves and each wave's weight
+  // 2^(m_w - M) (0 for a wave that saw no token).  The loops are unrolled so
+  // that all LDS reads are in flight together.
+  auto wave_ml = [&](int h, float& M, float& L, float* fw) {
+    float mw[NW];
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) mw[ww] = s_m[ww][h];
     M = -INFINITY;
-    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][h]);
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, mw[ww]);
     L = 0.f;
-    for (int ww = 0; ww < nw; ++ww) {
-      const float mw = s_m[ww][h];
-      L += (mw == -INFINITY) ? 0.f : s_l[ww][h] * __builtin_amdgcn_exp2f(mw - M);
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      fw[ww] = (mw[ww] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw[ww] - M);
+      L += s_l[ww][h] * fw[ww];
     }
   };
-  auto wave_acc = [&](int i, int h, float M) {
+  auto wave_acc = [&](int i, const float* fw) {
     float A = 0.f;
-    for (int ww = 0; ww < nw; ++ww) {
-      const float mw = s_m[ww][h];
-      if (mw != -INFINITY) A += s_acc[ww * G * D + i] * __builtin_amdgcn_exp2f(mw - M);
-    }
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) A += s_acc[ww * G * D + i] * fw[ww];
     return A;
   };
   QT* out = reinterpret_cast<QT*>(p.out) + (int64_t(b) * p.num_heads + kvh * G) * D;
@@ -661,9 +739,9 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   if (splits == 1) {
     for (int i = tid; i < G * D; i += nthreads) {
       const int h = i / D;
-      float M, L, f;
-      wave_ml(h, M, L);
-      const float A = wave_acc(i, h, M);
+      float M, L, f, fw[NW];
+      wave_ml(h, M, L, fw);
+      const float A = wave_acc(i, fw);
       cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
       out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
     }
@@ -672,8 +750,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
       for (int i = tid; i < G * stride; i += nthreads) {
         const int h = i / stride;
         const int blk = i - h * stride;
-        float M, L, f;
-        wave_ml(h, M, L);
+        float M, L, f, fw[NW];
+        wave_ml(h, M, L, fw);
         cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
         p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] =
             block_score<COLD_ZERO>(p, b, kvh * G + h, blk, nb, M, L);
@@ -685,10 +763,10 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(DecodePar
   // ---- splits: publish the partial, the last workgroup merges -----------------
   for (int i = tid; i < G * D; i += nthreads) {
     const int h = i / D;
-    float M, L;
-    wave_ml(h, M, L);
+    float M, L, fw[NW];
+    wave_ml(h, M, L, fw);
     const int64_t pi = (int64_t(unit) * splits + split) * G + h;
-    store_dev(p.ws_acc + pi * D + (i - h * D), wave_acc(i, h, M));
+    store_dev(p.ws_acc + pi * D + (i - h * D), wave_acc(i, fw));
     if (i - h * D == 0) {
       store_dev(p.ws_ml + pi * 2 + 0, M);
       store_dev(p.ws_ml + pi * 2 + 1, L);
@@ -947,7 +1025,13 @@ static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks
 template <int D, int WF, bool SC, bool CZ, typename QT>
 static void launch_fast(const DecodeParams& p, int nw, int grid, hipStream_t stream) {
   const size_t shmem = size_t(nw) * p.groups * D * sizeof(float);
-  hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT>), dim3(grid), dim3(nw * 64), shmem, stream, p);
+  const int32_t stride = int32_t(p.table_stride);
+  if (nw == 8)
+    hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, 8>), dim3(grid), dim3(8 * 64), shmem, stream,
+                       p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, p.kv_heads, p.splits, p);
+  else
+    hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, 4>), dim3(grid), dim3(4 * 64), shmem, stream,
+                       p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, p.kv_heads, p.splits, p);
 }
 
 template <int D, int WF, typename QT>
@@ -1071,7 +1155,7 @@ extern "C" int32_t tierkv_decode_attention(
   const bool cz = cold_mode == TIERKV_COLD_ZERO_LOGIT;
   const bool bf16 = query_dtype == TIERKV_DTYPE_BF16;
 
-  if (fast_path_ok(block_size, head_dim, p.groups)) {
+  if (fast_path_ok(block_size, head_dim, p.groups) && table_stride <= 0x7fffffff) {
     const bool aligned = aligned16(hot_k) && aligned16(hot_v) && aligned16(warm_k) && aligned16(warm_v) &&
                          aligned16(query);
     if (!aligned) return fail(TIERKV_ERR_INVALID, "query and pool base pointers must be 16-byte aligned");
