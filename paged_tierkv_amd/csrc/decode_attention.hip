@@ -33,6 +33,7 @@
 #include "tierkv_common.h"
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <cfloat>
 #include <cmath>
@@ -75,10 +76,28 @@ struct DecodeParams {
   float* ws_acc;      // [units][splits][G][D]
   float* ws_ml;       // [units][splits][G][2]
   float* ws_stage;    // [B][H][num_blocks][2]  (block reference max, block sum)
-  int32_t* ws_cnt;    // [units] arrival counters (zero between launches)
+  unsigned long long* ws_cnt;   // [units] split arrival counters: (stamp << 32) | arrivals
+  uint32_t stamp;     // launch stamp (never 0)
   int32_t* ws_err;
   float* score_sums;  // [B][H][table_stride] or null
 };
+
+// Arrival on a split counter whose word holds (launch stamp << 32) | count.
+// A word with another stamp is a leftover of an earlier launch, or bytes of
+// another shape's layout of the shared workspace, and counts as zero: the
+// counters need no reset between launches.  Returns the arrivals before this
+// one in this launch.  The caller has waited for its partial's stores.
+__device__ __forceinline__ int arrive_stamped(unsigned long long* c, uint32_t stamp) {
+  unsigned long long old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (true) {
+    const bool fresh = uint32_t(old >> 32) == stamp;
+    const uint32_t before = fresh ? uint32_t(old) : 0u;
+    const unsigned long long nv = (static_cast<unsigned long long>(stamp) << 32) | (before + 1u);
+    if (__hip_atomic_compare_exchange_strong(c, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      return int(before);
+  }
+}
 
 __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
   int nb = p.num_blocks;
@@ -776,7 +795,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(p.ws_cnt + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int prev = arrive_stamped(p.ws_cnt + unit, p.stamp);
     s_last = (prev == splits - 1) ? 1 : 0;
   }
   __syncthreads();
@@ -816,7 +835,6 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
           block_score<COLD_ZERO>(p, b, kvh * G + h, blk, nb, M, L);
     }
   }
-  if (tid == 0) __hip_atomic_store(p.ws_cnt + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // --------------------------------------------------------------------------
@@ -1008,7 +1026,7 @@ static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks
     const Plan pl = plan_launch(batch, kv_heads, num_blocks, groups, splits_hint);
     const int64_t units = int64_t(batch) * kv_heads;
     l.cnt = off;
-    off = up(off + units * 4);
+    off = up(off + units * 8);
     l.acc = off;
     if (pl.splits > 1) off = up(off + units * pl.splits * groups * head_dim * 4);
     l.ml = off;
@@ -1147,7 +1165,7 @@ extern "C" int32_t tierkv_decode_attention(
   p.scale_log2 = scaling * LOG2E;
   char* ws = reinterpret_cast<char*>(workspace);
   p.ws_err = reinterpret_cast<int32_t*>(ws + wl.err);
-  p.ws_cnt = reinterpret_cast<int32_t*>(ws + wl.cnt);
+  p.ws_cnt = reinterpret_cast<unsigned long long*>(ws + wl.cnt);
   p.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
   p.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   p.ws_stage = reinterpret_cast<float*>(ws + wl.stage);
@@ -1166,6 +1184,12 @@ extern "C" int32_t tierkv_decode_attention(
     }
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, p.groups, splits_hint);
     p.splits = pl.splits;
+    // Launch stamp: a bijection of the launch count (odd multiplier mod 2^32),
+    // never 0; the split counters carry it.
+    static std::atomic<uint32_t> launches{0};
+    uint32_t c = launches.fetch_add(1) + 1;
+    if (c == 0) c = launches.fetch_add(1) + 1;
+    p.stamp = c * 0x9E3779B1u;
     const int64_t grid = int64_t(batch) * num_kv_heads * pl.splits;
     if (grid > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
     if (bf16) dispatch_fast<__hip_bfloat16>(p, warm_format, scores, cz, pl.nw, int(grid), stream);

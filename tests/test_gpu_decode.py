@@ -95,9 +95,13 @@ def test_split_invariance(device, splits):
     case = W.make_tiered_case("splits", 2, 32, 8, 128, 100, 12, 60, seed=7)
     out_auto = _check(case, "absmax_i8", device)[0]
     out_s = _check(case, "absmax_i8", device, splits=splits)[0]
-    # Equal up to fp32 re-association and the fp16 rounding of the output:
-    # two fp16 ulps (2^-9 relative) plus a small absolute floor.
-    assert_close(out_s.float().cpu().numpy(), out_auto.float().cpu().numpy(), atol=1e-4, rtol=2.0 ** -9,
+    # Both match the oracle above.  Between themselves they differ by fp32
+    # re-association, the fp16 rounding of the output, and the fp16 rounding
+    # of the probabilities the PV product uses, which are taken relative to
+    # each wave's running maximum and so depend on how tiles are partitioned
+    # (splits, dynamic hand-out, work sharing): 2^-11 relative per
+    # probability, about 2^-11 * max|V| (~4) in the worst case per output.
+    assert_close(out_s.float().cpu().numpy(), out_auto.float().cpu().numpy(), atol=5e-4, rtol=2.0 ** -9,
                  what="split vs auto")
 
 
@@ -182,3 +186,19 @@ def test_reference_preservation_geometry(device, states):
     assert_close(sc.cpu().numpy()[None], exp_sc, what="1-D table scores")
     out2, none = tierkv_decode_attention(**args, return_scores=False)
     assert none is None and out2.shape == (1, 1, 8, 64)
+
+
+# -- workspace reuse ------------------------------------------------------------
+
+def test_workspace_reuse_across_shapes(device):
+    # The per-device workspace is shared by launches of every shape; split
+    # launches (several workgroups per unit, arrival counters stamped per
+    # launch) and score launches are interleaved with single-split ones: no
+    # launch may depend on what another layout left in the workspace.
+    big = W.make_tiered_case("reuse_big", 16, 32, 8, 128, 64, 6, 40, seed=31)
+    small = W.make_tiered_case("reuse_small", 3, 16, 4, 128, 48, 4, 30, seed=32)
+    split = W.make_tiered_case("reuse_split", 2, 32, 8, 128, 100, 12, 60, seed=33)
+    for case, kw in ((big, {}), (small, {}), (split, {}), (big, {"return_scores": True}),
+                     (split, {"return_scores": True}), (small, {"return_scores": True}),
+                     (split, {"splits": 3}), (big, {}), (split, {})):
+        _check(case, "absmax_i8", device, seqs=[0, case.batch - 1], **kw)
