@@ -176,10 +176,12 @@ __device__ __forceinline__ void load_hot(const DecodeParams& p, int kvh, int slo
   const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;   // first token row of the tile
   const auto rk = tile_rsrc(p.hot_k + tile0 * D, live ? TILE : 0u);
   const auto rv = tile_rsrc(p.hot_v + tile0 * D, live ? TILE : 0u);
-  const int ko = (n * (D / 8) + g * (D / 32)) * 16;
+  // Instruction i reads bytes [64i, 64i + 64) of every row (whole lines);
+  // lane g's 16 bytes are dims 32i + 8g .. +7 (the query's HOT permutation).
+  const int ko = n * (D * 2) + 16 * g;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
-    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * i, 0, TILE_CPOL);
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64 * i, 0, TILE_CPOL);
     t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
   }
 #pragma unroll
@@ -505,12 +507,14 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   const int g = lane >> 4;
   const bool head_ok = n < G;
   const int qh = kvh * G + (head_ok ? n : 0);
-  uint4 qraw[D / 32];
+  uint4 qraw[D / 32], qraw_h[D / 32];
   {
-    const uint4* qp = reinterpret_cast<const uint4*>(reinterpret_cast<const QT*>(a_q) +
-                                                     (int64_t(b) * p.num_heads + qh) * D + g * (D / 4));
+    const QT* qrow = reinterpret_cast<const QT*>(a_q) + (int64_t(b) * p.num_heads + qh) * D;
+    const uint4* qp = reinterpret_cast<const uint4*>(qrow + g * (D / 4));
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) qraw[i] = qp[i];
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) qraw_h[i] = *reinterpret_cast<const uint4*>(qrow + 32 * i + 8 * g);
   }
 
   // ---- this workgroup's share of the resident blocks ------------------------
@@ -587,24 +591,29 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   const int nwarm = uniform((seen_warm > split) ? (seen_warm - split + splits - 1) / splits : 0);
 
   // ---- query (fp16) and its per-head sum ------------------------------------
-  uint32_t qv[D / 8];
+  // qv: dims g*D/4 .. +D/4 (the WARM K permutation), qvh: dims 32i + 8g .. +7
+  // (the HOT K permutation); the same fp16 values in two orders.
+  uint32_t qv[D / 8], qvh[D / 8];
   float qsum = 0.f;
   {
+    auto to_f16x2 = [&](uint32_t wd) -> uint32_t {
+      uint32_t h2;
+      if constexpr (std::is_same<QT, __half>::value) {
+        h2 = wd;
+      } else {
+        h2 = pack_f16x2(__uint_as_float(wd << 16), __uint_as_float(wd & 0xffff0000u));
+      }
+      return head_ok ? h2 : 0u;
+    };
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) {
       const uint32_t wd[4] = {qraw[i].x, qraw[i].y, qraw[i].z, qraw[i].w};
+      const uint32_t wh[4] = {qraw_h[i].x, qraw_h[i].y, qraw_h[i].z, qraw_h[i].w};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        uint32_t h2;
-        if constexpr (std::is_same<QT, __half>::value) {
-          h2 = wd[k];
-        } else {
-          const float a = __uint_as_float(wd[k] << 16);
-          const float c = __uint_as_float(wd[k] & 0xffff0000u);
-          h2 = pack_f16x2(a, c);
-        }
-        h2 = head_ok ? h2 : 0u;
+        const uint32_t h2 = to_f16x2(wd[k]);
         qv[4 * i + k] = h2;
+        qvh[4 * i + k] = to_f16x2(wh[k]);
         qsum += half_lo(h2) + half_hi(h2);
       }
     }
@@ -702,7 +711,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         hne = s_list[min(gi, nhot - 1)];
         hnl = gi < nhot;
         if (lh[k])
-          process_hot<D, SCORES>(p, th[k], uniform(eh[k].x), uniform(eh[k].z), lane, head_ok, b, qh, qv, st);
+          process_hot<D, SCORES>(p, th[k], uniform(eh[k].x), uniform(eh[k].z), lane, head_ok, b, qh, qvh, st);
       }
     } while (lh[0]);
   }
