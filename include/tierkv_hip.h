@@ -134,6 +134,63 @@ TIERKV_API int32_t tierkv_promote_to_hot(
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* KV append into HOT slots.  Replaces the tensor copies of write_hot_tokens
+ * (tierkv_policy.py:934-967; dense pool 238-267): job i copies tokens
+ * [src_tok[i], src_tok[i] + count[i]) of sequence src_seq[i] of the fp16
+ * sources src_k/src_v [src_seqs, kv_heads, src_tokens, head_dim] into HOT
+ * slot dst_slot[i] at rows [dst_pos[i], dst_pos[i] + count[i]); with
+ * zero_tail the slot's rows past the written range are zeroed, as the
+ * reference does.  Jobs whose ranges fall outside their tensors are skipped. */
+TIERKV_API int32_t tierkv_write_hot_tokens(
+    const void* src_k, const void* src_v, int64_t src_seqs, int32_t src_tokens,
+    const int32_t* src_seq, const int32_t* src_tok, const int32_t* count,
+    const int32_t* dst_slot, const int32_t* dst_pos, int32_t n, int32_t zero_tail,
+    void* hot_k, void* hot_v, int64_t hot_slots,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
+/* Batched runtime (one layer of B sequences whose tables live on the device).
+ * Free-slot stacks: int32 [capacity] arrays whose first `top` entries are free
+ * slots; ctl is int32 [4] = {hot_top, warm_top, error bits, 0}.  Error bits:
+ * 1 no free HOT slot, 2 no free WARM slot, 4 a table row is full, 8 a
+ * sequence's last block was not HOT. */
+
+/* Append `tokens` new tokens per sequence from src_k/src_v [batch, kv_heads,
+ * tokens, head_dim] fp16 at the end of each sequence's block list: the open
+ * (last, HOT, not full) block first, then new HOT blocks popped from hot_free
+ * in sequence order (deterministic slot ids).  seq_num_blocks [batch] and the
+ * table rows are updated on the device.  All-or-nothing when slots run out.
+ * The per-step part of append_to_layer (tierkv_policy.py:1768-1816) for a
+ * batch of sequences, without host involvement. */
+TIERKV_API int32_t tierkv_runtime_append(
+    const void* src_k, const void* src_v, int32_t tokens,
+    int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
+    int32_t* seq_num_blocks, int32_t batch,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
+/* One policy tick for one layer, entirely on the device: block scores from the
+ * decode kernel's probability sums (block_scores_from_probability_sums,
+ * tierkv_policy.py:1905-1912), stable-rank tier labels with reserved HOT
+ * {0, n-1} and sticky COLD (enforce_budget mode 1 / enforce_tiered_budget
+ * mode 2, 1391-1477), slot allocation (pops before pushes, in (sequence,
+ * block) order) and the demote / promote data movement (sync_storage_states,
+ * 1849-1867).  A migration that finds no free slot leaves its block as it is
+ * and sets an error bit.  scratch: at least
+ * tierkv_runtime_tick_scratch_bytes(...) bytes. */
+TIERKV_API int32_t tierkv_runtime_tick(
+    const float* score_sums, int64_t sums_stride, int32_t num_heads,
+    int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
+    const int32_t* seq_num_blocks, int32_t batch, int32_t hot_budget, int32_t warm_budget, int32_t mode,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free,
+    void* warm_k, void* warm_v, int64_t warm_slots, int32_t* warm_free,
+    void* k_scale, void* k_zero, void* v_scale, void* v_zero, int32_t warm_format,
+    int32_t* ctl, void* scratch, int64_t scratch_bytes, int32_t max_demotions, int32_t max_promotions,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
+TIERKV_API int64_t tierkv_runtime_tick_scratch_bytes(int32_t batch, int64_t table_stride,
+                                                      int32_t max_demotions, int32_t max_promotions);
+
+/* ---------------------------------------------------------------------- */
 /* Block scores.  Per-block probability mass from softmax probabilities
  * probs fp32 [batch, num_heads, tokens] -> out fp32 [batch, tokens/block_size]:
  * sequential sum over heads, pairwise tree over the block's tokens, / heads,

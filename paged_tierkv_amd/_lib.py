@@ -65,6 +65,28 @@ SIGNATURES = {
         _P, _P, c_int64, c_int32,
         _P, _P, _P,
         c_int32, c_int32, c_int32, _P]),
+    "tierkv_write_hot_tokens": (c_int32, [
+        _P, _P, c_int64, c_int32,
+        _P, _P, _P,
+        _P, _P, c_int32, c_int32,
+        _P, _P, c_int64,
+        c_int32, c_int32, c_int32, _P]),
+    "tierkv_runtime_append": (c_int32, [
+        _P, _P, c_int32,
+        _P, _P, _P, c_int64,
+        _P, c_int32,
+        _P, _P, c_int64, _P, _P,
+        c_int32, c_int32, c_int32, _P]),
+    "tierkv_runtime_tick": (c_int32, [
+        _P, c_int64, c_int32,
+        _P, _P, _P, c_int64,
+        _P, c_int32, c_int32, c_int32, c_int32,
+        _P, _P, c_int64, _P,
+        _P, _P, c_int64, _P,
+        _P, _P, _P, _P, c_int32,
+        _P, _P, c_int64, c_int32, c_int32,
+        c_int32, c_int32, c_int32, _P]),
+    "tierkv_runtime_tick_scratch_bytes": (c_int64, [c_int32, c_int64, c_int32, c_int32]),
     "tierkv_block_mass_from_probs": (c_int32, [_P, _P, _P, c_int32, c_int32, c_int32, c_int32, _P]),
     "tierkv_block_scores_from_sums": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int32, c_int32, c_int32, _P]),
     "tierkv_tier_labels": (c_int32, [_P, _P, _P, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, _P]),

@@ -41,6 +41,7 @@ HIP_SOURCES = {
                              "-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
+    "runtime.hip": ["-ffp-contract=off"],
 }
 CXX_SOURCES = ["block_manager.cpp"]
 

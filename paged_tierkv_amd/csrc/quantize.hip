@@ -11,7 +11,7 @@
 // with __float2half_rn, divide with IEEE __fdiv_rn and round with rintf
 // (half to even).  This file is compiled with -ffp-contract=off.
 
-#include "tierkv_common.h"
+#include "quantize.h"
 
 namespace tierkv {
 
@@ -31,26 +31,13 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return r;
 }
 
-struct QuantJobs {
-  const __half* src[2];      // K, V source tiles [src_tiles, H_kv, bs, D]
-  int64_t src_tiles;
-  const int32_t* src_index;
-  const int32_t* dst_slot;
-  const int32_t* lengths;
-  void* warm[2];
-  int64_t warm_slots;
-  void* scale[2];
-  void* zero[2];
-  int32_t* table;
-  int32_t* states;
-  const int32_t* table_pos;
-  int32_t kv_heads, bs, D, pad_tail;
-};
+
 
 // ABSMAX_I8: one workgroup per (job, kv head, K|V) tile.
 __global__ __launch_bounds__(QT) void demote_absmax_kernel(QuantJobs q) {
   __shared__ float red[QT / 64];
   const int job = blockIdx.x;
+  if (q.n_dev && job >= *q.n_dev) return;
   const int h = blockIdx.y;
   const int kv = blockIdx.z;
   const int64_t si = q.src_index[job];
@@ -91,6 +78,7 @@ __global__ __launch_bounds__(QT) void demote_absmax_kernel(QuantJobs q) {
 __global__ __launch_bounds__(QT) void demote_absmax_vec_kernel(QuantJobs q) {
   __shared__ float red[QT / 64];
   const int job = blockIdx.x;
+  if (q.n_dev && job >= *q.n_dev) return;
   const int h = blockIdx.y;
   const int kv = blockIdx.z;
   const int64_t si = q.src_index[job];
@@ -161,6 +149,7 @@ __global__ __launch_bounds__(QT) void demote_absmax_vec_kernel(QuantJobs q) {
 // per (token, head) row; one workgroup per (job, kv head, K|V) tile.
 __global__ __launch_bounds__(QT) void demote_ref_kernel(QuantJobs q) {
   const int job = blockIdx.x;
+  if (q.n_dev && job >= *q.n_dev) return;
   const int h = blockIdx.y;
   const int kv = blockIdx.z;
   const int64_t si = q.src_index[job];
@@ -224,26 +213,13 @@ __global__ __launch_bounds__(QT) void demote_ref_kernel(QuantJobs q) {
   }
 }
 
-struct DequantJobs {
-  const void* warm[2];
-  int64_t warm_slots;
-  const void* scale[2];
-  const void* zero[2];
-  const int32_t* src_slot;
-  const int32_t* dst_slot;
-  const int32_t* lengths;
-  __half* hot[2];
-  int64_t hot_slots;
-  int32_t* table;
-  int32_t* states;
-  const int32_t* table_pos;
-  int32_t kv_heads, bs, D, warm_format;
-};
+
 
 // promote_to_hot: dequantize the first `length` tokens of a WARM slot into
 // a HOT slot (dequantize_int8_to_fp16, tierkv_policy.py:39-44).
 __global__ __launch_bounds__(QT) void promote_kernel(DequantJobs q) {
   const int job = blockIdx.x;
+  if (q.n_dev && job >= *q.n_dev) return;
   const int h = blockIdx.y;
   const int kv = blockIdx.z;
   const int64_t si = q.src_slot[job];
@@ -276,6 +252,30 @@ __global__ __launch_bounds__(QT) void promote_kernel(DequantJobs q) {
       q.states[pos] = HOT;
     }
   }
+}
+
+int32_t launch_demote(const QuantJobs& q, int n_grid, int32_t warm_format, hipStream_t stream) {
+  if (n_grid <= 0) return TIERKV_OK;
+  dim3 grid(n_grid, q.kv_heads, 2);
+  if (warm_format == TIERKV_WARM_ABSMAX_I8) {
+    const bool vec = (q.D % 8 == 0) && aligned16(q.src[0]) && aligned16(q.src[1]) &&
+                     (reinterpret_cast<uintptr_t>(q.warm[0]) % 8 == 0) &&
+                     (reinterpret_cast<uintptr_t>(q.warm[1]) % 8 == 0);
+    if (vec) hipLaunchKernelGGL(demote_absmax_vec_kernel, grid, dim3(QT), 0, stream, q);
+    else hipLaunchKernelGGL(demote_absmax_kernel, grid, dim3(QT), 0, stream, q);
+    return check_launch("demote_absmax_kernel");
+  }
+  if (warm_format == TIERKV_WARM_REF_U8) {
+    hipLaunchKernelGGL(demote_ref_kernel, grid, dim3(QT), 0, stream, q);
+    return check_launch("demote_ref_kernel");
+  }
+  return fail(TIERKV_ERR_INVALID, "unknown warm format");
+}
+
+int32_t launch_promote(const DequantJobs& q, int n_grid, hipStream_t stream) {
+  if (n_grid <= 0) return TIERKV_OK;
+  hipLaunchKernelGGL(promote_kernel, dim3(n_grid, q.kv_heads, 2), dim3(QT), 0, stream, q);
+  return check_launch("promote_kernel");
 }
 
 }  // namespace tierkv
@@ -321,20 +321,9 @@ extern "C" int32_t tierkv_demote_to_warm(
   q.bs = block_size;
   q.D = head_dim;
   q.pad_tail = pad_tail;
-  dim3 grid(n, num_kv_heads, 2);
-  if (warm_format == TIERKV_WARM_ABSMAX_I8) {
-    const bool vec = (head_dim % 8 == 0) && aligned16(src_k) && aligned16(src_v) &&
-                     (reinterpret_cast<uintptr_t>(warm_k) % 8 == 0) && (reinterpret_cast<uintptr_t>(warm_v) % 8 == 0);
-    if (vec) hipLaunchKernelGGL(demote_absmax_vec_kernel, grid, dim3(QT), 0, stream, q);
-    else hipLaunchKernelGGL(demote_absmax_kernel, grid, dim3(QT), 0, stream, q);
-    return check_launch("demote_absmax_kernel");
-  }
-  if (warm_format == TIERKV_WARM_REF_U8) {
-    if (!k_zero || !v_zero) return fail(TIERKV_ERR_INVALID, "reference format needs zero-point pools");
-    hipLaunchKernelGGL(demote_ref_kernel, grid, dim3(QT), 0, stream, q);
-    return check_launch("demote_ref_kernel");
-  }
-  return fail(TIERKV_ERR_INVALID, "unknown warm format");
+  if (warm_format == TIERKV_WARM_REF_U8 && (!k_zero || !v_zero))
+    return fail(TIERKV_ERR_INVALID, "reference format needs zero-point pools");
+  return launch_demote(q, n, warm_format, stream);
 }
 
 extern "C" int32_t tierkv_promote_to_hot(
@@ -379,6 +368,5 @@ extern "C" int32_t tierkv_promote_to_hot(
   q.bs = block_size;
   q.D = head_dim;
   q.warm_format = warm_format;
-  hipLaunchKernelGGL(promote_kernel, dim3(n, num_kv_heads, 2), dim3(QT), 0, stream, q);
-  return check_launch("promote_kernel");
+  return launch_promote(q, n, stream);
 }

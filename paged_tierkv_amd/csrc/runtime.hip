@@ -1,0 +1,606 @@
+// Runtime kernels of the tiered KV cache on gfx950: KV append into HOT slots,
+// device-side slot allocation and the device-side policy tick.
+//
+// Replaces, for the path's storage side:
+//   * write_hot_tokens (tierkv_policy.py:934-967, dense 238-267): token
+//     ranges copied into HOT slots, the rest of a written block zeroed;
+//   * append_to_layer's per-step append (tierkv_policy.py:1768-1816) for a
+//     batch of sequences, with new HOT blocks taken from a device free stack;
+//   * one policy tick per layer: block_scores_from_probability_sums
+//     (1905-1912), enforce_budget / enforce_tiered_budget (1391-1477) and
+//     sync_storage_states (1849-1867) -- block scores, stable-rank labels,
+//     slot allocation and the demote / promote data movement, with no host
+//     round trip.
+//
+// Free stacks: int32 [capacity] arrays whose first `top` entries are free
+// slots; the top counters live in a per-layer control word array
+// ctl = {hot_top, warm_top, error bits, 0}.  Allocation pops from the top in
+// a fixed order (sequence, then logical block), so slot ids are deterministic.
+
+#include "quantize.h"
+
+namespace tierkv {
+
+constexpr int RT = 1024;          // threads of the single-workgroup bookkeeping kernels
+constexpr int CT = 256;           // threads per copy workgroup
+
+// Error bits in ctl[2].
+constexpr int ERR_HOT_EMPTY = 1;     // no free HOT slot for a new block or a promotion
+constexpr int ERR_WARM_EMPTY = 2;    // no free WARM slot for a demotion
+constexpr int ERR_TABLE_FULL = 4;    // a sequence exceeded its table row
+constexpr int ERR_OPEN_STATE = 8;    // the last block of a sequence was not HOT
+
+// Inclusive block-wide prefix sum of v over RT threads; returns the sum of
+// all threads' values in *total.
+__device__ int block_scan(int v, int* sh, int* total) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  if (lane == 63) sh[w] = x;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int i = 0; i < RT / 64; ++i) {
+      const int t = sh[i];
+      sh[i] = run;
+      run += t;
+    }
+    sh[RT / 64] = run;
+  }
+  __syncthreads();
+  x += sh[w];
+  *total = sh[RT / 64];
+  __syncthreads();
+  return x;
+}
+
+// ---------------------------------------------------------------------------
+// write_hot_tokens: job i copies tokens [src_tok, src_tok + count) of sequence
+// src_seq of src [S, kv_heads, T, D] into HOT slot dst_slot at positions
+// [dst_pos, dst_pos + count); with zero_tail the block's positions past the
+// written range are zeroed (tierkv_policy.py:955-960).
+// ---------------------------------------------------------------------------
+struct CopyJobs {
+  const __half* src[2];
+  int64_t src_seqs;
+  int32_t src_tokens;
+  const int32_t* src_seq;
+  const int32_t* src_tok;
+  const int32_t* count;
+  const int32_t* dst_slot;
+  const int32_t* dst_pos;
+  __half* hot[2];
+  int64_t hot_slots;
+  int32_t kv_heads, bs, D, zero_tail;
+};
+
+__global__ __launch_bounds__(CT) void write_hot_kernel(CopyJobs c) {
+  const int job = blockIdx.x;
+  const int h = blockIdx.y;
+  const int kv = blockIdx.z;
+  const int64_t sq = c.src_seq[job];
+  const int64_t slot = c.dst_slot[job];
+  const int t0 = c.src_tok[job];
+  const int n = c.count[job];
+  const int p0 = c.dst_pos[job];
+  if (sq < 0 || sq >= c.src_seqs || slot < 0 || slot >= c.hot_slots) return;
+  if (n < 0 || t0 < 0 || t0 + n > c.src_tokens || p0 < 0 || p0 + n > c.bs) return;
+  const int D = c.D;
+  const __half* src = c.src[kv] + ((sq * c.kv_heads + h) * int64_t(c.src_tokens) + t0) * D;
+  __half* dst = c.hot[kv] + ((slot * c.kv_heads + h) * int64_t(c.bs) + p0) * D;
+  const int end = c.zero_tail ? (c.bs - p0) * D : n * D;   // elements from dst
+  const int copy = n * D;
+  if ((D & 7) == 0 && ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15u) == 0) {
+    const uint4* s4 = reinterpret_cast<const uint4*>(src);
+    uint4* d4 = reinterpret_cast<uint4*>(dst);
+    for (int e = threadIdx.x; e < end / 8; e += CT)
+      d4[e] = (e < copy / 8) ? s4[e] : make_uint4(0u, 0u, 0u, 0u);
+  } else {
+    for (int e = threadIdx.x; e < end; e += CT) dst[e] = (e < copy) ? src[e] : __float2half(0.f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Batched append: every sequence appends the same T tokens-count from
+// src [B, kv_heads, T, D] at the end of its block list.  The open (last,
+// HOT, not full) block is filled first; further tokens go to new HOT blocks
+// popped from the free stack in sequence order.  All-or-nothing: if the
+// stack cannot cover every new block, nothing is appended and ERR_HOT_EMPTY
+// is set.  One workgroup; meant for decode steps (a few tokens per
+// sequence): B * 2 * kv_heads * T * D / 8 must stay below 2^31.
+// ---------------------------------------------------------------------------
+struct AppendParams {
+  const __half* src[2];
+  int32_t T;
+  int32_t* table;
+  int32_t* states;
+  int32_t* lengths;
+  int64_t stride;
+  int32_t* nblocks;
+  __half* hot[2];
+  int64_t hot_slots;
+  int32_t* hot_free;
+  int32_t* ctl;
+  int32_t batch, kv_heads, bs, D;
+};
+
+constexpr int APPEND_MAX_BATCH = 4096;   // sequences per append call (LDS bookkeeping)
+
+__global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
+  __shared__ int sh[RT / 64 + 1];
+  __shared__ int s_ok;
+  __shared__ int s_fb[APPEND_MAX_BATCH];   // first block receiving a token, per sequence
+  __shared__ int s_fp[APPEND_MAX_BATCH];   // row of the first new token in it
+  const int tid = threadIdx.x;
+  const int B = a.batch, bs = a.bs, T = a.T;
+  // The open block (last, HOT, not full) of sequence b: its free rows.
+  auto open_room = [&](int b, int nb, int& len_open) {
+    len_open = 0;
+    if (nb <= 0) return 0;
+    const int64_t o = int64_t(b) * a.stride + nb - 1;
+    const int len = min(max(a.lengths[o], 0), bs);
+    if (a.states[o] != HOT) {
+      if (len < bs) atomicOr(a.ctl + 2, ERR_OPEN_STATE);
+      return 0;
+    }
+    len_open = len;
+    return bs - len;
+  };
+  // Phase 1: new blocks needed in total (all-or-nothing check).
+  if (tid == 0) s_ok = 1;
+  __syncthreads();
+  int run = 0;
+  for (int b0 = 0; b0 < B; b0 += RT) {
+    const int b = b0 + tid;
+    int need = 0;
+    if (b < B) {
+      const int nb = a.nblocks[b];
+      int len_open;
+      const int room = open_room(b, nb, len_open);
+      need = T > room ? (T - room + bs - 1) / bs : 0;
+      if (nb < 0 || nb + need > a.stride) s_ok = 0;
+    }
+    int tot;
+    block_scan(need, sh, &tot);
+    run += tot;
+  }
+  __syncthreads();
+  const int top = a.ctl[0];
+  if (!s_ok) {
+    if (tid == 0) atomicOr(a.ctl + 2, ERR_TABLE_FULL);
+    return;
+  }
+  if (run > top) {
+    if (tid == 0) atomicOr(a.ctl + 2, ERR_HOT_EMPTY);
+    return;
+  }
+  // Phase 2: table entries; new blocks pop the stack in sequence order.
+  int base = 0;
+  for (int b0 = 0; b0 < B; b0 += RT) {
+    const int b = b0 + tid;
+    int need = 0, nb = 0, room = 0, len_open = 0;
+    if (b < B) {
+      nb = a.nblocks[b];
+      room = open_room(b, nb, len_open);
+      need = T > room ? (T - room + bs - 1) / bs : 0;
+    }
+    int tot;
+    const int incl = block_scan(need, sh, &tot);
+    if (b < B) {
+      const int off = base + incl - need;
+      const int take_open = min(room, T);
+      if (take_open > 0) {
+        a.lengths[int64_t(b) * a.stride + nb - 1] = len_open + take_open;
+        s_fb[b] = nb - 1;
+        s_fp[b] = len_open;
+      } else {
+        s_fb[b] = nb;
+        s_fp[b] = 0;
+      }
+      for (int j = 0; j < need; ++j) {
+        const int64_t o = int64_t(b) * a.stride + nb + j;
+        a.table[o] = a.hot_free[top - 1 - (off + j)];
+        a.states[o] = HOT;
+        a.lengths[o] = min(T - take_open - j * bs, bs);
+      }
+      a.nblocks[b] = nb + need;
+    }
+    base += tot;
+  }
+  __syncthreads();
+  if (tid == 0) a.ctl[0] = top - run;
+  // Phase 3: copy the new tokens.  Token t of sequence b lands at row
+  // fp + t counted from row 0 of its first touched block.  Rows past a
+  // block's length are not cleared: pools start zeroed and only ever hold
+  // finite fp16 values, and every consumer masks rows by length.
+  const int D = a.D, C = D / 8;
+  const int H = a.kv_heads;
+  const int per_seq = 2 * H * T * C;
+  const int total = B * per_seq;
+  for (int e = tid; e < total; e += RT) {
+    const int b = e / per_seq;
+    int r = e - b * per_seq;
+    const int c = r % C;
+    r /= C;
+    const int t = r % T;
+    r /= T;
+    const int h = r % H;
+    const int kv = r / H;
+    const int g = s_fp[b] + t;
+    const int tb = s_fb[b] + g / bs;
+    const int64_t slot = a.table[int64_t(b) * a.stride + tb];
+    if (slot < 0 || slot >= a.hot_slots) continue;
+    uint4* dst = reinterpret_cast<uint4*>(a.hot[kv] + ((slot * H + h) * int64_t(bs) + g % bs) * D) + c;
+    *dst = reinterpret_cast<const uint4*>(a.src[kv] + ((int64_t(b) * H + h) * T + t) * D)[c];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Policy tick for one layer of a batch of sequences.
+// ---------------------------------------------------------------------------
+struct TickParams {
+  const float* score_sums;   // [B, heads, sums_stride]
+  int64_t sums_stride;
+  int32_t heads;
+  int32_t* table;
+  int32_t* states;
+  int32_t* lengths;
+  int64_t stride;
+  const int32_t* nblocks;
+  int32_t batch;
+  int32_t hot_budget, warm_budget, mode;   // mode 1: demoted blocks WARM, 2: WARM budget then COLD
+  int32_t* hot_free;
+  int32_t* warm_free;
+  int32_t* ctl;
+  float* scores;      // [B, stride] scratch: block scores
+  int32_t* labels;    // [B, stride] scratch: desired states
+  int32_t* dem;       // [3][max_dem] demotion jobs (src hot slot, dst warm slot, length)
+  int32_t* pro;       // [3][max_pro] promotion jobs (src warm slot, dst hot slot, length)
+  int32_t* counts;    // [2] demotions, promotions
+  int32_t max_dem, max_pro;
+};
+
+__global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
+  __shared__ int sh[RT / 64 + 1];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int B = t.batch;
+  // 1. Block scores: mean over heads of the per-block probability sums,
+  //    divided by max(length, 1) (block_scores_from_probability_sums).
+  for (int b = 0; b < B; ++b) {
+    const int n = min(max(t.nblocks[b], 0), int(t.stride));
+    for (int i = tid; i < n; i += RT) {
+      // The same operations, in the same order, as tierkv_block_scores_from_sums.
+      float acc = 0.f;
+      for (int h = 0; h < t.heads; ++h) acc += t.score_sums[(int64_t(b) * t.heads + h) * t.sums_stride + i];
+      const float sm = __fdiv_rn(acc, float(t.heads));
+      const int len = max(t.lengths[int64_t(b) * t.stride + i], 1);
+      t.scores[int64_t(b) * t.stride + i] = __fdiv_rn(sm, float(len));
+    }
+  }
+  __syncthreads();
+  // 2. Labels, one wave per sequence: reserved HOT {0, n-1}, candidates
+  //    ranked by score descending with ties to the lower index (Python's
+  //    stable sort), COLD never leaves COLD.
+  for (int b = w; b < B; b += RT / 64) {
+    const int n = min(max(t.nblocks[b], 0), int(t.stride));
+    const float* sc = t.scores + int64_t(b) * t.stride;
+    const int64_t ob = int64_t(b) * t.stride;
+    const int extra_hot = max(t.hot_budget - 2, 0);
+    for (int i = lane; i < n; i += 64) {
+      const int cur = t.states[ob + i];
+      int want;
+      if (n <= 2 || i == 0 || i == n - 1) {
+        want = HOT;
+      } else {
+        const float si = sc[i];
+        int rank = 0;
+        for (int j = 1; j < n - 1; ++j) {
+          const float sj = sc[j];
+          rank += (sj > si || (sj == si && j < i)) ? 1 : 0;
+        }
+        if (rank < extra_hot) want = HOT;
+        else if (t.mode == 2) want = (rank < extra_hot + max(t.warm_budget, 0)) ? WARM : COLD;
+        else want = WARM;
+      }
+      if (cur == COLD) want = COLD;
+      t.labels[ob + i] = want;
+    }
+  }
+  __syncthreads();
+  // 3. Allocation in (sequence, block) order: pops first from the stacks as
+  //    they stand, pushes of the freed slots afterwards, so no slot is both
+  //    read and written by this tick's data movement.
+  const int hot_top = t.ctl[0];
+  const int warm_top = t.ctl[1];
+  int dem_run = 0, pro_run = 0;
+  int64_t N = 0;
+  for (int b = 0; b < B; ++b) N = max(N, int64_t(b) * t.stride + min(max(t.nblocks[b], 0), int(t.stride)));
+  for (int64_t e0 = 0; e0 < N; e0 += RT) {
+    const int64_t e = e0 + tid;
+    int d = 0, p = 0;
+    int b = 0, i = 0, cur = COLD, want = COLD;
+    if (e < N) {
+      b = int(e / t.stride);
+      i = int(e % t.stride);
+      const int n = min(max(t.nblocks[b], 0), int(t.stride));
+      if (i < n) {
+        cur = t.states[e];
+        want = t.labels[e];
+        d = (cur == HOT && want == WARM) ? 1 : 0;
+        p = (cur == WARM && want == HOT) ? 1 : 0;
+      }
+    }
+    int dt, pt;
+    const int dk = block_scan(d, sh, &dt) - d + dem_run;
+    const int pk = block_scan(p, sh, &pt) - p + pro_run;
+    if (d) {
+      if (dk < warm_top && dk < t.max_dem) {
+        const int slot = t.warm_free[warm_top - 1 - dk];
+        t.dem[dk] = t.table[e];
+        t.dem[t.max_dem + dk] = slot;
+        t.dem[2 * t.max_dem + dk] = t.lengths[e];
+      } else {
+        atomicOr(t.ctl + 2, ERR_WARM_EMPTY);
+      }
+    }
+    if (p) {
+      if (pk < hot_top && pk < t.max_pro) {
+        const int slot = t.hot_free[hot_top - 1 - pk];
+        t.pro[pk] = t.table[e];
+        t.pro[t.max_pro + pk] = slot;
+        t.pro[2 * t.max_pro + pk] = t.lengths[e];
+      } else {
+        atomicOr(t.ctl + 2, ERR_HOT_EMPTY);
+      }
+    }
+    dem_run += dt;
+    pro_run += pt;
+  }
+  const int ndem = min(min(dem_run, warm_top), t.max_dem);
+  const int npro = min(min(pro_run, hot_top), t.max_pro);
+  __syncthreads();
+  // Frees and table rewrite (second pass, same order).  A migration that got
+  // no slot leaves its block as it was.
+  int hf_run = 0, wf_run = 0;
+  dem_run = 0;
+  pro_run = 0;
+  for (int64_t e0 = 0; e0 < N; e0 += RT) {
+    const int64_t e = e0 + tid;
+    int d = 0, p = 0, fh = 0, fw = 0;
+    int cur = COLD, want = COLD, slot_now = -1;
+    if (e < N) {
+      const int b = int(e / t.stride);
+      const int i = int(e % t.stride);
+      const int n = min(max(t.nblocks[b], 0), int(t.stride));
+      if (i < n) {
+        cur = t.states[e];
+        want = t.labels[e];
+        slot_now = t.table[e];
+        d = (cur == HOT && want == WARM) ? 1 : 0;
+        p = (cur == WARM && want == HOT) ? 1 : 0;
+      }
+    }
+    int dt, pt;
+    const int dk = block_scan(d, sh, &dt) - d + dem_run;
+    const int pk = block_scan(p, sh, &pt) - p + pro_run;
+    const bool d_ok = d && dk < ndem;
+    const bool p_ok = p && pk < npro;
+    fh = (d_ok || (cur == HOT && want == COLD)) ? 1 : 0;
+    fw = (p_ok || (cur == WARM && want == COLD)) ? 1 : 0;
+    int fht, fwt;
+    const int fhk = block_scan(fh, sh, &fht) - fh + hf_run;
+    const int fwk = block_scan(fw, sh, &fwt) - fw + wf_run;
+    if (fh) t.hot_free[hot_top - npro + fhk] = slot_now;
+    if (fw) t.warm_free[warm_top - ndem + fwk] = slot_now;
+    if (d_ok) {
+      t.table[e] = t.dem[t.max_dem + dk];
+      t.states[e] = WARM;
+    } else if (p_ok) {
+      t.table[e] = t.pro[t.max_pro + pk];
+      t.states[e] = HOT;
+    } else if (want == COLD && cur != COLD) {
+      t.table[e] = -1;
+      t.states[e] = COLD;
+    }
+    dem_run += dt;
+    pro_run += pt;
+    hf_run += fht;
+    wf_run += fwt;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    t.ctl[0] = hot_top - npro + hf_run;
+    t.ctl[1] = warm_top - ndem + wf_run;
+    t.counts[0] = ndem;
+    t.counts[1] = npro;
+  }
+}
+
+}  // namespace tierkv
+
+using namespace tierkv;
+
+extern "C" int32_t tierkv_write_hot_tokens(
+    const void* src_k, const void* src_v, int64_t src_seqs, int32_t src_tokens,
+    const int32_t* src_seq, const int32_t* src_tok, const int32_t* count,
+    const int32_t* dst_slot, const int32_t* dst_pos, int32_t n, int32_t zero_tail,
+    void* hot_k, void* hot_v, int64_t hot_slots,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
+  clear_error();
+  if (n < 0) return fail(TIERKV_ERR_INVALID, "negative job count");
+  if (n == 0) return TIERKV_OK;
+  if (!src_k || !src_v || !src_seq || !src_tok || !count || !dst_slot || !dst_pos || !hot_k || !hot_v)
+    return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256 || src_tokens <= 0)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim in [1, 256]");
+  if (n > 65535 * 64) return fail(TIERKV_ERR_UNSUPPORTED, "too many copy jobs in one call");
+  CopyJobs c{};
+  c.src[0] = reinterpret_cast<const __half*>(src_k);
+  c.src[1] = reinterpret_cast<const __half*>(src_v);
+  c.src_seqs = src_seqs;
+  c.src_tokens = src_tokens;
+  c.src_seq = src_seq;
+  c.src_tok = src_tok;
+  c.count = count;
+  c.dst_slot = dst_slot;
+  c.dst_pos = dst_pos;
+  c.hot[0] = reinterpret_cast<__half*>(hot_k);
+  c.hot[1] = reinterpret_cast<__half*>(hot_v);
+  c.hot_slots = hot_slots;
+  c.kv_heads = num_kv_heads;
+  c.bs = block_size;
+  c.D = head_dim;
+  c.zero_tail = zero_tail;
+  hipLaunchKernelGGL(write_hot_kernel, dim3(n, num_kv_heads, 2), dim3(CT), 0,
+                     reinterpret_cast<hipStream_t>(stream), c);
+  return check_launch("write_hot_kernel");
+}
+
+extern "C" int32_t tierkv_runtime_append(
+    const void* src_k, const void* src_v, int32_t tokens,
+    int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
+    int32_t* seq_num_blocks, int32_t batch,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
+  clear_error();
+  if (!src_k || !src_v || !block_table || !block_states || !block_lengths || !seq_num_blocks || !hot_k ||
+      !hot_v || !hot_free || !ctl)
+    return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (batch <= 0 || tokens <= 0 || table_stride <= 0) return fail(TIERKV_ERR_INVALID, "empty append");
+  if (batch > APPEND_MAX_BATCH) return fail(TIERKV_ERR_UNSUPPORTED, "append supports at most 4096 sequences per call");
+  if (int64_t(batch) * 2 * num_kv_heads * tokens * (head_dim / 8) >= (int64_t(1) << 31))
+    return fail(TIERKV_ERR_UNSUPPORTED, "append too large for one call");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256 ||
+      head_dim % 8 != 0)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim a multiple of 8 up to 256");
+  if (!aligned16(src_k) || !aligned16(src_v) || !aligned16(hot_k) || !aligned16(hot_v))
+    return fail(TIERKV_ERR_INVALID, "KV sources and HOT pools must be 16-byte aligned");
+  AppendParams a{};
+  a.src[0] = reinterpret_cast<const __half*>(src_k);
+  a.src[1] = reinterpret_cast<const __half*>(src_v);
+  a.T = tokens;
+  a.table = block_table;
+  a.states = block_states;
+  a.lengths = block_lengths;
+  a.stride = table_stride;
+  a.nblocks = seq_num_blocks;
+  a.hot[0] = reinterpret_cast<__half*>(hot_k);
+  a.hot[1] = reinterpret_cast<__half*>(hot_v);
+  a.hot_slots = hot_slots;
+  a.hot_free = hot_free;
+  a.ctl = ctl;
+  a.batch = batch;
+  a.kv_heads = num_kv_heads;
+  a.bs = block_size;
+  a.D = head_dim;
+  hipLaunchKernelGGL(append_tokens_kernel, dim3(1), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("append_tokens_kernel");
+}
+
+extern "C" int32_t tierkv_runtime_tick(
+    const float* score_sums, int64_t sums_stride, int32_t num_heads,
+    int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
+    const int32_t* seq_num_blocks, int32_t batch, int32_t hot_budget, int32_t warm_budget, int32_t mode,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free,
+    void* warm_k, void* warm_v, int64_t warm_slots, int32_t* warm_free,
+    void* k_scale, void* k_zero, void* v_scale, void* v_zero, int32_t warm_format,
+    int32_t* ctl, void* scratch, int64_t scratch_bytes, int32_t max_demotions, int32_t max_promotions,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream_) {
+  clear_error();
+  if (!score_sums || !block_table || !block_states || !block_lengths || !seq_num_blocks || !hot_k || !hot_v ||
+      !hot_free || !warm_k || !warm_v || !warm_free || !k_scale || !v_scale || !ctl || !scratch)
+    return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (mode != 1 && mode != 2) return fail(TIERKV_ERR_INVALID, "tick mode must be 1 (hot_warm) or 2 (hot_warm_cold)");
+  if (warm_format == TIERKV_WARM_REF_U8 && (!k_zero || !v_zero))
+    return fail(TIERKV_ERR_INVALID, "reference format needs zero-point pools");
+  if (batch <= 0 || num_heads <= 0 || table_stride <= 0 || sums_stride < table_stride)
+    return fail(TIERKV_ERR_INVALID, "bad tick geometry");
+  if (max_demotions < 0 || max_promotions < 0 || max_demotions > 65535 * 64 || max_promotions > 65535 * 64)
+    return fail(TIERKV_ERR_INVALID, "bad job bounds");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim in [1, 256]");
+  const int64_t cells = int64_t(batch) * table_stride;
+  const int64_t need = cells * 8 + (int64_t(max_demotions) + max_promotions) * 12 + 16;
+  if (scratch_bytes < need) return fail(TIERKV_ERR_WORKSPACE, "tick scratch too small");
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  char* s = reinterpret_cast<char*>(scratch);
+  TickParams t{};
+  t.score_sums = score_sums;
+  t.sums_stride = sums_stride;
+  t.heads = num_heads;
+  t.table = block_table;
+  t.states = block_states;
+  t.lengths = block_lengths;
+  t.stride = table_stride;
+  t.nblocks = seq_num_blocks;
+  t.batch = batch;
+  t.hot_budget = hot_budget;
+  t.warm_budget = warm_budget;
+  t.mode = mode;
+  t.hot_free = hot_free;
+  t.warm_free = warm_free;
+  t.ctl = ctl;
+  t.scores = reinterpret_cast<float*>(s);
+  t.labels = reinterpret_cast<int32_t*>(s + cells * 4);
+  t.dem = reinterpret_cast<int32_t*>(s + cells * 8);
+  t.pro = t.dem + 3 * int64_t(max_demotions);
+  t.counts = t.pro + 3 * int64_t(max_promotions);
+  t.max_dem = max_demotions;
+  t.max_pro = max_promotions;
+  hipLaunchKernelGGL(tick_plan_kernel, dim3(1), dim3(RT), 0, stream, t);
+  int32_t rc = check_launch("tick_plan_kernel");
+  if (rc != TIERKV_OK) return rc;
+
+  QuantJobs q{};
+  q.src[0] = reinterpret_cast<const __half*>(hot_k);
+  q.src[1] = reinterpret_cast<const __half*>(hot_v);
+  q.src_tiles = hot_slots;
+  q.src_index = t.dem;
+  q.dst_slot = t.dem + max_demotions;
+  q.lengths = t.dem + 2 * int64_t(max_demotions);
+  q.warm[0] = warm_k;
+  q.warm[1] = warm_v;
+  q.warm_slots = warm_slots;
+  q.scale[0] = k_scale;
+  q.scale[1] = v_scale;
+  q.zero[0] = k_zero;
+  q.zero[1] = v_zero;
+  q.kv_heads = num_kv_heads;
+  q.bs = block_size;
+  q.D = head_dim;
+  q.pad_tail = 0;
+  q.n_dev = t.counts;
+  rc = launch_demote(q, max_demotions, warm_format, stream);
+  if (rc != TIERKV_OK) return rc;
+
+  DequantJobs d{};
+  d.warm[0] = warm_k;
+  d.warm[1] = warm_v;
+  d.warm_slots = warm_slots;
+  d.scale[0] = k_scale;
+  d.scale[1] = v_scale;
+  d.zero[0] = k_zero;
+  d.zero[1] = v_zero;
+  d.src_slot = t.pro;
+  d.dst_slot = t.pro + max_promotions;
+  d.lengths = t.pro + 2 * int64_t(max_promotions);
+  d.hot[0] = reinterpret_cast<__half*>(hot_k);
+  d.hot[1] = reinterpret_cast<__half*>(hot_v);
+  d.hot_slots = hot_slots;
+  d.kv_heads = num_kv_heads;
+  d.bs = block_size;
+  d.D = head_dim;
+  d.warm_format = warm_format;
+  d.n_dev = t.counts + 1;
+  return launch_promote(d, max_promotions, stream);
+}
+
+extern "C" int64_t tierkv_runtime_tick_scratch_bytes(int32_t batch, int64_t table_stride, int32_t max_demotions,
+                                                      int32_t max_promotions) {
+  if (batch <= 0 || table_stride <= 0 || max_demotions < 0 || max_promotions < 0) return -1;
+  return int64_t(batch) * table_stride * 8 + (int64_t(max_demotions) + max_promotions) * 12 + 16;
+}
