@@ -156,15 +156,19 @@ TIERKV_API int32_t tierkv_write_hot_tokens(
 
 /* Append `tokens` new tokens per sequence from src_k/src_v [batch, kv_heads,
  * tokens, head_dim] fp16 at the end of each sequence's block list: the open
- * (last, HOT, not full) block first, then new HOT blocks popped from hot_free
- * in sequence order (deterministic slot ids).  seq_num_blocks [batch] and the
- * table rows are updated on the device.  All-or-nothing when slots run out.
- * The per-step part of append_to_layer (tierkv_policy.py:1768-1816) for a
- * batch of sequences, without host involvement. */
+ * block first (the last block, when open_blocks[b] != 0), then new HOT blocks
+ * popped from hot_free in sequence order (deterministic slot ids).
+ * open_blocks [batch] is 1 while the last block was left partially filled by
+ * an append; a prefill sets it to 0, since the reference starts decode
+ * tokens in a new block (append_prefill_with_policy resets the open block,
+ * tierkv_policy.py:1764-1766).  seq_num_blocks, open_blocks and the table
+ * rows are updated on the device.  All-or-nothing when slots run out.  The
+ * per-step part of append_to_layer (tierkv_policy.py:1768-1816) for a batch
+ * of sequences, without host involvement. */
 TIERKV_API int32_t tierkv_runtime_append(
     const void* src_k, const void* src_v, int32_t tokens,
     int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
-    int32_t* seq_num_blocks, int32_t batch,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
 
@@ -189,6 +193,15 @@ TIERKV_API int32_t tierkv_runtime_tick(
 
 TIERKV_API int64_t tierkv_runtime_tick_scratch_bytes(int32_t batch, int64_t table_stride,
                                                       int32_t max_demotions, int32_t max_promotions);
+
+/* Table writes planned on the host: dst[pairs[2i]] = pairs[2i + 1] for
+ * i < n, positions distinct, out-of-range positions skipped; pairs is an
+ * 8-byte-aligned int32 device array.  Replaces the per-entry device writes of
+ * _set_metadata, set_block_entry, set_block_state and sync_gpu_block_tables
+ * (tierkv_policy.py:917-926, 1019-1040, 1164-1174; dense pool 269-290,
+ * 450-477), which the reference issues as one launch per table entry. */
+TIERKV_API int32_t tierkv_scatter_i32(int32_t* dst, int64_t dst_len, const int32_t* pairs, int32_t n,
+                                      void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Block scores.  Per-block probability mass from softmax probabilities

@@ -17,8 +17,13 @@ it follows.  Modules:
 * ``policy``        -- block scores, budget enforcement (tier labels), block
                        mass from probabilities.
 * ``block_manager`` -- the native BlockManager's allocation/state rules.
-* ``pools``         -- compact-pool slot bookkeeping (LIFO free lists) and the
-                       batched demotion plan.
+* ``runtime``       -- the batched runtime's allocation order and tick rules
+                       (per-sequence rules of the reference runtime; the
+                       batch-level order is this build's own).
+
+The reference-API pools and runtime (paged_tierkv_amd.tierkv_policy) have no
+restatement here: they are pinned directly against trajectories the
+reference runtime itself recorded (tests/golden/runtime_*.npz).
 
 How each function is pinned (reference known answers, golden vectors written
 by ``tests/golden/make_golden.py``, the compiled reference BlockManager in

@@ -6,7 +6,9 @@ Each sequence follows the reference runtime's rules (tierkv_policy.py):
   HOT blocks copied with a zeroed tail (write_hot_tokens, 934-967), WARM
   blocks quantized with a padded tail (write_warm_block, 969-1002), COLD
   blocks metadata only (register_cold_block, 1004-1014);
-* decode append: the open HOT block first, then new HOT blocks
+* decode append: the open block first -- the last block, while an earlier
+  append left it partially filled; a prefill leaves no open block
+  (append_prefill_with_policy resets it, 1764-1766) -- then new HOT blocks
   (append_to_layer, 1768-1816);
 * policy tick: block_scores_from_probability_sums (1905-1912), then
   enforce_budget / enforce_tiered_budget (1391-1477), then the storage moves
@@ -45,6 +47,7 @@ class BatchedRuntimeOracle:
         self.states = np.full((batch, max_blocks), COLD, np.int32)
         self.lengths = np.zeros((batch, max_blocks), np.int32)
         self.nb = np.zeros(batch, np.int32)
+        self.open = np.zeros(batch, bool)
         self.hot_k = np.zeros((hot_slots, kv_heads, block_size, head_dim), np.float16)
         self.hot_v = np.zeros_like(self.hot_k)
         if warm_format == "absmax_i8":
@@ -121,6 +124,7 @@ class BatchedRuntimeOracle:
                     self._quantize_into(nw, blk_k, blk_v, ln, pad_tail=True)
                     nw += 1
             self.nb[b] = n
+            self.open[b] = False
         self.hot_free = list(range(self.hot_slots - 1, nh - 1, -1))
         self.warm_free = list(range(self.warm_slots - 1, nw - 1, -1))
 
@@ -129,7 +133,7 @@ class BatchedRuntimeOracle:
         needs = []
         for b in range(self.B):
             n = int(self.nb[b])
-            open_ = n > 0 and self.states[b, n - 1] == HOT and self.lengths[b, n - 1] < self.bs
+            open_ = bool(self.open[b]) and n > 0 and self.states[b, n - 1] == HOT and self.lengths[b, n - 1] < self.bs
             needs.append(0 if open_ else 1)
         if sum(needs) > len(self.hot_free):
             raise RuntimeError("no free HOT slot")
@@ -148,11 +152,15 @@ class BatchedRuntimeOracle:
                 self.lengths[b, n - 1] = pos + 1
             self.hot_k[slot, :, pos] = k1[b, :, 0]
             self.hot_v[slot, :, pos] = v1[b, :, 0]
+            self.open[b] = self.lengths[b, int(self.nb[b]) - 1] < self.bs
 
-    def tick(self, score_sums, hot_budget, warm_budget):
-        """score_sums fp32 [B, H, >= n]; every sequence has the same n."""
+    def tick(self, score_sums, hot_budget, warm_budget, scores=None):
+        """score_sums fp32 [B, H, >= n]; every sequence has the same n.  Given
+        ``scores`` [B, n], they replace the block mass of the sums."""
         n = int(self.nb.max())
-        scores = block_mass_from_sums(score_sums, self.lengths, n)
+        if scores is None:
+            scores = block_mass_from_sums(score_sums, self.lengths, n)
+        scores = np.asarray(scores, np.float32)
         want = tier_labels(scores, self.states[:, :n], hot_budget, warm_budget, mode=self.mode)
         want = np.where(self.states[:, :n] == COLD, COLD, want)
         dem, pro = [], []

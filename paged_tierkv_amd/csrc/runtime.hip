@@ -106,12 +106,15 @@ __global__ __launch_bounds__(CT) void write_hot_kernel(CopyJobs c) {
 
 // ---------------------------------------------------------------------------
 // Batched append: every sequence appends the same T tokens-count from
-// src [B, kv_heads, T, D] at the end of its block list.  The open (last,
-// HOT, not full) block is filled first; further tokens go to new HOT blocks
-// popped from the free stack in sequence order.  All-or-nothing: if the
-// stack cannot cover every new block, nothing is appended and ERR_HOT_EMPTY
-// is set.  One workgroup; meant for decode steps (a few tokens per
-// sequence): B * 2 * kv_heads * T * D / 8 must stay below 2^31.
+// src [B, kv_heads, T, D] at the end of its block list.  The open block is
+// filled first: the last block, when open[b] says an earlier append left it
+// partially filled (a prefill leaves no open block, as append_prefill_with_
+// policy resets open_physical_idx, tierkv_policy.py:1764-1766).  Further
+// tokens go to new HOT blocks popped from the free stack in sequence order,
+// and open[b] records whether the new last block has room.  All-or-nothing:
+// if the stack cannot cover every new block, nothing is appended and
+// ERR_HOT_EMPTY is set.  One workgroup; meant for decode steps (a few tokens
+// per sequence): B * 2 * kv_heads * T * D / 8 must stay below 2^31.
 // ---------------------------------------------------------------------------
 struct AppendParams {
   const __half* src[2];
@@ -121,6 +124,7 @@ struct AppendParams {
   int32_t* lengths;
   int64_t stride;
   int32_t* nblocks;
+  int32_t* open;
   __half* hot[2];
   int64_t hot_slots;
   int32_t* hot_free;
@@ -137,10 +141,10 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
   __shared__ int s_fp[APPEND_MAX_BATCH];   // row of the first new token in it
   const int tid = threadIdx.x;
   const int B = a.batch, bs = a.bs, T = a.T;
-  // The open block (last, HOT, not full) of sequence b: its free rows.
+  // The open block of sequence b (flagged, last, HOT, not full): its free rows.
   auto open_room = [&](int b, int nb, int& len_open) {
     len_open = 0;
-    if (nb <= 0) return 0;
+    if (nb <= 0 || a.open[b] == 0) return 0;
     const int64_t o = int64_t(b) * a.stride + nb - 1;
     const int len = min(max(a.lengths[o], 0), bs);
     if (a.states[o] != HOT) {
@@ -208,6 +212,8 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
         a.lengths[o] = min(T - take_open - j * bs, bs);
       }
       a.nblocks[b] = nb + need;
+      const int last_len = need > 0 ? min(T - take_open - (need - 1) * bs, bs) : len_open + take_open;
+      a.open[b] = last_len < bs ? 1 : 0;
     }
     base += tot;
   }
@@ -420,9 +426,34 @@ __global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Host-planned table writes: dst[pairs[2i]] = pairs[2i + 1].  The host
+// coalesces its writes per position, so positions are distinct and the
+// launch order of the pairs does not matter.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(CT) void scatter_i32_kernel(int32_t* dst, int64_t len, const int32_t* pairs, int n) {
+  const int i = blockIdx.x * CT + threadIdx.x;
+  if (i >= n) return;
+  const int2 pv = reinterpret_cast<const int2*>(pairs)[i];
+  if (pv.x >= 0 && pv.x < len) dst[pv.x] = pv.y;
+}
+
 }  // namespace tierkv
 
 using namespace tierkv;
+
+extern "C" int32_t tierkv_scatter_i32(int32_t* dst, int64_t dst_len, const int32_t* pairs, int32_t n,
+                                      void* stream) {
+  clear_error();
+  if (n < 0) return fail(TIERKV_ERR_INVALID, "negative pair count");
+  if (n == 0) return TIERKV_OK;
+  if (!dst || !pairs) return fail(TIERKV_ERR_INVALID, "null pointer");
+  if ((reinterpret_cast<uintptr_t>(pairs) & 7u) != 0) return fail(TIERKV_ERR_INVALID, "pairs must be 8-byte aligned");
+  if (dst_len > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "scatter target above 2^31 entries");
+  hipLaunchKernelGGL(scatter_i32_kernel, dim3((n + CT - 1) / CT), dim3(CT), 0,
+                     reinterpret_cast<hipStream_t>(stream), dst, dst_len, pairs, n);
+  return check_launch("scatter_i32_kernel");
+}
 
 extern "C" int32_t tierkv_write_hot_tokens(
     const void* src_k, const void* src_v, int64_t src_seqs, int32_t src_tokens,
@@ -463,12 +494,12 @@ extern "C" int32_t tierkv_write_hot_tokens(
 extern "C" int32_t tierkv_runtime_append(
     const void* src_k, const void* src_v, int32_t tokens,
     int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
-    int32_t* seq_num_blocks, int32_t batch,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
   clear_error();
-  if (!src_k || !src_v || !block_table || !block_states || !block_lengths || !seq_num_blocks || !hot_k ||
-      !hot_v || !hot_free || !ctl)
+  if (!src_k || !src_v || !block_table || !block_states || !block_lengths || !seq_num_blocks || !open_blocks ||
+      !hot_k || !hot_v || !hot_free || !ctl)
     return fail(TIERKV_ERR_INVALID, "null pointer");
   if (batch <= 0 || tokens <= 0 || table_stride <= 0) return fail(TIERKV_ERR_INVALID, "empty append");
   if (batch > APPEND_MAX_BATCH) return fail(TIERKV_ERR_UNSUPPORTED, "append supports at most 4096 sequences per call");
@@ -488,6 +519,7 @@ extern "C" int32_t tierkv_runtime_append(
   a.lengths = block_lengths;
   a.stride = table_stride;
   a.nblocks = seq_num_blocks;
+  a.open = open_blocks;
   a.hot[0] = reinterpret_cast<__half*>(hot_k);
   a.hot[1] = reinterpret_cast<__half*>(hot_v);
   a.hot_slots = hot_slots;

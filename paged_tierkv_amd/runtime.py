@@ -98,6 +98,7 @@ class LayerStorage:
     states: torch.Tensor      # [B, max_blocks]
     lengths: torch.Tensor     # [B, max_blocks]
     nblocks: torch.Tensor     # [B]
+    open: torch.Tensor        # [B] 1 while the last block takes further appended tokens
     hot_free: torch.Tensor    # [hot capacity] free-slot stack
     warm_free: torch.Tensor   # [warm capacity]
     ctl: torch.Tensor         # [4] hot_top, warm_top, error bits, 0
@@ -149,6 +150,10 @@ class BatchedTieredKVRuntime:
         self.hot_slots = self.batch * self.hot_per_seq
         self.warm_slots = max(1, self.batch * self.warm_per_seq)
         self.layers = [self._new_layer() for _ in range(self.num_layers)]
+        # Host copy of the (lockstep) block count and open-block fill per layer,
+        # so launch sizes and budgets need no device read-back.
+        self._blocks = [0] * self.num_layers
+        self._open_tokens = [0] * self.num_layers
         self.seq_len = 0              # tokens per sequence (lockstep)
         self.decode_step = 0
         self.max_demotions = self.batch * self.hot_per_seq
@@ -185,6 +190,7 @@ class BatchedTieredKVRuntime:
             states=torch.full(tab, COLD_STATE, dtype=torch.int32, device=dev),
             lengths=torch.zeros(tab, dtype=torch.int32, device=dev),
             nblocks=torch.zeros(self.batch, dtype=torch.int32, device=dev),
+            open=torch.zeros(self.batch, dtype=torch.int32, device=dev),
             hot_free=torch.zeros(self.hot_slots, dtype=torch.int32, device=dev),
             warm_free=torch.zeros(self.warm_slots, dtype=torch.int32, device=dev),
             ctl=torch.zeros(4, dtype=torch.int32, device=dev))
@@ -255,6 +261,9 @@ class BatchedTieredKVRuntime:
         st.states.copy_(states)
         st.lengths.copy_(lengths)
         st.nblocks.fill_(n)
+        st.open.zero_()      # decode tokens start a new block (tierkv_policy.py:1764-1766)
+        self._blocks[layer] = n
+        self._open_tokens[layer] = 0
         # Free stacks: popping from the top yields the lowest free slot first.
         st.hot_free[: self.hot_slots - next_hot].copy_(
             torch.arange(self.hot_slots - 1, next_hot - 1, -1, dtype=torch.int32))
@@ -280,6 +289,20 @@ class BatchedTieredKVRuntime:
         _lib.check(rc, "tierkv_write_hot_tokens")
 
     # -- decode -------------------------------------------------------------
+
+    def _advance_blocks(self, layer: int, tokens: int) -> int:
+        """Mirror of the device append's block accounting (every sequence of
+        the batch appends the same count): returns the new block count."""
+        room = self.block_size - self._open_tokens[layer] if self._open_tokens[layer] else 0
+        take = min(room, tokens)
+        rest = tokens - take
+        if rest > 0:
+            self._blocks[layer] += _ceil_div(rest, self.block_size)
+            last = rest - (_ceil_div(rest, self.block_size) - 1) * self.block_size
+        else:
+            last = self._open_tokens[layer] + take
+        self._open_tokens[layer] = last if last < self.block_size else 0
+        return self._blocks[layer]
 
     def begin_step(self) -> bool:
         """Start a decode step; returns whether it is a policy step (every
@@ -307,11 +330,11 @@ class BatchedTieredKVRuntime:
         rc = lib.tierkv_runtime_append(
             _lib.ptr(k), _lib.ptr(v), tokens,
             _lib.ptr(st.table), _lib.ptr(st.states), _lib.ptr(st.lengths), self.max_blocks,
-            _lib.ptr(st.nblocks), self.batch,
+            _lib.ptr(st.nblocks), _lib.ptr(st.open), self.batch,
             _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), self.hot_slots, _lib.ptr(st.hot_free), _lib.ptr(st.ctl),
             self.kv_heads, self.block_size, self.head_dim, stream)
         _lib.check(rc, "tierkv_runtime_append")
-        num_blocks = min(_ceil_div(self.seq_len + tokens, self.block_size), self.max_blocks)
+        num_blocks = min(self._advance_blocks(layer, tokens), self.max_blocks)
         out, sums = tierkv_decode_attention(
             query_states, st.table, st.states, st.lengths, st.hot_k, st.hot_v, st.warm_k, st.warm_v,
             st.k_scale, st.k_zero, st.v_scale, st.v_zero, num_blocks, num_key_value_groups, scaling,
