@@ -105,7 +105,14 @@ class LayerStorage:
 
 
 class BatchedTieredKVRuntime:
-    """Tiered KV cache for ``batch`` sequences of a ``num_layers`` model."""
+    """Tiered KV cache for ``batch`` sequences of a ``num_layers`` model.
+
+    ``cache`` is the HF cache object the model hooks (hf_llama) recognise;
+    ``begin_forward`` / ``finish_forward`` follow the reference runtime's
+    (tierkv_policy.py:1639-1648): a one-token forward is a decode step, and
+    every ``policy_interval``-th decode step is a policy step."""
+
+    is_batched = True
 
     def __init__(self, num_layers: int, batch: int, kv_heads: int, head_dim: int, max_seq_len: int,
                  block_size: int = 16, hot_fraction: float = 0.15, warm_fraction: float = 0.55,
@@ -161,6 +168,10 @@ class BatchedTieredKVRuntime:
         nbytes = _lib.lib().tierkv_runtime_tick_scratch_bytes(self.batch, self.max_blocks, self.max_demotions,
                                                               self.max_promotions)
         self.tick_scratch = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
+        self.current_query_length = 0
+        self.policy_tick_this_forward = False
+        from .tierkv_policy import TieredKVCache
+        self.cache = TieredKVCache(self)
 
     # -- storage ------------------------------------------------------------
 
@@ -304,6 +315,16 @@ class BatchedTieredKVRuntime:
         self._open_tokens[layer] = last if last < self.block_size else 0
         return self._blocks[layer]
 
+    def begin_forward(self, query_length: int) -> None:
+        self.current_query_length = int(query_length)
+        self.policy_tick_this_forward = self.begin_step() if self.current_query_length == 1 else False
+
+    def finish_forward(self) -> None:
+        if self.current_query_length == 1:
+            self.end_step()
+        self.current_query_length = 0
+        self.policy_tick_this_forward = False
+
     def begin_step(self) -> bool:
         """Start a decode step; returns whether it is a policy step (every
         policy_interval generated tokens, as begin_forward does at
@@ -405,9 +426,15 @@ class BatchedTieredKVRuntime:
         meta_block = kv * 4 * 2 if self.warm_format == "absmax_i8" else 0
         resident = hot_tok * fp16_tok + warm_tok * (int8_tok + meta_tok) + warm_blocks * meta_block
         dense = (hot_tok + warm_tok + cold_tok) * fp16_tok
+        physical = 0
+        for st in self.layers:
+            for t in (st.hot_k, st.hot_v, st.warm_k, st.warm_v, st.k_scale, st.k_zero, st.v_scale, st.v_zero):
+                if t is not None:
+                    physical += t.numel() * t.element_size()
         return {
             "hot_blocks": hot_blocks, "warm_blocks": warm_blocks, "cold_blocks": cold_blocks,
             "hot_tokens": hot_tok, "warm_tokens": warm_tok, "cold_tokens": cold_tok,
             "resident_kv_bytes": resident, "dense_equivalent_bytes": dense,
             "compression_x": dense / resident if resident else 0.0,
+            "physical_pool_bytes": physical,
         }

@@ -1,0 +1,135 @@
+"""GPU end-to-end checks of the HF hooks (paged_tierkv_amd.hf_llama) in a
+small random-init Llama (fp16, GQA group 4, head_dim 64), teacher-forced so
+every run sees the same token sequence:
+
+* reference-API runtime, HOT only: logits match the stock HF model with its
+  DynamicCache (fp16 model arithmetic; the decode kernel accumulates in fp32);
+* reference-API runtime with HOT+WARM tiering: the kernel backend matches
+  the reference's eager backend (reconstructed K/V + the model's attention)
+  on the same tier layout, and WARM blocks really are in use;
+* batched runtime, everything HOT: logits match stock HF batched decoding;
+* batched runtime with HOT/WARM/COLD tiering and device policy ticks: runs
+  without allocator errors, keeps logits finite and compresses the cache."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+
+from paged_tierkv_amd import hf_llama, tierkv_policy as tp  # noqa: E402
+from paged_tierkv_amd.block_manager import BlockManager  # noqa: E402
+from paged_tierkv_amd.runtime import BatchedTieredKVRuntime  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+PROMPT, STEPS = 100, 24
+
+
+@pytest.fixture(scope="module")
+def model(device):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=8,
+                      num_key_value_heads=2, head_dim=64, vocab_size=1000, max_position_embeddings=1024)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    m = LlamaForCausalLM(cfg).to(device=device, dtype=torch.float16).eval()
+    hf_llama.install()
+    yield m
+    hf_llama.uninstall()
+    tp.reset_global_tierkv()
+
+
+def _tokens(batch, device):
+    g = torch.Generator().manual_seed(11)
+    return torch.randint(0, 1000, (batch, PROMPT + STEPS), generator=g).to(device)
+
+
+def _teacher_forced(model, ids, cache):
+    """Prefill ids[:, :PROMPT], then feed ids[:, PROMPT + s] one at a time;
+    returns the last-position logits of every forward [STEPS + 1, B, V]."""
+    outs = []
+    with torch.no_grad():
+        out = model(input_ids=ids[:, :PROMPT], past_key_values=cache, use_cache=True, logits_to_keep=1)
+        outs.append(out.logits[:, -1].float())
+        cache = out.past_key_values
+        for s in range(STEPS):
+            out = model(input_ids=ids[:, PROMPT + s: PROMPT + s + 1], past_key_values=cache, use_cache=True,
+                        logits_to_keep=1)
+            outs.append(out.logits[:, -1].float())
+            cache = out.past_key_values
+    return torch.stack(outs)
+
+
+def _dropin_runtime(model, **kw):
+    cfg = model.config
+    return tp.TieredKVRuntime(block_manager=BlockManager(total_blocks=4096), num_layers=cfg.num_hidden_layers,
+                              block_size=16, max_seq_len=PROMPT + STEPS + 16, **kw)
+
+
+def test_dropin_hot_only_matches_stock(model, device):
+    print("[hf] drop-in hot_only vs stock", flush=True)
+    from transformers import DynamicCache
+
+    ids = _tokens(1, device)
+    ref = _teacher_forced(model, ids, DynamicCache(config=model.config))
+    rt = _dropin_runtime(model, hot_budget=3, attention_backend="triton", policy_interval=8, policy_mode="hot_only")
+    got = _teacher_forced(model, ids, rt.cache)
+    torch.testing.assert_close(got, ref, atol=2e-2, rtol=2e-2)
+    assert rt.cache.get_seq_length() == PROMPT + STEPS
+
+
+def test_dropin_tiered_kernel_matches_eager_backend(model, device):
+    print("[hf] drop-in hot_warm kernel vs eager", flush=True)
+    ids = _tokens(1, device)
+    kw = dict(hot_budget=3, policy_interval=10_000, policy_mode="hot_warm")
+    rt_k = _dropin_runtime(model, attention_backend="triton", **kw)
+    got = _teacher_forced(model, ids, rt_k.cache)
+    rt_e = _dropin_runtime(model, attention_backend="eager", **kw)
+    ref = _teacher_forced(model, ids, rt_e.cache)
+    torch.testing.assert_close(got, ref, atol=2e-2, rtol=2e-2)
+    m = rt_k.collect_memory_metrics()
+    assert m["warm_blocks"] > 0 and m["logical_compression_x"] > 1.0
+
+
+def test_dropin_policy_ticks_run(model, device):
+    print("[hf] drop-in hot_warm_cold with ticks", flush=True)
+    ids = _tokens(1, device)
+    rt = _dropin_runtime(model, hot_budget=3, attention_backend="triton", policy_interval=4,
+                         policy_mode="hot_warm_cold", warm_budget=2)
+    got = _teacher_forced(model, ids, rt.cache)
+    assert torch.isfinite(got).all()
+    m = rt.collect_memory_metrics()
+    assert m["cold_blocks"] > 0 and m["warm_blocks"] > 0
+
+
+def test_batched_all_hot_matches_stock(model, device):
+    print("[hf] batched all-HOT vs stock", flush=True)
+    from transformers import DynamicCache
+
+    ids = _tokens(3, device)
+    ref = _teacher_forced(model, ids, DynamicCache(config=model.config))
+    cfg = model.config
+    rt = BatchedTieredKVRuntime(cfg.num_hidden_layers, 3, cfg.num_key_value_heads, cfg.head_dim,
+                                PROMPT + STEPS + 16, hot_fraction=1.0, warm_fraction=0.0, policy_mode="hot_warm",
+                                policy_interval=8, device=device)
+    got = _teacher_forced(model, ids, rt.cache)
+    rt.check_errors()
+    torch.testing.assert_close(got, ref, atol=2e-2, rtol=2e-2)
+    assert rt.cache.get_seq_length() == PROMPT + STEPS
+
+
+def test_batched_tiered_runs(model, device):
+    print("[hf] batched hot_warm_cold with device ticks", flush=True)
+    ids = _tokens(4, device)
+    cfg = model.config
+    rt = BatchedTieredKVRuntime(cfg.num_hidden_layers, 4, cfg.num_key_value_heads, cfg.head_dim,
+                                PROMPT + STEPS + 16, hot_fraction=0.15, warm_fraction=0.55,
+                                policy_mode="hot_warm_cold", policy_interval=8, device=device)
+    got = _teacher_forced(model, ids, rt.cache)
+    rt.check_errors()
+    assert torch.isfinite(got).all()
+    m = rt.memory_metrics()
+    assert m["cold_blocks"] > 0 and m["compression_x"] > 1.0
