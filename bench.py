@@ -44,7 +44,12 @@ def parse():
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c4"], default="c3")
+    p.add_argument("--workload", choices=["c3", "c4", "c5"], default="c3",
+                   help="c5: end-to-end random-init Llama-3-8B decode through the HF hooks (own JSON line)")
+    p.add_argument("--c5-steps", type=int, default=256)
+    p.add_argument("--c5-batch", type=int, default=16)
+    p.add_argument("--c5-prompt", type=int, default=2048)
+    p.add_argument("--no-dense-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--mode", choices=["bench", "copy"], default="bench",
@@ -137,6 +142,128 @@ def copy_calibration(device):
                       "GBps_read_plus_write": 2 * n / t / 1e9}))
 
 
+C5_METRIC = ("C5 end-to-end decode tokens/s + resident KV bytes, random-init Llama-3-8B, batch 16, "
+             "prompt 2048, 256 greedy steps")
+
+
+def c5_model(device):
+    """Random-init Llama-3-8B-shaped decoder:
+    32 layers, hidden 4096, 32 / 8 heads, head_dim 128, FFN 14336, vocab
+    128256, fp16 weights ~N(0, 0.02) (transformers' own init with
+    initializer_range 0.02), built directly on the GPU."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
+                      num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=8192,
+                      rope_theta=500000.0, initializer_range=0.02, rms_norm_eps=1e-5, tie_word_embeddings=False)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(device):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    return model
+
+
+def c5_generate(model, prompt, cache, steps):
+    """Prefill, then `steps` greedy decode steps; returns (tokens [B, steps],
+    decode seconds measured with a device sync on both sides)."""
+    import torch
+
+    toks = []
+    with torch.no_grad():
+        out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        cache = out.past_key_values
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            out = model(input_ids=tok, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            cache = out.past_key_values
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            toks.append(tok)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+    return torch.cat(toks, dim=1), sec, cache
+
+
+def run_c5(args, device):
+    import torch
+    from transformers import DynamicCache
+
+    from paged_tierkv_amd import hf_llama
+    from paged_tierkv_amd.runtime import BatchedTieredKVRuntime
+
+    B, T, steps = args.c5_batch, args.c5_prompt, args.c5_steps
+    log(f"[c5] building random-init Llama-3-8B on {torch.cuda.get_device_name(0)}")
+    model = c5_model(device)
+    cfg = model.config
+    hf_llama.install()
+    prompt = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(1)).to(device)
+
+    def runtime():
+        return BatchedTieredKVRuntime(cfg.num_hidden_layers, B, cfg.num_key_value_heads, cfg.head_dim,
+                                      T + steps + 16, block_size=16, hot_fraction=0.15, warm_fraction=0.55,
+                                      policy_mode="hot_warm_cold", policy_interval=64, warm_format="absmax_i8",
+                                      cold_mode="masked", device=device)
+
+    log("[c5] warm-up run (kernels, GEMM heuristics)")
+    c5_generate(model, prompt[:, :256], runtime().cache, 8)
+    log(f"[c5] tiered run: batch {B}, prompt {T}, {steps} greedy steps, policy every 64")
+    rt = runtime()
+    toks, sec, _ = c5_generate(model, prompt, rt.cache, steps)
+    rt.check_errors()
+    metrics = rt.memory_metrics()
+    tps = B * steps / sec
+    log(f"[c5] tiered: {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step), resident KV "
+        f"{metrics['resident_kv_bytes'] / 2**20:.1f} MiB vs dense {metrics['dense_equivalent_bytes'] / 2**20:.1f} MiB")
+    dense = None
+    if not args.no_dense_baseline:
+        del rt
+        torch.cuda.empty_cache()
+        log("[c5] dense baseline: stock transformers DynamicCache, same model and prompt")
+        c5_generate(model, prompt[:, :256], DynamicCache(config=cfg), 8)
+        dtoks, dsec, dcache = c5_generate(model, prompt, DynamicCache(config=cfg), steps)
+        kv_bytes = 0
+        for layer in dcache.layers:
+            for t in (layer.keys, layer.values):
+                kv_bytes += t.numel() * t.element_size()
+        agree = (dtoks == toks).float().mean().item()
+        dense = {"tokens_per_s": round(B * steps / dsec, 1), "ms_per_step": round(dsec / steps * 1e3, 3),
+                 "kv_bytes": kv_bytes, "greedy_token_agreement_with_tiered": round(agree, 4)}
+        log(f"[c5] dense: {dense['tokens_per_s']} tok/s, KV {kv_bytes / 2**20:.1f} MiB, token agreement {agree:.3f}")
+    hf_llama.uninstall()
+    line = {
+        "metric": C5_METRIC,
+        "value": round(tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": 8,
+        "ms_per_step": round(sec / steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: random-init weights N(0, 0.02), uniform random prompt ids",
+        "config": {"workload": "c5_llama3_8b_e2e", "batch": B, "prompt": T, "decode_steps": steps,
+                   "block_size": 16, "hot_fraction": 0.15, "warm_fraction": 0.55, "policy_interval": 64,
+                   "policy_mode": "hot_warm_cold", "warm_format": "int8 absmax per (block, kv head)",
+                   "cold": "masked", "attention": "tiered HIP decode kernel; prefill via the model's SDPA"},
+        "kv_resident_bytes": metrics["resident_kv_bytes"],
+        "kv_dense_equivalent_bytes": metrics["dense_equivalent_bytes"],
+        "kv_compression_x": round(metrics["compression_x"], 3),
+        "kv_physical_pool_bytes": metrics["physical_pool_bytes"],
+        "tiers_at_end": {k: metrics[k] for k in ("hot_blocks", "warm_blocks", "cold_blocks")},
+        "dense_hf_baseline": dense,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -150,6 +277,9 @@ def main():
     device = torch.device("cuda:0")
     if args.mode == "copy":
         copy_calibration(device)
+        return
+    if args.workload == "c5":
+        run_c5(args, device)
         return
     log(f"[bench] building {args.layers} layers of {args.workload} on {torch.cuda.get_device_name(0)}")
     layers = build_layers(args, device)
