@@ -194,6 +194,16 @@ TIERKV_API int32_t tierkv_runtime_tick(
 TIERKV_API int64_t tierkv_runtime_tick_scratch_bytes(int32_t batch, int64_t table_stride,
                                                       int32_t max_demotions, int32_t max_promotions);
 
+/* Tier telemetry without a host sync: adds one layer's per-tier block and
+ * token counts over sequences b < batch and blocks i < seq_num_blocks[b] into
+ * counts int64[6] = {HOT, WARM, COLD blocks, HOT, WARM, COLD tokens} on the
+ * device; the caller reads them back when it wants the numbers.  The counts
+ * collect_memory_metrics derives from the tables (tierkv_policy.py:1193-1317,
+ * 489-654) with one `.item()` sync per counter and layer. */
+TIERKV_API int32_t tierkv_tier_counts(const int32_t* block_states, const int32_t* block_lengths,
+                                      int64_t table_stride, const int32_t* seq_num_blocks, int32_t batch,
+                                      int64_t* counts, void* stream);
+
 /* Table writes planned on the host: dst[pairs[2i]] = pairs[2i + 1] for
  * i < n, positions distinct, out-of-range positions skipped; pairs is an
  * 8-byte-aligned int32 device array.  Replaces the per-entry device writes of

@@ -438,9 +438,53 @@ __global__ __launch_bounds__(CT) void scatter_i32_kernel(int32_t* dst, int64_t l
   if (pv.x >= 0 && pv.x < len) dst[pv.x] = pv.y;
 }
 
+// ---------------------------------------------------------------------------
+// Tier telemetry: per-tier block and token counts of one layer, added into
+// counts[6] = {HOT, WARM, COLD blocks, HOT, WARM, COLD tokens} (int64).  One
+// workgroup; LDS partial sums, one global add per counter.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(CT) void tier_counts_kernel(const int32_t* states, const int32_t* lengths,
+                                                         int64_t stride, const int32_t* nblocks, int batch,
+                                                         int max_blocks, unsigned long long* counts) {
+  __shared__ unsigned long long s_cnt[6];
+  if (threadIdx.x < 6) s_cnt[threadIdx.x] = 0ull;
+  __syncthreads();
+  unsigned long long c[6] = {0ull, 0ull, 0ull, 0ull, 0ull, 0ull};
+  for (int b = 0; b < batch; ++b) {
+    const int n = min(max(nblocks[b], 0), max_blocks);
+    for (int i = threadIdx.x; i < n; i += CT) {
+      const int64_t o = int64_t(b) * stride + i;
+      const int st = states[o];
+      if (st < 0 || st > 2) continue;
+      c[st] += 1ull;
+      c[3 + st] += static_cast<unsigned long long>(max(lengths[o], 0));
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    unsigned long long v = c[k];
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    if ((threadIdx.x & 63) == 0 && v) atomicAdd(&s_cnt[k], v);
+  }
+  __syncthreads();
+  if (threadIdx.x < 6) atomicAdd(&counts[threadIdx.x], s_cnt[threadIdx.x]);
+}
+
 }  // namespace tierkv
 
 using namespace tierkv;
+
+extern "C" int32_t tierkv_tier_counts(const int32_t* block_states, const int32_t* block_lengths,
+                                      int64_t table_stride, const int32_t* seq_num_blocks, int32_t batch,
+                                      int64_t* counts, void* stream) {
+  clear_error();
+  if (!block_states || !block_lengths || !seq_num_blocks || !counts) return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (batch <= 0 || table_stride <= 0 || table_stride > 0x7fffffff) return fail(TIERKV_ERR_INVALID, "bad table geometry");
+  hipLaunchKernelGGL(tier_counts_kernel, dim3(1), dim3(CT), 0, reinterpret_cast<hipStream_t>(stream), block_states,
+                     block_lengths, table_stride, seq_num_blocks, batch, int(table_stride),
+                     reinterpret_cast<unsigned long long*>(counts));
+  return check_launch("tier_counts_kernel");
+}
 
 extern "C" int32_t tierkv_scatter_i32(int32_t* dst, int64_t dst_len, const int32_t* pairs, int32_t n,
                                       void* stream) {

@@ -394,32 +394,30 @@ class BatchedTieredKVRuntime:
             msgs = [m for b, m in ERROR_BITS.items() if bits & b]
             raise RuntimeError("tiered KV runtime: " + "; ".join(msgs))
 
+    def tier_counters(self, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Device int64 [6] = {HOT, WARM, COLD blocks, HOT, WARM, COLD tokens}
+        summed over layers and sequences, computed on the device
+        (``tierkv_tier_counts``) without a host sync; ``out`` is zeroed and
+        reused when given."""
+        lib = _lib.lib()
+        if out is None:
+            out = torch.zeros(6, dtype=torch.int64, device=self.device)
+        else:
+            out.zero_()
+        stream = _lib.stream_of(self.device)
+        for st in self.layers:
+            rc = lib.tierkv_tier_counts(_lib.ptr(st.states), _lib.ptr(st.lengths), self.max_blocks,
+                                        _lib.ptr(st.nblocks), self.batch, _lib.ptr(out), stream)
+            _lib.check(rc, "tierkv_tier_counts")
+        return out
+
     def memory_metrics(self) -> dict:
         """Resident KV bytes and tier counts over all layers and sequences
-        (collect_memory_metrics, tierkv_policy.py:1193-1317, computed from
-        the device tables; synchronises)."""
+        (collect_memory_metrics, tierkv_policy.py:1193-1317) from the device
+        counters: one host sync, for the single read-back."""
         kv, d = self.kv_heads, self.head_dim
-        hot_blocks = warm_blocks = cold_blocks = 0
-        hot_tok = warm_tok = cold_tok = 0
-        for st in self.layers:
-            n = int(st.nblocks.max().item())
-            if n == 0:
-                continue
-            s = st.states[:, :n]
-            ln = st.lengths[:, :n].to(torch.int64)
-            for code, acc in ((HOT_STATE, "h"), (WARM_STATE, "w"), (COLD_STATE, "c")):
-                m = s == code
-                blocks = int(m.sum().item())
-                toks = int(ln[m].sum().item())
-                if acc == "h":
-                    hot_blocks += blocks
-                    hot_tok += toks
-                elif acc == "w":
-                    warm_blocks += blocks
-                    warm_tok += toks
-                else:
-                    cold_blocks += blocks
-                    cold_tok += toks
+        hot_blocks, warm_blocks, cold_blocks, hot_tok, warm_tok, cold_tok = (
+            int(x) for x in self.tier_counters().cpu().tolist())
         fp16_tok = kv * d * 2 * 2
         int8_tok = kv * d * 2
         meta_tok = kv * 4 * 2 if self.warm_format == "ref_u8" else 0

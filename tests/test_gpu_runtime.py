@@ -114,6 +114,15 @@ def test_batched_runtime_matches_model(device, warm_format, policy_mode, cold_mo
         assert orc.migrations["evict"] > 0, orc.migrations
     m = rt.memory_metrics()
     assert m["hot_blocks"] + m["warm_blocks"] + m["cold_blocks"] == int(orc.nb.sum())
+    # Device telemetry counters equal the counts of the model's tables.
+    want = []
+    for tier in (0, 1, 2):
+        mask = np.zeros_like(orc.states, dtype=bool)
+        for b in range(B):
+            mask[b, :orc.nb[b]] = orc.states[b, :orc.nb[b]] == tier
+        want.append((int(mask.sum()), int(orc.lengths[mask].sum())))
+    got = rt.tier_counters().cpu().tolist()
+    assert got == [w[0] for w in want] + [w[1] for w in want]
     assert 0 < m["resident_kv_bytes"] < m["dense_equivalent_bytes"]
 
 
