@@ -194,6 +194,25 @@ TIERKV_API int32_t tierkv_runtime_tick(
 TIERKV_API int64_t tierkv_runtime_tick_scratch_bytes(int32_t batch, int64_t table_stride,
                                                       int32_t max_demotions, int32_t max_promotions);
 
+/* Prefill block scores without materialising the attention probabilities.
+ * Replaces compute_block_scores on the prefill attention weights
+ * (tierkv_policy.py:1380-1389 via modeling_llama.py:282-292), per sequence:
+ *   mass[b, blk] = sum_{h, q} sum_{t in blk} p[b, h, q, t] / (H * T) / len(blk)
+ * with p the causal softmax of scaling * q . k.  q [B, H, T, D] and k
+ * [B, H_kv, T, D] are fp16 or bf16 with the given element strides (head_dim
+ * contiguous, strides multiples of 8, 16-byte aligned); head_dim 64 or 128,
+ * GQA group <= 8, block_size a multiple of 16, T <= 32768.  mass is fp32
+ * [B, ceil(T / block_size)].  Two MFMA passes over K (log-sum-exp, then
+ * block sums); deterministic (fixed reduction order).  workspace: at least
+ * tierkv_prefill_block_mass_workspace_bytes(B, H_kv, T) bytes, no
+ * initialisation needed. */
+TIERKV_API int64_t tierkv_prefill_block_mass_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t tokens);
+TIERKV_API int32_t tierkv_prefill_block_mass(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t, int32_t dtype,
+    float* mass, int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t tokens, int32_t head_dim,
+    int32_t block_size, float scaling, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Tier telemetry without a host sync: adds one layer's per-tier block and
  * token counts over sequences b < batch and blocks i < seq_num_blocks[b] into
  * counts int64[6] = {HOT, WARM, COLD blocks, HOT, WARM, COLD tokens} on the

@@ -24,6 +24,11 @@
 * ``tier_labels`` batches ``enforce_tiered_budget`` / ``enforce_budget`` over
   sequences with a rank-by-counting formulation (rank_i = #{j: s_j > s_i or
   (s_j == s_i and j < i)}) that equals the stable descending sort.
+* ``prefill_block_mass`` is ``compute_block_scores`` applied per sequence to
+  the causal prefill attention probabilities, in float64 (the quantity the
+  prefill block-score kernel computes without materialising them); pinned by
+  closed forms (zero keys give p = 1 / (q + 1); one token gives mass 1;
+  length-weighted masses sum to 1; a dominant key takes its queries' mass).
 
 Pinned by the reference's known answer (main.py:375-389: block means
 [0.4, 0.9, 0.1, 0.2], hot_budget 3 -> [0, 0, 1, 0]), its mode checks
@@ -188,4 +193,34 @@ def tier_labels(scores, current_states, hot_budget, warm_budget, mode="hot_warm_
             out[b] = cur[b]  # enforce_policy returns early (tierkv_policy.py:1888-1889)
         else:
             raise ValueError(mode)
+    return out
+
+
+def prefill_block_mass(q, k, scaling, block_size):
+    """Per-sequence prefill block scores: compute_block_scores
+    (tierkv_policy.py:1380-1389) applied to one sequence's causal attention
+    probabilities (eager_attention_forward, modeling_llama.py:225-247: fp32
+    softmax of scaling * q . k with the causal mask), here in float64 without
+    the reference's fp16 rounding of the probabilities.
+
+    q [B, H, T, D], k [B, H_kv, T, D] -> [B, ceil(T / block_size)]: the mean
+    probability over heads and queries, averaged over each block's tokens.
+    Materialises [H, T, T] per sequence: small T only."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    B, H, T, _ = q.shape
+    G = H // k.shape[1]
+    nblk = -(-T // block_size)
+    out = np.zeros((B, nblk))
+    causal = np.tril(np.ones((T, T), bool))
+    for b in range(B):
+        kk = np.repeat(k[b], G, axis=0)                       # [H, T, D]
+        logits = np.einsum("hqd,htd->hqt", q[b], kk) * scaling
+        logits = np.where(causal[None], logits, -np.inf)
+        logits -= logits.max(axis=-1, keepdims=True)
+        p = np.exp(logits)
+        p /= p.sum(axis=-1, keepdims=True)
+        per_token = p.sum(axis=(0, 1)) / (H * T)              # mean over heads and queries
+        for blk in range(nblk):
+            out[b, blk] = per_token[blk * block_size:(blk + 1) * block_size].mean()
     return out

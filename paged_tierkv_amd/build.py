@@ -42,6 +42,7 @@ HIP_SOURCES = {
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
     "runtime.hip": ["-ffp-contract=off"],
+    "prefill_score.hip": [],
 }
 CXX_SOURCES = ["block_manager.cpp"]
 

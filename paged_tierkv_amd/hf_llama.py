@@ -102,6 +102,17 @@ def _attention_interface(module):
     return fn
 
 
+def _attention_block_scores(runtime, query_states, key_states, scaling):
+    """Per-sequence prefill block scores [B, n] from the prefill block-score
+    kernel (no materialised probabilities), when the runtime asks for them
+    (``prefill_scoring="attention"``); None otherwise."""
+    if getattr(runtime, "prefill_scoring", "proxy") != "attention":
+        return None
+    from . import kernels
+
+    return kernels.prefill_block_mass(query_states, key_states, runtime.block_size, scaling)
+
+
 def _batched_block_scores(attn_weights, runtime, seq_len: int):
     """Per-sequence prefill scores [B, n] from returned probabilities
     [B, H, Q, T] (mean over heads and queries, then over the block's tokens,
@@ -153,8 +164,14 @@ def tierkv_attention_forward(self, hidden_states: torch.Tensor, position_embeddi
         runtime.profile_end("prefill_attention_ms", start)
         if seq_id in runtime.tiered_layer_indices and runtime.policy_mode != "hot_only":
             start = runtime.profile_start()
-            block_scores = compute_prefill_block_scores(runtime.policy_engine, attn_weights, key_states.shape[-2],
-                                                        runtime.block_size, query_states.device)
+            block_scores = None
+            if attn_weights is None:
+                block_scores = _attention_block_scores(runtime, query_states, key_states, self.scaling)
+            if block_scores is not None:
+                block_scores = block_scores[0]
+            else:
+                block_scores = compute_prefill_block_scores(runtime.policy_engine, attn_weights, key_states.shape[-2],
+                                                            runtime.block_size, query_states.device)
             runtime.append_prefill_with_policy(seq_id, key_states, value_states, block_scores)
             runtime.profile_end("prefill_policy_ms", start)
         else:
@@ -220,8 +237,10 @@ def _batched_forward(self, runtime, query_states, key_states, value_states, atte
     if query_states.shape[-2] > 1:
         attn_output, attn_weights = _attention_interface(self)(
             self, query_states, key_states, value_states, attention_mask, scaling=self.scaling, dropout=dropout)
-        runtime.prefill_layer(layer, key_states, value_states,
-                              block_scores=_batched_block_scores(attn_weights, runtime, key_states.shape[-2]))
+        scores = _batched_block_scores(attn_weights, runtime, key_states.shape[-2])
+        if scores is None:
+            scores = _attention_block_scores(runtime, query_states, key_states, self.scaling)
+        runtime.prefill_layer(layer, key_states, value_states, block_scores=scores)
         attn_output = attn_output.reshape(*input_shape, -1).contiguous()
         return self.o_proj(attn_output), attn_weights
     if not bool(kwargs.get("tierkv_triton_mask_safe", False)):

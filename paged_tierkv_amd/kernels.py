@@ -166,3 +166,45 @@ def tier_labels(scores: torch.Tensor, cur_states: torch.Tensor, hot_budget: int,
                                 _lib.stream_of(sc.device))
     _lib.check(rc, "tierkv_tier_labels")
     return out[0] if squeeze else out
+
+
+_prefill_ws: dict = {}
+
+
+def prefill_block_mass(query_states: torch.Tensor, key_states: torch.Tensor, block_size: int, scaling: float):
+    """Per-sequence prefill block scores without materialised probabilities
+    (``tierkv_prefill_block_mass``): query [B, H, T, D] and key [B, H_kv, T, D]
+    (fp16 / bf16, any layout with head_dim contiguous, e.g. HF's transposed
+    projections) -> fp32 [B, ceil(T / block_size)], the mean causal attention
+    probability of each block over heads and queries (compute_block_scores,
+    tierkv_policy.py:1380-1389, per sequence)."""
+    lib = _lib.lib()
+    _lib.require_gpu_tensor(query_states, "query_states")
+    _lib.require_gpu_tensor(key_states, "key_states")
+    if query_states.ndim != 4 or key_states.ndim != 4:
+        raise ValueError("query and key states must be [batch, heads, tokens, head_dim].")
+    if query_states.dtype not in (torch.float16, torch.bfloat16) or key_states.dtype != query_states.dtype:
+        raise ValueError("query and key states must share an fp16 / bf16 dtype.")
+    q, k = query_states, key_states
+    if q.stride(-1) != 1 or q.stride(0) % 8 or q.stride(1) % 8 or q.stride(2) % 8 or q.data_ptr() % 16:
+        q = q.contiguous()
+    if k.stride(-1) != 1 or k.stride(0) % 8 or k.stride(1) % 8 or k.stride(2) % 8 or k.data_ptr() % 16:
+        k = k.contiguous()
+    batch, heads, tokens, dim = (int(x) for x in q.shape)
+    if k.shape[0] != batch or k.shape[2] != tokens or k.shape[3] != dim:
+        raise ValueError("key states do not match the query geometry.")
+    kv_heads = int(k.shape[1])
+    need = int(lib.tierkv_prefill_block_mass_workspace_bytes(batch, kv_heads, tokens))
+    key = (q.device.type, q.device.index)
+    ws = _prefill_ws.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)
+        _prefill_ws[key] = ws
+    nblk = (tokens + int(block_size) - 1) // int(block_size)
+    out = torch.empty((batch, nblk), dtype=torch.float32, device=q.device)
+    rc = lib.tierkv_prefill_block_mass(
+        _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2), _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _lib.DTYPE_BF16 if q.dtype == torch.bfloat16 else _lib.DTYPE_F16, _lib.ptr(out), batch, heads, kv_heads,
+        tokens, dim, int(block_size), float(scaling), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(q.device))
+    _lib.check(rc, "tierkv_prefill_block_mass")
+    return out

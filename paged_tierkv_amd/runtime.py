@@ -117,13 +117,16 @@ class BatchedTieredKVRuntime:
     def __init__(self, num_layers: int, batch: int, kv_heads: int, head_dim: int, max_seq_len: int,
                  block_size: int = 16, hot_fraction: float = 0.15, warm_fraction: float = 0.55,
                  policy_mode: str = "hot_warm_cold", policy_interval: int = 64,
-                 warm_format: str = "absmax_i8", cold_mode: str = "masked", device=None):
+                 warm_format: str = "absmax_i8", cold_mode: str = "masked", device=None,
+                 prefill_scoring: str = "proxy"):
         if policy_mode not in _MODES:
             raise ValueError('policy_mode must be "hot_warm" or "hot_warm_cold".')
         if warm_format not in kernels.WARM_FORMATS:
             raise ValueError('warm_format must be "absmax_i8" or "ref_u8".')
         if policy_interval <= 0:
             raise ValueError("policy_interval must be positive.")
+        if prefill_scoring not in ("proxy", "attention"):
+            raise ValueError('prefill_scoring must be "proxy" or "attention".')
         if not (0.0 <= hot_fraction <= 1.0 and 0.0 <= warm_fraction <= 1.0):
             raise ValueError("tier fractions must lie in [0, 1].")
         self.device = torch.device(device or "cuda")
@@ -143,6 +146,10 @@ class BatchedTieredKVRuntime:
         self.policy_interval = int(policy_interval)
         self.warm_format = warm_format
         self.cold_mode = cold_mode
+        # Prefill block scores when the model's attention returns no
+        # probabilities: "proxy" = sink + recency (the reference under SDPA),
+        # "attention" = the prefill block-score kernel.
+        self.prefill_scoring = prefill_scoring
         n = self.max_blocks
         # Capacities per sequence.  HOT: the budget, the blocks appended between
         # ticks, and room for a tick's promotions before its demotions free

@@ -1660,8 +1660,15 @@ class TieredKVRuntime:
         pool_layout: str | None = None,
         *,
         warm_format: str = "ref_u8",
+        prefill_scoring: str = "proxy",
     ):
         attention_backend = attention_backend or os.environ.get("TIERKV_ATTENTION_BACKEND", "triton")
+        if prefill_scoring not in ("proxy", "attention"):
+            raise ValueError('prefill_scoring must be "proxy" or "attention".')
+        # Prefill block scores when the model's attention returns no
+        # probabilities: "proxy" = the reference's sink + recency scores,
+        # "attention" = the prefill block-score kernel (extension).
+        self.prefill_scoring = prefill_scoring
         if attention_backend not in ("eager", "triton"):
             raise ValueError('attention_backend must be "eager" or "triton".')
         if policy_interval is None:

@@ -133,3 +133,28 @@ def test_batched_tiered_runs(model, device):
     assert torch.isfinite(got).all()
     m = rt.memory_metrics()
     assert m["cold_blocks"] > 0 and m["compression_x"] > 1.0
+
+
+def test_attention_prefill_scoring_changes_tiers(model, device):
+    """prefill_scoring="attention" ranks prompt blocks by the prefill
+    block-score kernel instead of the sink + recency proxy: the prompt's tier
+    layout differs, the run stays finite, and the batched runtime accepts the
+    same option."""
+    print("[hf] attention prefill scoring", flush=True)
+    ids = _tokens(1, device)
+    layouts = {}
+    for scoring in ("proxy", "attention"):
+        rt = _dropin_runtime(model, hot_budget=3, attention_backend="triton", policy_interval=10_000,
+                             policy_mode="hot_warm_cold", warm_budget=2, prefill_scoring=scoring)
+        with torch.no_grad():
+            out = model(input_ids=ids[:, :PROMPT], past_key_values=rt.cache, use_cache=True, logits_to_keep=1)
+        assert torch.isfinite(out.logits).all()
+        layouts[scoring] = [rt.block_manager.get_states(layer) for layer in range(model.config.num_hidden_layers)]
+    assert layouts["proxy"] != layouts["attention"]
+    cfg = model.config
+    rt = BatchedTieredKVRuntime(cfg.num_hidden_layers, 2, cfg.num_key_value_heads, cfg.head_dim, PROMPT + STEPS + 16,
+                                hot_fraction=0.2, warm_fraction=0.3, policy_mode="hot_warm_cold", policy_interval=8,
+                                device=device, prefill_scoring="attention")
+    got = _teacher_forced(model, _tokens(2, device), rt.cache)
+    rt.check_errors()
+    assert torch.isfinite(got).all()

@@ -98,3 +98,35 @@ def test_bad_inputs_raise():
         P.enforce_budget([0.1, 0.2, 0.3], [0, 0, 0], 2, demoted_state=0)
     with pytest.raises(ValueError):
         P.enforce_tiered_budget([0.1, 0.2], [0, 0, 0], 2, 1)
+
+
+def test_prefill_block_mass_closed_forms():
+    """oracle.policy.prefill_block_mass against what the mathematics fixes:
+    with all keys zero every query spreads its probability uniformly over the
+    keys it may see, p[q, t] = 1 / (q + 1) for t <= q, so the mass of token t
+    is sum_{q >= t} 1 / (q + 1) / T; with one token the mass is 1; masses
+    weighted by block length sum to 1 (every query row sums to 1)."""
+    import numpy as np
+    from oracle.policy import prefill_block_mass
+
+    T, bs = 37, 16
+    rng = np.random.default_rng(0)
+    q = rng.standard_normal((1, 4, T, 8))
+    k = np.zeros((1, 2, T, 8))
+    got = prefill_block_mass(q, k, 0.3, bs)[0]
+    per_token = np.array([sum(1.0 / (qq + 1) for qq in range(t, T)) / T for t in range(T)])
+    want = [per_token[i * bs:(i + 1) * bs].mean() for i in range(-(-T // bs))]
+    np.testing.assert_allclose(got, want, rtol=1e-12)
+    assert prefill_block_mass(q[:, :, :1], k[:, :, :1], 0.3, bs)[0].tolist() == [1.0]
+    k2 = rng.standard_normal((2, 2, T, 8))
+    q2 = rng.standard_normal((2, 4, T, 8))
+    m = prefill_block_mass(q2, k2, 0.5, bs)
+    lens = np.array([min(bs, T - i * bs) for i in range(m.shape[1])])
+    np.testing.assert_allclose((m * lens).sum(axis=1), 1.0, rtol=1e-12)
+    # A key that dominates every logit takes (almost) all the mass of the
+    # queries that can see it.
+    k3 = np.zeros((1, 1, T, 8))
+    k3[0, 0, 0] = 50.0
+    q3 = np.ones((1, 1, T, 8))
+    m3 = prefill_block_mass(q3, k3, 1.0, bs)[0]
+    assert m3[0] * bs > 0.999
