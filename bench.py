@@ -50,6 +50,8 @@ def parse():
     p.add_argument("--c5-batch", type=int, default=16)
     p.add_argument("--c5-prompt", type=int, default=2048)
     p.add_argument("--no-dense-baseline", action="store_true")
+    p.add_argument("--c5-eager", action="store_true",
+                   help="c5: run decode steps eagerly only (no HIP-graph replay, no eager comparison run)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--mode", choices=["bench", "copy"], default="bench",
@@ -169,22 +171,32 @@ def c5_model(device):
     return model
 
 
-def c5_generate(model, prompt, cache, steps):
+def c5_generate(model, prompt, cache, steps, runtime=None):
     """Prefill, then `steps` greedy decode steps; returns (tokens [B, steps],
-    decode seconds measured with a device sync on both sides)."""
+    decode seconds measured with a device sync on both sides, cache).  With
+    ``runtime`` the decode steps go through hf_llama.DecodeGraphRunner
+    (captured steps replayed as HIP graphs; the captures happen inside the
+    timed region)."""
     import torch
+
+    from paged_tierkv_amd import hf_llama
 
     toks = []
     with torch.no_grad():
         out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
         cache = out.past_key_values
         tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        runner = hf_llama.DecodeGraphRunner(model, runtime) if runtime is not None else None
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
-            out = model(input_ids=tok, past_key_values=cache, use_cache=True, logits_to_keep=1)
-            cache = out.past_key_values
-            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            if runner is not None:
+                logits = runner.step(tok)
+            else:
+                out = model(input_ids=tok, past_key_values=cache, use_cache=True, logits_to_keep=1)
+                cache = out.past_key_values
+                logits = out.logits
+            tok = logits[:, -1].argmax(-1, keepdim=True)
             toks.append(tok)
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
@@ -213,13 +225,24 @@ def run_c5(args, device):
 
     log("[c5] warm-up run (kernels, GEMM heuristics)")
     c5_generate(model, prompt[:, :256], runtime().cache, 8)
-    log(f"[c5] tiered run: batch {B}, prompt {T}, {steps} greedy steps, policy every 64")
+    eager = None
+    if not args.c5_eager:
+        log(f"[c5] tiered run (eager steps): batch {B}, prompt {T}, {steps} greedy steps, policy every 64")
+        rt = runtime()
+        _, esec, _ = c5_generate(model, prompt, rt.cache, steps)
+        rt.check_errors()
+        eager = {"tokens_per_s": round(B * steps / esec, 1), "ms_per_step": round(esec / steps * 1e3, 3)}
+        log(f"[c5] tiered eager: {eager['tokens_per_s']} tok/s ({eager['ms_per_step']} ms/step)")
+        del rt
+        torch.cuda.empty_cache()
+    mode = "eager" if args.c5_eager else "HIP graphs"
+    log(f"[c5] tiered run ({mode}): batch {B}, prompt {T}, {steps} greedy steps, policy every 64")
     rt = runtime()
-    toks, sec, _ = c5_generate(model, prompt, rt.cache, steps)
+    toks, sec, _ = c5_generate(model, prompt, rt.cache, steps, runtime=None if args.c5_eager else rt)
     rt.check_errors()
     metrics = rt.memory_metrics()
     tps = B * steps / sec
-    log(f"[c5] tiered: {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step), resident KV "
+    log(f"[c5] tiered ({mode}): {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step), resident KV "
         f"{metrics['resident_kv_bytes'] / 2**20:.1f} MiB vs dense {metrics['dense_equivalent_bytes'] / 2**20:.1f} MiB")
     dense = None
     if not args.no_dense_baseline:
@@ -253,7 +276,9 @@ def run_c5(args, device):
         "config": {"workload": "c5_llama3_8b_e2e", "batch": B, "prompt": T, "decode_steps": steps,
                    "block_size": 16, "hot_fraction": 0.15, "warm_fraction": 0.55, "policy_interval": 64,
                    "policy_mode": "hot_warm_cold", "warm_format": "int8 absmax per (block, kv head)",
-                   "cold": "masked", "attention": "tiered HIP decode kernel; prefill via the model's SDPA"},
+                   "cold": "masked", "attention": "tiered HIP decode kernel; prefill via the model's SDPA",
+                   "decode_steps_as": mode},
+        "tiered_eager_steps": eager,
         "kv_resident_bytes": metrics["resident_kv_bytes"],
         "kv_dense_equivalent_bytes": metrics["dense_equivalent_bytes"],
         "kv_compression_x": round(metrics["compression_x"], 3),

@@ -272,6 +272,78 @@ def tierkv_model_forward(self, input_ids=None, attention_mask=None, position_ids
     return out
 
 
+class DecodeGraphRunner:
+    """Decode steps of an HF Llama over a ``BatchedTieredKVRuntime`` replayed
+    as HIP graphs.
+
+    Between policy ticks a decode step launches the same kernels with the same
+    arguments every time: the runtime's tables, free stacks and block counts
+    live on the device, and the decode kernel is launched with the table width
+    as its bound (``fixed_launch_bound``).  The step is therefore captured once
+    and replayed, which removes the host cost of transformers' ~40 launches per
+    layer.  The host bookkeeping a Python forward would do (step counter,
+    block counts, cache length) is done by the runner around each replay.
+
+    * The first step runs eagerly (it sizes every workspace); the next two
+      are captured and replayed.  Policy steps run eagerly.
+    * Two graphs alternate: the decode kernel's split-arrival counters need
+      consecutive launches on a workspace to carry different stamps, and a
+      graph replays the stamps it captured.
+    * ``step`` returns the graph's static logits tensor: read it before the
+      same graph is replayed again (two steps later).
+    * Everything runs on the current stream; sequences must be unpadded.
+    """
+
+    def __init__(self, model, runtime):
+        if not getattr(runtime, "is_batched", False):
+            raise ValueError("DecodeGraphRunner drives a BatchedTieredKVRuntime.")
+        self.model = model
+        self.rt = runtime
+        runtime.fixed_launch_bound = True
+        self.ids = torch.zeros((runtime.batch, 1), dtype=torch.long, device=runtime.device)
+        self.pos = torch.zeros((1, 1), dtype=torch.long, device=runtime.device)
+        self.graphs: list = []
+        self.outs: list = []
+        self.turn = 0
+        self.eager_steps = 0
+        self.replays = 0
+
+    def _forward(self):
+        return self.model(input_ids=self.ids, position_ids=self.pos, past_key_values=self.rt.cache, use_cache=True,
+                          logits_to_keep=1).logits
+
+    def step(self, input_ids: torch.Tensor) -> torch.Tensor:
+        """One decode step for input_ids [B, 1]; returns logits [B, 1, V]."""
+        rt = self.rt
+        self.ids.copy_(input_ids)
+        self.pos.fill_(rt.cache.get_seq_length())
+        tick_next = (rt.decode_step + 1) % rt.policy_interval == 0
+        with torch.no_grad():
+            if tick_next or self.eager_steps == 0:
+                self.eager_steps += 1
+                return self._forward()
+            if len(self.graphs) < 2:
+                # The Python forward runs once under capture (doing this step's
+                # host bookkeeping); the recorded kernels then run by replay.
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    out = self._forward()
+                self.graphs.append(g)
+                self.outs.append(out)
+                g.replay()
+                self.turn = len(self.graphs) % 2
+                return out
+        g, out = self.graphs[self.turn], self.outs[self.turn]
+        self.turn ^= 1
+        rt.cache.begin_forward(1)
+        for layer in range(rt.num_layers):
+            rt._advance_blocks(layer, 1)
+        g.replay()
+        rt.cache.finish_forward()
+        self.replays += 1
+        return out
+
+
 def install() -> None:
     """Patch the installed transformers' LlamaAttention / LlamaModel forwards
     (idempotent).  Models without a tiered cache keep the stock behaviour."""

@@ -177,6 +177,7 @@ class BatchedTieredKVRuntime:
         self.tick_scratch = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
         self.current_query_length = 0
         self.policy_tick_this_forward = False
+        self.fixed_launch_bound = False
         from .tierkv_policy import TieredKVCache
         self.cache = TieredKVCache(self)
 
@@ -363,9 +364,13 @@ class BatchedTieredKVRuntime:
             self.kv_heads, self.block_size, self.head_dim, stream)
         _lib.check(rc, "tierkv_runtime_append")
         num_blocks = min(self._advance_blocks(layer, tokens), self.max_blocks)
+        # With a fixed launch bound (captured decode steps) the kernel scans the
+        # whole table row and takes each sequence's block count from nblocks on
+        # the device, so the launch is the same at every step.
+        bound = self.max_blocks if self.fixed_launch_bound else num_blocks
         out, sums = tierkv_decode_attention(
             query_states, st.table, st.states, st.lengths, st.hot_k, st.hot_v, st.warm_k, st.warm_v,
-            st.k_scale, st.k_zero, st.v_scale, st.v_zero, num_blocks, num_key_value_groups, scaling,
+            st.k_scale, st.k_zero, st.v_scale, st.v_zero, bound, num_key_value_groups, scaling,
             return_scores=policy_step, cold_mode=self.cold_mode, seq_num_blocks=st.nblocks)
         if policy_step:
             self.last_score_sums = sums   # the probability sums the tick ranked (kept for inspection)

@@ -158,3 +158,46 @@ def test_attention_prefill_scoring_changes_tiers(model, device):
     got = _teacher_forced(model, _tokens(2, device), rt.cache)
     rt.check_errors()
     assert torch.isfinite(got).all()
+
+
+def test_decode_graph_replays_match_eager(model, device):
+    """Captured decode steps (two alternating graphs, eager policy steps in
+    between) give the logits of the eager run, step by step, and leave the
+    runtime in the same state."""
+    print("[hf] decode graph runner vs eager", flush=True)
+    cfg = model.config
+    steps = 30
+    ids = torch.randint(0, 1000, (3, PROMPT + steps), generator=torch.Generator().manual_seed(12)).to(device)
+
+    def make():
+        return BatchedTieredKVRuntime(cfg.num_hidden_layers, 3, cfg.num_key_value_heads, cfg.head_dim,
+                                      PROMPT + steps + 16, hot_fraction=0.2, warm_fraction=0.4,
+                                      policy_mode="hot_warm_cold", policy_interval=8, device=device)
+
+    with torch.no_grad():
+        rt_e = make()
+        rt_e.fixed_launch_bound = True           # the same launches as the graphs
+        model(input_ids=ids[:, :PROMPT], past_key_values=rt_e.cache, use_cache=True, logits_to_keep=1)
+        ref = []
+        for s in range(steps):
+            out = model(input_ids=ids[:, PROMPT + s: PROMPT + s + 1], past_key_values=rt_e.cache, use_cache=True,
+                        logits_to_keep=1)
+            ref.append(out.logits[:, -1].float().clone())
+        rt_g = make()
+        model(input_ids=ids[:, :PROMPT], past_key_values=rt_g.cache, use_cache=True, logits_to_keep=1)
+    runner = hf_llama.DecodeGraphRunner(model, rt_g)
+    for s in range(steps):
+        logits = runner.step(ids[:, PROMPT + s: PROMPT + s + 1])
+        got = logits[:, -1].float()
+        torch.cuda.synchronize()
+        # The decode kernel hands tiles to waves dynamically, so two eager runs
+        # already differ at the fp32 rounding level; compare at model tolerance.
+        print(f"step {s}: max |diff| {(got - ref[s]).abs().max().item():.2e}", flush=True)
+        torch.testing.assert_close(got, ref[s], atol=1e-2, rtol=1e-2)
+    assert runner.replays > 10 and len(runner.graphs) == 2
+    rt_e.check_errors()
+    rt_g.check_errors()
+    for le, lg in zip(rt_e.layers, rt_g.layers):
+        for name in ("table", "states", "lengths", "nblocks", "open", "hot_free", "warm_free", "ctl"):
+            assert torch.equal(getattr(le, name), getattr(lg, name)), name
+    assert rt_g.cache.get_seq_length() == rt_e.cache.get_seq_length() == PROMPT + steps
