@@ -172,6 +172,28 @@ TIERKV_API int32_t tierkv_runtime_append(
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
 
+/* tierkv_runtime_append with the decode step's rotary embedding fused in, for
+ * fp16 models: K is rotated on its way into the pool, q is rotated into q_out
+ * (contiguous fp16 [batch, num_heads, tokens, head_dim]), V is copied.  The
+ * rotation is transformers' apply_rotary_pos_emb in its fp16 op order,
+ * fp16(fp16(x * cos) + fp16(rotate_half(x) * sin)), so both are bit-identical
+ * to it; it replaces the ~10 elementwise launches per layer that the HF hook
+ * (modeling_llama.py:376-377) spends on the rotation.  q / k / v are fp16
+ * [batch, heads, tokens, head_dim] with element strides (head_dim contiguous;
+ * HF's projection views need no copy); cos / sin are fp16 [Bc, tokens,
+ * head_dim] with strides (stride_b 0 broadcasts one row set over the batch).
+ * head_dim a multiple of 16; every stride a multiple of 8 elements; every
+ * pointer 16-byte aligned. */
+TIERKV_API int32_t tierkv_runtime_append_rope(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int32_t num_heads, void* q_out,
+    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+    const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+    const void* cos, const void* sin, int64_t cs_stride_b, int64_t cs_stride_t, int32_t tokens,
+    int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
 /* One policy tick for one layer, entirely on the device: block scores from the
  * decode kernel's probability sums (block_scores_from_probability_sums,
  * tierkv_policy.py:1905-1912), stable-rank tier labels with reserved HOT

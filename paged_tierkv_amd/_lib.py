@@ -77,6 +77,15 @@ SIGNATURES = {
         _P, _P, c_int32,
         _P, _P, c_int64, _P, _P,
         c_int32, c_int32, c_int32, _P]),
+    "tierkv_runtime_append_rope": (c_int32, [
+        _P, c_int64, c_int64, c_int64, c_int32, _P,
+        _P, c_int64, c_int64, c_int64,
+        _P, c_int64, c_int64, c_int64,
+        _P, _P, c_int64, c_int64, c_int32,
+        _P, _P, _P, c_int64,
+        _P, _P, c_int32,
+        _P, _P, c_int64, _P, _P,
+        c_int32, c_int32, c_int32, _P]),
     "tierkv_runtime_tick": (c_int32, [
         _P, c_int64, c_int32,
         _P, _P, _P, c_int64,

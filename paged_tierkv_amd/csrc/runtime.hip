@@ -118,6 +118,7 @@ __global__ __launch_bounds__(CT) void write_hot_kernel(CopyJobs c) {
 // ---------------------------------------------------------------------------
 struct AppendParams {
   const __half* src[2];
+  int64_t ss_b[2], ss_h[2], ss_t[2];   // element strides of the K / V sources [B, kv_heads, T, D]
   int32_t T;
   int32_t* table;
   int32_t* states;
@@ -130,9 +131,47 @@ struct AppendParams {
   int32_t* hot_free;
   int32_t* ctl;
   int32_t batch, kv_heads, bs, D;
+  // Rotary embedding (rope != 0): K is rotated on its way into the pool and
+  // q [B, heads, T, D] (strides qs_*) is rotated into q_out ([B, heads, T, D]
+  // contiguous), with cos / sin [Bc, T, D] (cs_b = 0 broadcasts over the batch).
+  int32_t rope;
+  const __half* q;
+  int64_t qs_b, qs_h, qs_t;
+  __half* q_out;
+  int32_t heads;
+  const __half* cos;
+  const __half* sin;
+  int64_t cs_b, cs_t;
 };
 
 constexpr int APPEND_MAX_BATCH = 4096;   // sequences per append call (LDS bookkeeping)
+
+// Eight consecutive elements [8c, 8c + 8) of a rotated row, in the fp16 op
+// sequence of transformers' apply_rotary_pos_emb:
+//   out = fp16(fp16(x * cos) + fp16(rotate_half(x) * sin)),
+//   rotate_half(x)[d] = -x[d + D/2] (d < D/2), x[d - D/2] (d >= D/2).
+__device__ __forceinline__ uint4 rope8(const __half* row, const __half* cosr, const __half* sinr, int c, int D) {
+  const int C2 = D / 16;                        // chunks per half row
+  const bool lo = c < C2;
+  const uint4 xv = *reinterpret_cast<const uint4*>(row + 8 * c);
+  const uint4 yv = *reinterpret_cast<const uint4*>(row + 8 * (lo ? c + C2 : c - C2));
+  const uint4 cv = *reinterpret_cast<const uint4*>(cosr + 8 * c);
+  const uint4 sv = *reinterpret_cast<const uint4*>(sinr + 8 * c);
+  const __half* x = reinterpret_cast<const __half*>(&xv);
+  const __half* y = reinterpret_cast<const __half*>(&yv);
+  const __half* cs = reinterpret_cast<const __half*>(&cv);
+  const __half* sn = reinterpret_cast<const __half*>(&sv);
+  uint4 ov;
+  __half* o = reinterpret_cast<__half*>(&ov);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float rot = lo ? -__half2float(y[i]) : __half2float(y[i]);
+    const float p = __half2float(__float2half_rn(__half2float(x[i]) * __half2float(cs[i])));
+    const float r = __half2float(__float2half_rn(rot * __half2float(sn[i])));
+    o[i] = __float2half_rn(p + r);
+  }
+  return ov;
+}
 
 __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
   __shared__ int sh[RT / 64 + 1];
@@ -225,7 +264,8 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
   // finite fp16 values, and every consumer masks rows by length.
   const int D = a.D, C = D / 8;
   const int H = a.kv_heads;
-  const int per_seq = 2 * H * T * C;
+  const int per_seq_kv = 2 * H * T * C;
+  const int per_seq = per_seq_kv + (a.rope ? a.heads * T * C : 0);
   const int total = B * per_seq;
   for (int e = tid; e < total; e += RT) {
     const int b = e / per_seq;
@@ -234,6 +274,14 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
     r /= C;
     const int t = r % T;
     r /= T;
+    if (r >= 2 * H) {                          // rotated query row -> q_out
+      const int qh = r - 2 * H;
+      const __half* row = a.q + b * a.qs_b + qh * a.qs_h + t * a.qs_t;
+      const __half* cr = a.cos + b * a.cs_b + t * a.cs_t;
+      const __half* sr = a.sin + b * a.cs_b + t * a.cs_t;
+      reinterpret_cast<uint4*>(a.q_out + ((int64_t(b) * a.heads + qh) * T + t) * D)[c] = rope8(row, cr, sr, c, D);
+      continue;
+    }
     const int h = r % H;
     const int kv = r / H;
     const int g = s_fp[b] + t;
@@ -241,7 +289,12 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
     const int64_t slot = a.table[int64_t(b) * a.stride + tb];
     if (slot < 0 || slot >= a.hot_slots) continue;
     uint4* dst = reinterpret_cast<uint4*>(a.hot[kv] + ((slot * H + h) * int64_t(bs) + g % bs) * D) + c;
-    *dst = reinterpret_cast<const uint4*>(a.src[kv] + ((int64_t(b) * H + h) * T + t) * D)[c];
+    const __half* row = a.src[kv] + b * a.ss_b[kv] + h * a.ss_h[kv] + t * a.ss_t[kv];
+    if (a.rope && kv == 0) {
+      *dst = rope8(row, a.cos + b * a.cs_b + t * a.cs_t, a.sin + b * a.cs_b + t * a.cs_t, c, D);
+    } else {
+      *dst = reinterpret_cast<const uint4*>(row)[c];
+    }
   }
 }
 
@@ -557,6 +610,11 @@ extern "C" int32_t tierkv_runtime_append(
   AppendParams a{};
   a.src[0] = reinterpret_cast<const __half*>(src_k);
   a.src[1] = reinterpret_cast<const __half*>(src_v);
+  for (int kv = 0; kv < 2; ++kv) {
+    a.ss_t[kv] = head_dim;
+    a.ss_h[kv] = int64_t(tokens) * head_dim;
+    a.ss_b[kv] = int64_t(num_kv_heads) * tokens * head_dim;
+  }
   a.T = tokens;
   a.table = block_table;
   a.states = block_states;
@@ -573,6 +631,74 @@ extern "C" int32_t tierkv_runtime_append(
   a.kv_heads = num_kv_heads;
   a.bs = block_size;
   a.D = head_dim;
+  hipLaunchKernelGGL(append_tokens_kernel, dim3(1), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
+  return check_launch("append_tokens_kernel");
+}
+
+extern "C" int32_t tierkv_runtime_append_rope(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int32_t num_heads, void* q_out,
+    const void* k, int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+    const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+    const void* cos, const void* sin, int64_t cs_stride_b, int64_t cs_stride_t, int32_t tokens,
+    int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
+    void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
+  clear_error();
+  if (!q || !q_out || !k || !v || !cos || !sin || !block_table || !block_states || !block_lengths ||
+      !seq_num_blocks || !open_blocks || !hot_k || !hot_v || !hot_free || !ctl)
+    return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (batch <= 0 || tokens <= 0 || table_stride <= 0 || num_heads <= 0) return fail(TIERKV_ERR_INVALID, "empty append");
+  if (batch > APPEND_MAX_BATCH) return fail(TIERKV_ERR_UNSUPPORTED, "append supports at most 4096 sequences per call");
+  if (int64_t(batch) * (2 * num_kv_heads + num_heads) * tokens * (head_dim / 8) >= (int64_t(1) << 31))
+    return fail(TIERKV_ERR_UNSUPPORTED, "append too large for one call");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256 ||
+      head_dim % 16 != 0)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim a multiple of 16 up to 256");
+  const int64_t strides[11] = {q_stride_b, q_stride_h, q_stride_t, k_stride_b, k_stride_h, k_stride_t,
+                               v_stride_b, v_stride_h, v_stride_t, cs_stride_b, cs_stride_t};
+  for (int64_t st : strides)
+    if (st < 0 || st % 8 != 0) return fail(TIERKV_ERR_INVALID, "strides must be non-negative multiples of 8 elements");
+  const void* ptrs[7] = {q, q_out, k, v, cos, sin, hot_k};
+  for (const void* ptr : ptrs)
+    if (!aligned16(ptr)) return fail(TIERKV_ERR_INVALID, "q, k, v, cos, sin, q_out and pools must be 16-byte aligned");
+  if (!aligned16(hot_v)) return fail(TIERKV_ERR_INVALID, "HOT pools must be 16-byte aligned");
+  AppendParams a{};
+  a.src[0] = reinterpret_cast<const __half*>(k);
+  a.src[1] = reinterpret_cast<const __half*>(v);
+  a.ss_b[0] = k_stride_b;
+  a.ss_h[0] = k_stride_h;
+  a.ss_t[0] = k_stride_t;
+  a.ss_b[1] = v_stride_b;
+  a.ss_h[1] = v_stride_h;
+  a.ss_t[1] = v_stride_t;
+  a.T = tokens;
+  a.table = block_table;
+  a.states = block_states;
+  a.lengths = block_lengths;
+  a.stride = table_stride;
+  a.nblocks = seq_num_blocks;
+  a.open = open_blocks;
+  a.hot[0] = reinterpret_cast<__half*>(hot_k);
+  a.hot[1] = reinterpret_cast<__half*>(hot_v);
+  a.hot_slots = hot_slots;
+  a.hot_free = hot_free;
+  a.ctl = ctl;
+  a.batch = batch;
+  a.kv_heads = num_kv_heads;
+  a.bs = block_size;
+  a.D = head_dim;
+  a.rope = 1;
+  a.q = reinterpret_cast<const __half*>(q);
+  a.qs_b = q_stride_b;
+  a.qs_h = q_stride_h;
+  a.qs_t = q_stride_t;
+  a.q_out = reinterpret_cast<__half*>(q_out);
+  a.heads = num_heads;
+  a.cos = reinterpret_cast<const __half*>(cos);
+  a.sin = reinterpret_cast<const __half*>(sin);
+  a.cs_b = cs_stride_b;
+  a.cs_t = cs_stride_t;
   hipLaunchKernelGGL(append_tokens_kernel, dim3(1), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch("append_tokens_kernel");
 }

@@ -147,8 +147,15 @@ def tierkv_attention_forward(self, hidden_states: torch.Tensor, position_embeddi
     key_states = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
     value_states = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
     cos, sin = position_embeddings
-    query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
     dropout = 0.0 if not self.training else self.attention_dropout
+    if (getattr(runtime, "is_batched", False) and getattr(runtime, "fused_rope", False)
+            and query_states.shape[-2] == 1 and query_states.dtype == torch.float16
+            and cos.dtype == torch.float16 and bool(kwargs.get("tierkv_triton_mask_safe", False))):
+        # Decode step: the append kernel applies the rotation (same fp16 ops).
+        out = runtime.decode_layer(self.layer_idx, query_states, key_states, value_states, self.num_key_value_groups,
+                                   self.scaling, policy_step=runtime.policy_tick_this_forward, rope=(cos, sin))
+        return self.o_proj(out.reshape(*input_shape, -1)), None
+    query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
 
     if getattr(runtime, "is_batched", False):
         return _batched_forward(self, runtime, query_states, key_states, value_states, attention_mask,

@@ -84,6 +84,16 @@ def recency_scores(num_blocks: int) -> list[float]:
     return s
 
 
+def _strided_f16(t: torch.Tensor) -> torch.Tensor:
+    """fp16 tensor whose head dimension is contiguous, with strides that are
+    multiples of 8 elements and a 16-byte aligned start (copied otherwise)."""
+    if t.dtype != torch.float16:
+        raise ValueError("the fused rotary append takes fp16 tensors.")
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
 @dataclass
 class LayerStorage:
     hot_k: torch.Tensor
@@ -178,6 +188,8 @@ class BatchedTieredKVRuntime:
         self.current_query_length = 0
         self.policy_tick_this_forward = False
         self.fixed_launch_bound = False
+        # HF hooks: rotate q / k inside the decode append (fp16 models).
+        self.fused_rope = True
         from .tierkv_policy import TieredKVCache
         self.cache = TieredKVCache(self)
 
@@ -345,24 +357,44 @@ class BatchedTieredKVRuntime:
 
     def decode_layer(self, layer: int, query_states: torch.Tensor, key_states: torch.Tensor,
                      value_states: torch.Tensor, num_key_value_groups: int, scaling: float,
-                     policy_step: bool = False) -> torch.Tensor:
+                     policy_step: bool = False, rope=None) -> torch.Tensor:
         """One decode step of one layer: append K/V [B, kv_heads, 1, D], attend
         with query [B, H, 1, D], and on policy steps re-tier the layer.  Returns
-        the attention output [B, 1, H, D]."""
+        the attention output [B, 1, H, D].
+
+        rope: None (q and k already rotated), or the step's (cos, sin)
+        [Bc, tokens, D] fp16 -- then q and k are the unrotated projections and
+        the append kernel applies the rotation (transformers' fp16 op order)
+        while copying K and producing the rotated q."""
         st = self.layers[layer]
         lib = _lib.lib()
         dev = self.device
-        k = key_states.to(torch.float16).contiguous()
-        v = value_states.to(torch.float16).contiguous()
-        tokens = int(k.shape[2])
         stream = _lib.stream_of(dev)
-        rc = lib.tierkv_runtime_append(
-            _lib.ptr(k), _lib.ptr(v), tokens,
-            _lib.ptr(st.table), _lib.ptr(st.states), _lib.ptr(st.lengths), self.max_blocks,
-            _lib.ptr(st.nblocks), _lib.ptr(st.open), self.batch,
-            _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), self.hot_slots, _lib.ptr(st.hot_free), _lib.ptr(st.ctl),
-            self.kv_heads, self.block_size, self.head_dim, stream)
-        _lib.check(rc, "tierkv_runtime_append")
+        tokens = int(key_states.shape[2])
+        table_args = (_lib.ptr(st.table), _lib.ptr(st.states), _lib.ptr(st.lengths), self.max_blocks,
+                      _lib.ptr(st.nblocks), _lib.ptr(st.open), self.batch,
+                      _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), self.hot_slots, _lib.ptr(st.hot_free),
+                      _lib.ptr(st.ctl), self.kv_heads, self.block_size, self.head_dim, stream)
+        if rope is not None:
+            cos, sin = rope
+            q, k, v = (_strided_f16(t) for t in (query_states, key_states, value_states))
+            cos, sin = (_strided_f16(t) for t in (cos, sin))
+            if cos.shape != sin.shape or cos.stride() != sin.stride():
+                raise ValueError("cos and sin must share shape and layout.")
+            q_rot = torch.empty((self.batch, q.shape[1], tokens, self.head_dim), dtype=torch.float16, device=dev)
+            cs_b = 0 if cos.shape[0] == 1 else cos.stride(0)
+            rc = lib.tierkv_runtime_append_rope(
+                _lib.ptr(q), q.stride(0), q.stride(1), q.stride(2), int(q.shape[1]), _lib.ptr(q_rot),
+                _lib.ptr(k), k.stride(0), k.stride(1), k.stride(2),
+                _lib.ptr(v), v.stride(0), v.stride(1), v.stride(2),
+                _lib.ptr(cos), _lib.ptr(sin), cs_b, cos.stride(1), tokens, *table_args)
+            _lib.check(rc, "tierkv_runtime_append_rope")
+            query_states = q_rot
+        else:
+            k = key_states.to(torch.float16).contiguous()
+            v = value_states.to(torch.float16).contiguous()
+            rc = lib.tierkv_runtime_append(_lib.ptr(k), _lib.ptr(v), tokens, *table_args)
+            _lib.check(rc, "tierkv_runtime_append")
         num_blocks = min(self._advance_blocks(layer, tokens), self.max_blocks)
         # With a fixed launch bound (captured decode steps) the kernel scans the
         # whole table row and takes each sequence's block count from nblocks on

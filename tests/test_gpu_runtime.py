@@ -140,3 +140,61 @@ def test_batched_runtime_reports_exhausted_slots(device):
         rt.begin_step()
         rt.decode_layer(0, q, one, one, 1, D ** -0.5)
         rt.check_errors()
+
+
+def test_fused_rope_append_is_bit_exact(device):
+    """decode_layer(rope=(cos, sin)) rotates k into the pool and q for the
+    kernel with transformers' own fp16 op order: pools, tables and the rotated
+    query equal apply_rotary_pos_emb followed by the plain append, bit for
+    bit, with HF's strided projection views as inputs."""
+    transformers = pytest.importorskip("transformers")
+    from transformers import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaRotaryEmbedding, apply_rotary_pos_emb
+
+    B, kv, G, D, bs, prompt = 3, 2, 4, 128, 16, 40
+    H = kv * G
+    cfg = LlamaConfig(hidden_size=H * D, num_attention_heads=H, num_key_value_heads=kv, head_dim=D,
+                      max_position_embeddings=4096, rope_theta=500000.0)
+    rot = LlamaRotaryEmbedding(cfg, device=device)
+    gen = torch.Generator().manual_seed(21)
+    k0 = torch.randn((B, kv, prompt, D), generator=gen).half().to(device)
+    v0 = torch.randn((B, kv, prompt, D), generator=gen).half().to(device)
+    rts = [BatchedTieredKVRuntime(1, B, kv, D, prompt + 64, block_size=bs, hot_fraction=1.0, warm_fraction=0.0,
+                                  policy_mode="hot_warm", policy_interval=1000, device=device) for _ in range(2)]
+    for rt in rts:
+        rt.prefill_layer(0, k0, v0)
+    for step in range(20):
+        pos = torch.full((1, 1), prompt + step, dtype=torch.long, device=device)
+        # HF's layout: projections [B, 1, heads * D] viewed as [B, heads, 1, D].
+        qp = (torch.randn((B, 1, H * D), generator=gen) * 2).half().to(device).view(B, 1, H, D).transpose(1, 2)
+        kp = (torch.randn((B, 1, kv * D), generator=gen) * 2).half().to(device).view(B, 1, kv, D).transpose(1, 2)
+        vp = torch.randn((B, 1, kv * D), generator=gen).half().to(device).view(B, 1, kv, D).transpose(1, 2)
+        cos, sin = rot(qp, pos)
+        q_ref, k_ref = apply_rotary_pos_emb(qp, kp, cos, sin)
+        out_ref = rts[0].decode_layer(0, q_ref, k_ref, vp, G, D ** -0.5)
+        out = rts[1].decode_layer(0, qp, kp, vp, G, D ** -0.5, rope=(cos, sin))
+        torch.testing.assert_close(out.float(), out_ref.float(), atol=2e-3, rtol=1e-2)
+        for rt in rts:
+            rt.end_step()
+    a, b = rts[0].layers[0], rts[1].layers[0]
+    for name in ("table", "states", "lengths", "nblocks", "open", "hot_k", "hot_v"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    # The rotated query itself: run the fused append once more and compare.
+    pos = torch.full((1, 1), prompt + 20, dtype=torch.long, device=device)
+    qp = torch.randn((B, 1, H * D), generator=gen).half().to(device).view(B, 1, H, D).transpose(1, 2)
+    cos, sin = rot(qp, pos)
+    q_ref, _ = apply_rotary_pos_emb(qp, qp[:, :kv], cos, sin)
+    q_rot = torch.empty((B, H, 1, D), dtype=torch.float16, device=device)
+    st = b
+    from paged_tierkv_amd import _lib
+    lib = _lib.lib()
+    kx = torch.zeros((B, kv, 1, D), dtype=torch.float16, device=device)
+    rc = lib.tierkv_runtime_append_rope(
+        _lib.ptr(qp), qp.stride(0), qp.stride(1), qp.stride(2), H, _lib.ptr(q_rot),
+        _lib.ptr(kx), kx.stride(0), kx.stride(1), kx.stride(2), _lib.ptr(kx), kx.stride(0), kx.stride(1), kx.stride(2),
+        _lib.ptr(cos), _lib.ptr(sin), 0, cos.stride(1), 1,
+        _lib.ptr(st.table), _lib.ptr(st.states), _lib.ptr(st.lengths), rts[1].max_blocks, _lib.ptr(st.nblocks),
+        _lib.ptr(st.open), B, _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), rts[1].hot_slots, _lib.ptr(st.hot_free),
+        _lib.ptr(st.ctl), kv, bs, D, _lib.stream_of(device))
+    _lib.check(rc)
+    assert torch.equal(q_rot, q_ref.contiguous())
