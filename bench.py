@@ -44,8 +44,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c4", "c5"], default="c3",
-                   help="c5: end-to-end random-init Llama-3-8B decode through the HF hooks (own JSON line)")
+    p.add_argument("--workload", choices=["c3", "c4", "c2a", "c2b", "c5"], default="c3",
+                   help="c2a / c2b: demotion / scoring microbenchmarks, c5: end-to-end random-init "
+                        "Llama-3-8B decode through the HF hooks (each its own JSON line)")
     p.add_argument("--c5-steps", type=int, default=256)
     p.add_argument("--c5-batch", type=int, default=16)
     p.add_argument("--c5-prompt", type=int, default=2048)
@@ -142,6 +143,175 @@ def copy_calibration(device):
     t = e0.elapsed_time(e1) / 1e3 / 20
     print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "sec": t,
                       "GBps_read_plus_write": 2 * n / t / 1e9}))
+
+
+def graph_timed(fn, n_variants, steps, warmup):
+    """Average device time of fn(i) over `steps` calls (i cycling over
+    n_variants input buffers): the launches of one pass over the variants are
+    captured once in a HIP graph, and replays are timed with HIP events on
+    the current stream, so host launch cost stays outside the measurement."""
+    import torch
+
+    for i in range(max(warmup, n_variants)):
+        fn(i % n_variants)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(n_variants):
+            fn(i)
+    reps = max(1, steps // n_variants)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / (reps * n_variants), reps * n_variants
+
+
+def _line(metric, value, unit, steps, warmup, sec, dtype, config, **extra):
+    line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": round(sec * 1e3, 6), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config}
+    line.update(extra)
+    return line
+
+
+C2A_METRIC = "demotion HOT fp16 -> WARM int8 absmax GB/s (% peak), Llama-3-8B KV shape, 2048 of 4096 blocks"
+C2B_METRIC = "block-score + tier-label µs per call, probs [32, 32, 4096] -> per-block mass [32, 256] + labels"
+
+
+def run_c2a(args, device):
+    """BASELINE.json configs[1](a): quantize a seeded 50 % of a 4096-block
+    fp16 pool (8 kv heads, 16 x 128) into int8 absmax WARM slots with fp32
+    per-(block, head) scales, table/state rewrite fused.  One step = one
+    demotion launch; 3 source pools are rotated (805 MB)."""
+    import torch
+
+    from paged_tierkv_amd import kernels, workloads as W
+
+    case = W.config2a()
+    n = len(case.demote_logical)
+    H, bs, D = 8, 16, 128
+    pools = []
+    gen = torch.Generator(device=device)
+    for li in range(3):
+        gen.manual_seed(2000 + li)
+        shp = (case.hot_k.shape[0], H, bs, D)
+        pools.append((torch.randn(shp, generator=gen, device=device, dtype=torch.float16),
+                      torch.randn(shp, generator=gen, device=device, dtype=torch.float16)))
+    del case.hot_k, case.hot_v
+    src = case.table[0, case.demote_logical].to(device)
+    dst = case.warm_slots.to(device)
+    lens = torch.full((n,), bs, dtype=torch.int32, device=device)
+    pos = case.demote_logical.to(torch.int32).to(device)
+    table, states = case.table.to(device), case.states.to(device)
+    warm_k = torch.empty((n, H, bs, D), dtype=torch.int8, device=device)
+    warm_v = torch.empty_like(warm_k)
+    ks = torch.empty((n, H), device=device)
+    vs = torch.empty_like(ks)
+
+    def step(i):
+        kernels.demote_to_warm(pools[i][0], pools[i][1], src, dst, lens, warm_k, warm_v, ks, None, vs, None,
+                               warm_format="absmax_i8", block_table=table, block_states=states, table_pos=pos)
+
+    sec, steps = graph_timed(step, len(pools), args.steps, 20)
+    nbytes = W.demote_ideal_bytes(n, H, bs, D)
+    gbs = nbytes / sec / 1e9
+    log(f"[c2a] {sec * 1e6:.2f} us per demotion launch, {gbs:.1f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of peak)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, ROOT)
+        from oracle import codec
+
+        sample = pools[0][0][src[:128].long()].cpu().numpy()
+        codec.quantize_absmax_i8(sample)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds / 2:
+            codec.quantize_absmax_i8(sample)
+            reps += 1
+        per_tile_set = (time.perf_counter() - t0) / reps
+        cpu_gbs = W.demote_ideal_bytes(128, H, bs, D) / 2 / per_tile_set / 1e9
+        cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+               "sample": f"K codes of 128 of the {n} demoted blocks, {reps} reps "
+                         f"({per_tile_set * 1e3:.1f} ms; oracle NumPy absmax codec, single thread)"}
+    cfg = {"workload": "c2a_demote_llama3_8b_kv", "pool_blocks": int(table.shape[1]), "demoted_blocks": n,
+           "kv_heads": H, "block_size": bs, "head_dim": D, "warm_format": "int8 absmax per (block, kv head)",
+           "source_pools_rotated": len(pools)}
+    print(json.dumps(_line(C2A_METRIC, round(gbs, 2), "GB/s", steps, 20, sec, "f16->i8", cfg,
+                           us_per_call=round(sec * 1e6, 3), ideal_bytes_per_step=nbytes,
+                           roofline={"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
+                                     "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
+                                     "traffic": _profile_traffic("demote_absmax_wave_kernel", cfg["workload"])},
+                           cpu_baseline=cpu)), flush=True)
+
+
+def run_c2b(args, device):
+    """BASELINE.json configs[1](b): per-block probability mass of fp32
+    probabilities [32, 32, 4096] and top-k HOT / bottom-k COLD tier labels
+    (26 HOT incl. blocks 0 and 255, 77 COLD).  One step = the block-mass
+    launch plus the label launch; 20 probability buffers are rotated
+    (336 MB)."""
+    import numpy as np
+    import torch
+
+    from paged_tierkv_amd import kernels, workloads as W
+
+    base = W.config2b().to(device)
+    bufs = [base] + [torch.softmax(torch.randn(base.shape, generator=torch.Generator(device=device).manual_seed(3000 + i),
+                                               device=device) * 3.0, dim=-1) for i in range(19)]
+    B, H, T = base.shape
+    nblk = T // 16
+    mass = torch.empty((B, nblk), device=device)
+    cur = torch.zeros((B, nblk), dtype=torch.int32, device=device)
+    labels = torch.empty_like(cur)
+
+    def step(i):
+        kernels.block_mass_from_probs(bufs[i], 16, out=mass)
+        kernels.tier_labels(mass, cur, W.C2B_HOT_BUDGET, W.C2B_WARM_BUDGET, "hot_warm_cold", out=labels)
+
+    sec, steps = graph_timed(step, len(bufs), args.steps, 20)
+    nbytes = W.score_ideal_bytes(B, H, T, 16)
+    gbs = nbytes / sec / 1e9
+    log(f"[c2b] {sec * 1e6:.2f} us per scoring step, {gbs:.1f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of peak)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle import policy as opolicy
+
+        p = base.cpu().numpy()
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds / 2:
+            m = opolicy.block_mass_from_probs(p, 16)
+            opolicy.tier_labels(m, np.zeros((B, nblk), np.int32), W.C2B_HOT_BUDGET, W.C2B_WARM_BUDGET,
+                                "hot_warm_cold")
+            reps += 1
+        per = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(per * 1e6, 1), "unit": "µs per call", "cores": 1, "kind": "port",
+               "sample": f"the full C2(b) input, {reps} reps (oracle NumPy block mass + stable-rank labels, "
+                         f"single thread)"}
+    cfg = {"workload": "c2b_block_score_labels", "batch": B, "num_heads": H, "tokens": T, "block_size": 16,
+           "hot_budget": W.C2B_HOT_BUDGET, "warm_budget": W.C2B_WARM_BUDGET, "prob_buffers_rotated": len(bufs)}
+    line = _line(C2B_METRIC, round(sec * 1e6, 3), "µs", steps, 20, sec, "f32", cfg,
+                 GBps=round(gbs, 2), ideal_bytes_per_step=nbytes,
+                 roofline={"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4),
+                           "traffic": _profile_traffic("block_mass_kernel", cfg["workload"])},
+                 cpu_baseline=cpu)
+    line["higher_is_better"] = False
+    print(json.dumps(line), flush=True)
+
+
+def _profile_traffic(kernel, workload):
+    """HBM bytes per launch from a committed copy-calibrated PMC summary
+    (profiles/<kernel>_<workload>_traffic.json), or None."""
+    tpath = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
 
 
 C5_METRIC = ("C5 end-to-end decode tokens/s + resident KV bytes, random-init Llama-3-8B, batch 16, "
@@ -305,6 +475,12 @@ def main():
         return
     if args.workload == "c5":
         run_c5(args, device)
+        return
+    if args.workload == "c2a":
+        run_c2a(args, device)
+        return
+    if args.workload == "c2b":
+        run_c2b(args, device)
         return
     log(f"[bench] building {args.layers} layers of {args.workload} on {torch.cuda.get_device_name(0)}")
     layers = build_layers(args, device)

@@ -41,6 +41,54 @@ __global__ __launch_bounds__(256) void block_mass_kernel(const float* __restrict
   }
 }
 
+// The same reduction with four consecutive tokens per thread (block_size a
+// power of two >= 4, probs 16-byte aligned): each thread keeps up to 32
+// 16-byte head-row loads in flight at once, sums every token over the heads
+// in order, folds its four tokens as (t0 + t1) + (t2 + t3) and the lanes of
+// one block with an xor butterfly -- the same pairwise tree as
+// block_mass_kernel, so the results are bit-identical.
+constexpr int MASS_T = 128;   // threads per workgroup (512 tokens)
+constexpr int MASS_BATCH = 32;   // head rows loaded before they are summed
+
+__global__ __launch_bounds__(MASS_T) void block_mass_vec4_kernel(const float* __restrict__ probs,
+                                                                  const int32_t* __restrict__ lengths,
+                                                                  float* __restrict__ out, int heads,
+                                                                  int tokens, int bs, int nblk) {
+  const int b = blockIdx.y;
+  const int tok0 = (blockIdx.x * MASS_T + threadIdx.x) * 4;
+  const bool in = tok0 < tokens;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  if (in) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(probs + int64_t(b) * heads * tokens + tok0);
+    const int64_t row = tokens / 4;
+    for (int h0 = 0; h0 < heads; h0 += MASS_BATCH) {
+      f32x4 v[MASS_BATCH];
+#pragma unroll
+      for (int k = 0; k < MASS_BATCH; ++k)
+        if (h0 + k < heads) v[k] = __builtin_nontemporal_load(p + (h0 + k) * row);
+#pragma unroll
+      for (int k = 0; k < MASS_BATCH; ++k) {
+        if (h0 + k < heads) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a[e] += v[k][e];
+        }
+      }
+    }
+  }
+  const int blk = in ? tok0 / bs : 0;
+  const int pos = tok0 - blk * bs;
+  const int len = !in ? 0 : (lengths ? min(max(lengths[int64_t(b) * nblk + blk], 0), bs) : bs);
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (pos + e >= len) a[e] = 0.f;
+  float acc = (a[0] + a[1]) + (a[2] + a[3]);
+  for (int m = 1; m < bs / 4; m <<= 1) acc += __shfl_xor(acc, m, 64);
+  if (in && pos == 0) {
+    const float s = __fdiv_rn(acc, float(heads));
+    out[int64_t(b) * nblk + blk] = __fdiv_rn(s, float(max(len, 1)));
+  }
+}
+
 __global__ __launch_bounds__(256) void scores_from_sums_kernel(const float* __restrict__ sums, int64_t sums_stride,
                                                                const int32_t* __restrict__ lengths, int64_t len_stride,
                                                                float* __restrict__ out, int heads, int nblk) {
@@ -61,9 +109,9 @@ __global__ __launch_bounds__(256) void tier_labels_kernel(const float* __restric
                                                           int32_t* __restrict__ out, int64_t stride,
                                                           int n, int hot_budget, int warm_budget,
                                                           int mode, int demoted_state) {
-  __shared__ float s[LABEL_MAX_BLOCKS];
+  __shared__ __align__(16) uint64_t key[LABEL_MAX_BLOCKS];
   const int b = blockIdx.x;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) s[i] = scores[int64_t(b) * n + i];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) key[i] = label_key(scores[int64_t(b) * n + i], i);
   __syncthreads();
   const int extra_hot = max(hot_budget - 2, 0);
   const int warm = max(warm_budget, 0);
@@ -75,12 +123,20 @@ __global__ __launch_bounds__(256) void tier_labels_kernel(const float* __restric
     } else if (n <= 2 || i == 0 || i == n - 1) {
       desired = HOT;                     // reserved {0, n-1}; n <= 2 -> all HOT
     } else {
-      const float si = s[i];
+      // rank among the candidates j in [1, n - 1): every lane walks the same
+      // j, so each LDS read is a broadcast (two keys per read).
+      const uint64_t ki = key[i];
       int rank = 0;
-      for (int j = 1; j < n - 1; ++j) {
-        const float sj = s[j];
-        rank += (sj > si || (sj == si && j < i)) ? 1 : 0;
+      int j = 1;
+      if (n - 1 > 1) rank += key[1] > ki ? 1 : 0;   // leading odd candidate, then aligned pairs
+      j = 2;
+#pragma unroll 8
+      for (; j + 1 < n - 1; j += 2) {
+        const uint64_t* kp = key + j;
+        const uint64_t a0 = kp[0], a1 = kp[1];
+        rank += (a0 > ki ? 1 : 0) + (a1 > ki ? 1 : 0);
       }
+      for (; j < n - 1; ++j) rank += key[j] > ki ? 1 : 0;
       if (rank < extra_hot) desired = HOT;
       else if (mode == 2) desired = (rank < extra_hot + warm) ? WARM : COLD;
       else desired = demoted_state;
@@ -105,6 +161,12 @@ extern "C" int32_t tierkv_block_mass_from_probs(const float* probs, const int32_
   if (tokens % block_size != 0) return fail(TIERKV_ERR_INVALID, "tokens must be a multiple of block_size");
   if (batch > 65535) return fail(TIERKV_ERR_UNSUPPORTED, "batch too large");
   const int nblk = tokens / block_size;
+  if (block_size >= 4 && aligned16(probs)) {
+    dim3 grid((tokens / 4 + MASS_T - 1) / MASS_T, batch);
+    hipLaunchKernelGGL(block_mass_vec4_kernel, grid, dim3(MASS_T), 0, reinterpret_cast<hipStream_t>(stream_),
+                       probs, lengths, out, num_heads, tokens, block_size, nblk);
+    return check_launch("block_mass_vec4_kernel");
+  }
   dim3 grid((tokens + 255) / 256, batch);
   hipLaunchKernelGGL(block_mass_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream_), probs,
                      lengths, out, num_heads, tokens, block_size, nblk);

@@ -17,6 +17,9 @@ namespace tierkv {
 
 constexpr int QT = 256;   // threads per quantize workgroup
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ float r16(float x) { return __half2float(__float2half_rn(x)); }
 
 __device__ __forceinline__ float block_max(float v, float* red) {
@@ -145,6 +148,161 @@ __global__ __launch_bounds__(QT) void demote_absmax_vec_kernel(QuantJobs q) {
   }
 }
 
+// Codes of eight elements of an absmax tile (one 16-byte vector, all
+// finite): byte k of the result is rintf(x_k / s) clamped to [-127, 127],
+// with x_k / s the IEEE (correctly rounded) quotient, computed without the
+// division in all but rare cases.  r = RN(1 / s) and q0 = RN(x * r) each
+// differ from the exact x / s by a relative 2^-24, so for |x| <= amax
+// (|x / s| <= 127 (1 + 2^-24)) |q0 - RN(x / s)| < 2^-16 + 2^-18 < 2^-15.
+// rintf changes value only at half-integers; when q0 lies farther than
+// 2^-13 from the nearest one, RN(x / s) lies strictly on the same side and
+// rintf(q0) == rintf(RN(x / s)), which needs no clamp (|rintf(q0)| <= 127).
+// rintf(q0) comes from adding 1.5 * 2^23 (round to nearest even), whose low
+// byte is then the two's complement code.  A lane with an element near a
+// half-integer (about 2.4e-4 of the elements) recomputes its eight codes
+// with the IEEE division.
+__device__ __forceinline__ uint2 absmax_codes8(u32x4 w, float s, float r) {
+  constexpr float kMagic = 12582912.f;   // 1.5 * 2^23
+  float xs[8], t[8], d[8];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    xs[2 * k] = half_lo(w[k]);
+    xs[2 * k + 1] = half_hi(w[k]);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float q0 = xs[e] * r;
+    t[e] = q0 + kMagic;
+    d[e] = q0 - (t[e] - kMagic);   // q0 - rintf(q0), in [-0.5, 0.5]
+  }
+  const float dmax = fmaxf(fmaxf(fmaxf(fabsf(d[0]), fabsf(d[1])), fmaxf(fabsf(d[2]), fabsf(d[3]))),
+                           fmaxf(fmaxf(fabsf(d[4]), fabsf(d[5])), fmaxf(fabsf(d[6]), fabsf(d[7]))));
+  if (__builtin_expect(dmax >= 0.5f - 0x1p-13f, 0)) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) t[e] = rintf(__fdiv_rn(xs[e], s)) + kMagic;
+  }
+  uint32_t bt[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) bt[e] = __float_as_uint(t[e]);
+  // Low bytes of bt[0..3] -> one word, of bt[4..7] -> the other.
+  const uint32_t lo = perm_b32(perm_b32(bt[3], bt[2], 0x0c0c0400u), perm_b32(bt[1], bt[0], 0x0c0c0400u), 0x05040100u);
+  const uint32_t hi = perm_b32(perm_b32(bt[7], bt[6], 0x0c0c0400u), perm_b32(bt[5], bt[4], 0x0c0c0400u), 0x05040100u);
+  return make_uint2(lo, hi);
+}
+
+// The same codes by the IEEE division and the clamp, for tiles holding an
+// infinity or a NaN.
+__device__ __forceinline__ uint2 absmax_codes8_exact(u32x4 w, float s) {
+  uint32_t out[2] = {0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = (e & 1) ? half_hi(w[e >> 1]) : half_lo(w[e >> 1]);
+    const float n = fminf(fmaxf(rintf(__fdiv_rn(x, s)), -127.f), 127.f);
+    out[e >> 2] |= (static_cast<uint32_t>(static_cast<int>(n)) & 0xffu) << (8 * (e & 3));
+  }
+  return make_uint2(out[0], out[1]);
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), m, 64)));
+  return v;
+}
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+// ABSMAX_I8, one wave per (job, K|V, kv head) tile, four tiles (consecutive
+// heads of one job) per 256-thread workgroup.  The tile stays in registers
+// (NV 16-byte vectors per lane: load i of the wave covers bytes
+// [1024 i, 1024 i + 1024) of the tile), the absmax is a wave reduction, and
+// each wave stores its codes as 8-byte runs (512 contiguous bytes per store
+// instruction).  Needs head_dim % 8 == 0, so every vector lies inside one
+// token row, and a tile of at most 64 * NV vectors.
+//
+// The absmax is taken on the fp16 bit patterns with the sign cleared, which
+// order like unsigned integers for finite values, so it is a packed 16-bit
+// integer max; a result of 0x7c00 or more flags an infinity or a NaN, and
+// such a tile takes the exact path with the fp32 absmax (NaN ignored).
+template <int NV>
+__global__ __launch_bounds__(QT) void demote_absmax_wave_kernel(QuantJobs q, int32_t n_jobs) {
+  const int lane = threadIdx.x & 63;
+  const int tiles_per_job = 2 * q.kv_heads;
+  const int64_t tile = int64_t(blockIdx.x) * (QT / 64) + (threadIdx.x >> 6);
+  const int64_t job = tile / tiles_per_job;
+  if (job >= n_jobs) return;
+  if (q.n_dev && job >= *q.n_dev) return;
+  const int rem = static_cast<int>(tile - job * tiles_per_job);
+  const int kv = rem / q.kv_heads;
+  const int h = rem - kv * q.kv_heads;
+  const int64_t si = q.src_index[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.src_tiles || di < 0 || di >= q.warm_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int64_t E = int64_t(q.bs) * q.D;
+  const int nvec = static_cast<int>(E / 8);
+  const int valid_vec = len * q.D / 8;
+  const u32x4* src = reinterpret_cast<const u32x4*>(q.src[kv] + (si * q.kv_heads + h) * E);
+  u32x2* dst = reinterpret_cast<u32x2*>(reinterpret_cast<int8_t*>(q.warm[kv]) + (di * q.kv_heads + h) * E);
+
+  // Every source byte is read once and every code written once: non-temporal
+  // loads and stores.
+  u32x4 x[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * 64 + lane;
+    x[i] = vi < valid_vec ? __builtin_nontemporal_load(src + vi) : u32x4{0u, 0u, 0u, 0u};
+  }
+  u16x2 m2 = {0, 0};
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t a = x[i][k] & 0x7fff7fffu;
+      m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, a));
+    }
+  }
+  const uint32_t abits = wave_max_u32(max(static_cast<uint32_t>(m2[0]), static_cast<uint32_t>(m2[1])));
+  if (abits < 0x7c00u) {
+    const float amax = __half2float(__ushort_as_half(static_cast<unsigned short>(abits)));
+    const float s = __fdiv_rn(amax, 127.f);
+    const float r = __fdiv_rn(1.f, s);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int vi = i * 64 + lane;
+      if (vi < nvec) {
+        const uint2 c = (vi < valid_vec && s != 0.f) ? absmax_codes8(x[i], s, r) : make_uint2(0u, 0u);
+        __builtin_nontemporal_store(u32x2{c.x, c.y}, dst + vi);
+      }
+    }
+    if (lane == 0) reinterpret_cast<float*>(q.scale[kv])[di * q.kv_heads + h] = s;
+  } else {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) amax = fmaxf(amax, fmaxf(fabsf(half_lo(x[i][k])), fabsf(half_hi(x[i][k]))));
+    }
+    amax = wave_max(amax);
+    const float s = __fdiv_rn(amax, 127.f);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int vi = i * 64 + lane;
+      if (vi < nvec) {
+        const uint2 c = (vi < valid_vec && s != 0.f) ? absmax_codes8_exact(x[i], s) : make_uint2(0u, 0u);
+        dst[vi] = u32x2{c.x, c.y};
+      }
+    }
+    if (lane == 0) reinterpret_cast<float*>(q.scale[kv])[di * q.kv_heads + h] = s;
+  }
+  if (lane == 0 && q.table_pos && h == 0 && kv == 0) {
+    const int32_t pos = q.table_pos[job];
+    if (pos >= 0) {
+      q.table[pos] = static_cast<int32_t>(di);
+      q.states[pos] = WARM;
+    }
+  }
+}
+
 // REF_U8 (quantize_fp16_to_int8, tierkv_policy.py:21-36): one 16-lane group
 // per (token, head) row; one workgroup per (job, kv head, K|V) tile.
 __global__ __launch_bounds__(QT) void demote_ref_kernel(QuantJobs q) {
@@ -261,7 +419,22 @@ int32_t launch_demote(const QuantJobs& q, int n_grid, int32_t warm_format, hipSt
     const bool vec = (q.D % 8 == 0) && aligned16(q.src[0]) && aligned16(q.src[1]) &&
                      (reinterpret_cast<uintptr_t>(q.warm[0]) % 8 == 0) &&
                      (reinterpret_cast<uintptr_t>(q.warm[1]) % 8 == 0);
-    if (vec) hipLaunchKernelGGL(demote_absmax_vec_kernel, grid, dim3(QT), 0, stream, q);
+    const int64_t nvec = int64_t(q.bs) * q.D / 8;
+    const int64_t tiles = int64_t(n_grid) * 2 * q.kv_heads;
+    const dim3 wgrid(static_cast<unsigned>((tiles + QT / 64 - 1) / (QT / 64)));
+    // One wave per tile: the launch's work-item count (64 per tile) must stay below 2^32.
+    if (tiles >= (int64_t(1) << 25)) {
+      if (vec) hipLaunchKernelGGL(demote_absmax_vec_kernel, grid, dim3(QT), 0, stream, q);
+      else hipLaunchKernelGGL(demote_absmax_kernel, grid, dim3(QT), 0, stream, q);
+    } else if (vec && nvec <= 64) {
+      hipLaunchKernelGGL(demote_absmax_wave_kernel<1>, wgrid, dim3(QT), 0, stream, q, n_grid);
+    } else if (vec && nvec <= 128) {
+      hipLaunchKernelGGL(demote_absmax_wave_kernel<2>, wgrid, dim3(QT), 0, stream, q, n_grid);
+    } else if (vec && nvec <= 256) {
+      hipLaunchKernelGGL(demote_absmax_wave_kernel<4>, wgrid, dim3(QT), 0, stream, q, n_grid);
+    } else if (vec && nvec <= 512) {
+      hipLaunchKernelGGL(demote_absmax_wave_kernel<8>, wgrid, dim3(QT), 0, stream, q, n_grid);
+    } else if (vec) hipLaunchKernelGGL(demote_absmax_vec_kernel, grid, dim3(QT), 0, stream, q);
     else hipLaunchKernelGGL(demote_absmax_kernel, grid, dim3(QT), 0, stream, q);
     return check_launch("demote_absmax_kernel");
   }

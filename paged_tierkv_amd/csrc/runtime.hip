@@ -328,45 +328,77 @@ __global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int B = t.batch;
   // 1. Block scores: mean over heads of the per-block probability sums,
-  //    divided by max(length, 1) (block_scores_from_probability_sums).
-  for (int b = 0; b < B; ++b) {
+  //    divided by max(length, 1) (block_scores_from_probability_sums), for
+  //    every (sequence, block) at once; head rows are loaded in batches of 8
+  //    before they are summed.
+  const int64_t NB = int64_t(B) * t.stride;
+  for (int64_t e = tid; e < NB; e += RT) {
+    const int b = static_cast<int>(e / t.stride);
+    const int i = static_cast<int>(e - int64_t(b) * t.stride);
     const int n = min(max(t.nblocks[b], 0), int(t.stride));
-    for (int i = tid; i < n; i += RT) {
-      // The same operations, in the same order, as tierkv_block_scores_from_sums.
-      float acc = 0.f;
-      for (int h = 0; h < t.heads; ++h) acc += t.score_sums[(int64_t(b) * t.heads + h) * t.sums_stride + i];
-      const float sm = __fdiv_rn(acc, float(t.heads));
-      const int len = max(t.lengths[int64_t(b) * t.stride + i], 1);
-      t.scores[int64_t(b) * t.stride + i] = __fdiv_rn(sm, float(len));
+    if (i >= n) continue;
+    // The same operations, in the same order, as tierkv_block_scores_from_sums.
+    const float* p = t.score_sums + int64_t(b) * t.heads * t.sums_stride + i;
+    float acc = 0.f;
+    for (int h0 = 0; h0 < t.heads; h0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = (h0 + k < t.heads) ? p[int64_t(h0 + k) * t.sums_stride] : 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (h0 + k < t.heads) acc += v[k];
     }
+    const float sm = __fdiv_rn(acc, float(t.heads));
+    const int len = max(t.lengths[e], 1);
+    t.scores[e] = __fdiv_rn(sm, float(len));
   }
   __syncthreads();
   // 2. Labels, one wave per sequence: reserved HOT {0, n-1}, candidates
   //    ranked by score descending with ties to the lower index (Python's
-  //    stable sort), COLD never leaves COLD.
+  //    stable sort, as the 64-bit label keys order them), COLD never leaves
+  //    COLD.  The keys of 64 blocks are loaded at once (one per lane) and
+  //    broadcast lane by lane.
   for (int b = w; b < B; b += RT / 64) {
     const int n = min(max(t.nblocks[b], 0), int(t.stride));
     const float* sc = t.scores + int64_t(b) * t.stride;
     const int64_t ob = int64_t(b) * t.stride;
     const int extra_hot = max(t.hot_budget - 2, 0);
-    for (int i = lane; i < n; i += 64) {
-      const int cur = t.states[ob + i];
-      int want;
-      if (n <= 2 || i == 0 || i == n - 1) {
-        want = HOT;
-      } else {
-        const float si = sc[i];
-        int rank = 0;
-        for (int j = 1; j < n - 1; ++j) {
-          const float sj = sc[j];
-          rank += (sj > si || (sj == si && j < i)) ? 1 : 0;
+    const uint64_t k_first = n > 2 ? label_key(sc[0], 0) : 0;
+    const uint64_t k_last = n > 2 ? label_key(sc[n - 1], n - 1) : 0;
+    for (int i0 = 0; i0 < n; i0 += 64) {
+      const int i = i0 + lane;
+      const bool cand = n > 2 && i > 0 && i < n - 1;
+      const uint64_t ki = cand ? label_key(sc[i], i) : ~uint64_t(0);
+      int rank = 0;
+      for (int j0 = 0; j0 < n; j0 += 64) {
+        const int jj = j0 + lane;
+        const uint64_t kj = jj < n ? label_key(sc[jj], jj) : 0;   // 0 ranks above nothing
+        const int lo = static_cast<int>(static_cast<uint32_t>(kj));
+        const int hi = static_cast<int>(static_cast<uint32_t>(kj >> 32));
+#pragma unroll
+        for (int l = 0; l < 64; ++l) {
+          const uint64_t k = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(hi, l))) << 32) |
+                             static_cast<uint32_t>(__builtin_amdgcn_readlane(lo, l));
+          rank += k > ki ? 1 : 0;
         }
-        if (rank < extra_hot) want = HOT;
-        else if (t.mode == 2) want = (rank < extra_hot + max(t.warm_budget, 0)) ? WARM : COLD;
-        else want = WARM;
       }
-      if (cur == COLD) want = COLD;
-      t.labels[ob + i] = want;
+      // blocks 0 and n - 1 are reserved, not candidates
+      rank -= (k_first > ki ? 1 : 0) + (k_last > ki ? 1 : 0);
+      if (i < n) {
+        const int cur = t.states[ob + i];
+        int want;
+        if (!cand) {
+          want = HOT;
+        } else if (rank < extra_hot) {
+          want = HOT;
+        } else if (t.mode == 2) {
+          want = (rank < extra_hot + max(t.warm_budget, 0)) ? WARM : COLD;
+        } else {
+          want = WARM;
+        }
+        if (cur == COLD) want = COLD;
+        t.labels[ob + i] = want;
+      }
     }
   }
   __syncthreads();

@@ -106,6 +106,20 @@ __device__ __forceinline__ float half_hi(uint32_t w) {
   return __half2float(__ushort_as_half(static_cast<unsigned short>(w >> 16)));
 }
 
+// Sort key of tier-label candidate j with score f: the fp32 bits mapped to
+// an unsigned integer of the same order (-0 folded into +0 first, so the two
+// compare equal, as floats do) in the high word and ~j in the low word.
+// Then K_j > K_i  <=>  s_j > s_i  or  (s_j == s_i and j < i): the order of
+// Python's stable descending sort (enforce_budget / enforce_tiered_budget,
+// tierkv_policy.py:1391-1477), so a rank is one 64-bit compare per
+// candidate.  NaN scores, which have no order as floats, are ordered by
+// their bits.
+__device__ __forceinline__ uint64_t label_key(float f, int j) {
+  const uint32_t b = __float_as_uint(f + 0.0f);
+  const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~j);
+}
+
 template <typename T> __device__ __forceinline__ float to_f32(T v);
 template <> __device__ __forceinline__ float to_f32<__half>(__half v) { return __half2float(v); }
 template <> __device__ __forceinline__ float to_f32<__hip_bfloat16>(__hip_bfloat16 v) { return __bfloat162float(v); }

@@ -106,8 +106,10 @@ def promote_to_hot(warm_k, warm_v, k_scale, k_zero, v_scale, v_zero, src_slot, d
     _lib.check(rc, "tierkv_promote_to_hot")
 
 
-def block_mass_from_probs(probs: torch.Tensor, block_size: int, lengths: torch.Tensor | None = None):
-    """fp32 probabilities [B, H, T] -> per-block mass [B, T / block_size]."""
+def block_mass_from_probs(probs: torch.Tensor, block_size: int, lengths: torch.Tensor | None = None,
+                          out: torch.Tensor | None = None):
+    """fp32 probabilities [B, H, T] -> per-block mass [B, T / block_size]
+    (written into ``out`` when given: contiguous fp32 of that shape)."""
     lib = _lib.lib()
     _lib.require_gpu_tensor(probs, "probs")
     if probs.dtype != torch.float32 or probs.ndim != 3:
@@ -117,7 +119,11 @@ def block_mass_from_probs(probs: torch.Tensor, block_size: int, lengths: torch.T
     if tokens % int(block_size):
         raise ValueError("tokens must be a multiple of block_size.")
     nblk = tokens // int(block_size)
-    out = torch.empty((batch, nblk), dtype=torch.float32, device=probs.device)
+    if out is None:
+        out = torch.empty((batch, nblk), dtype=torch.float32, device=probs.device)
+    elif (out.dtype != torch.float32 or tuple(out.shape) != (batch, nblk) or not out.is_contiguous()
+          or out.device != probs.device):
+        raise ValueError("out must be a contiguous fp32 [batch, tokens / block_size] tensor on the probs' device.")
     if lengths is not None:
         lengths = _i32(lengths, probs.device)
         if tuple(lengths.shape) != (batch, nblk):

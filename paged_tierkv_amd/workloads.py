@@ -246,6 +246,23 @@ def config2b(seed=None, batch=32, heads=32, tokens=4096, logit_std=3.0):
     return torch.softmax(logits, dim=-1)
 
 
+def demote_ideal_bytes(n_blocks, kv_heads, block_size, head_dim):
+    """Algorithmic bytes of demoting n_blocks full blocks (K and V) to int8
+    absmax: fp16 tiles read, int8 codes and fp32 per-(block, head) scales
+    written, four int32 job-list entries read and two table entries
+    (slot, state) written per block."""
+    tile = kv_heads * block_size * head_dim
+    return n_blocks * (2 * tile * 2 + 2 * tile + 2 * kv_heads * 4 + 4 * 4 + 2 * 4)
+
+
+def score_ideal_bytes(batch, heads, tokens, block_size):
+    """Algorithmic bytes of one scoring step: fp32 probabilities read, fp32
+    block mass written, then mass and current states read and labels
+    written by the label kernel."""
+    nblk = tokens // block_size
+    return batch * heads * tokens * 4 + batch * nblk * 4 + batch * nblk * (4 + 4 + 4)
+
+
 C2B_HOT_BUDGET = 26     # block 0 and 255 plus 24 by score
 C2B_COLD_COUNT = 77
 C2B_WARM_BUDGET = 256 - C2B_HOT_BUDGET - C2B_COLD_COUNT

@@ -30,7 +30,7 @@ def _eq(a, b, what):
     assert not bad.any(), f"{what}: {int(bad.sum())} of {a.size} differ; first {np.argwhere(bad)[:3].tolist()}"
 
 
-@pytest.mark.parametrize("bs,dim", [(16, 128), (16, 64), (4, 16), (8, 12)])
+@pytest.mark.parametrize("bs,dim", [(16, 128), (16, 64), (4, 16), (8, 12), (32, 128), (16, 256), (64, 128)])
 def test_absmax_demote_bit_exact(device, bs, dim):
     print(f"[quant] absmax bs={bs} dim={dim}", flush=True)
     g = torch.Generator().manual_seed(bs * 100 + dim)
@@ -64,6 +64,37 @@ def test_absmax_demote_bit_exact(device, bs, dim):
         if p >= 0:
             assert t[p] == int(dst[i]) and st[p] == 1
     assert (t[[1, 2, 4]] == -1).all()
+
+
+def test_absmax_demote_half_integer_quotients(device):
+    """Tiles whose absmax is 127 * 2^j have the exact scale 2^j, so every
+    element (k + 0.5) * 2^j has the quotient k + 0.5 exactly: rintf's
+    half-to-even ties, which the kernel's reciprocal fast path must hand to
+    the IEEE division.  Mixed with tiles of near-tie quotients from random
+    scales."""
+    g = torch.Generator().manual_seed(7)
+    tiles, heads, bs, dim = 12, 8, 16, 128
+    k = torch.randint(-127, 127, (tiles, heads, bs, dim), generator=g).double()
+    j = torch.randint(-12, 3, (tiles, heads, 1, 1), generator=g).double()
+    x = (k + 0.5) * torch.pow(2.0, j)
+    x[..., 0, 0] = 127 * torch.pow(2.0, j[..., 0, 0])
+    x = x.half()
+    x[tiles // 2:] = (torch.randn((tiles - tiles // 2, heads, bs, dim), generator=g) * 3).half()
+    idx = torch.arange(tiles, dtype=torch.int32)
+    warm = torch.empty((tiles, heads, bs, dim), dtype=torch.int8, device=device)
+    warm_v = torch.empty_like(warm)
+    ks = torch.empty((tiles, heads), device=device)
+    vs = torch.empty_like(ks)
+    xd = x.to(device)
+    kernels.demote_to_warm(xd, xd, idx, idx, torch.full((tiles,), bs, dtype=torch.int32), warm, warm_v,
+                           ks, None, vs, None, warm_format="absmax_i8")
+    torch.cuda.synchronize()
+    q, scale = codec.quantize_absmax_i8(x.numpy())
+    _eq(warm.cpu().numpy(), q, "half-integer quotient codes")
+    _eq(warm_v.cpu().numpy(), q, "half-integer quotient codes (V)")
+    _eq(ks.cpu().numpy(), scale, "half-integer quotient scales")
+    ties = np.abs(np.abs(x[: tiles // 2].float().numpy() / scale[: tiles // 2, :, None, None]) % 1 - 0.5) == 0
+    assert ties.sum() == (tiles // 2) * heads * (bs * dim - 1), "every element but the absmax is an exact tie"
 
 
 def test_c2a_demotion_full_size_bit_exact(device):

@@ -34,7 +34,7 @@ def test_c2b_block_mass_full_size_bit_exact(device):
 def test_block_mass_with_lengths_bit_exact(device):
     g = torch.Generator().manual_seed(2)
     probs = torch.softmax(torch.randn((3, 5, 64 * 8), generator=g) * 2, dim=-1)
-    for bs in (8, 16, 64):
+    for bs in (2, 4, 8, 16, 32, 64):
         nblk = probs.shape[-1] // bs
         lens = torch.randint(0, bs + 1, (3, nblk), generator=g, dtype=torch.int32)
         got = kernels.block_mass_from_probs(probs.to(device), bs, lens).cpu().numpy()
