@@ -17,6 +17,8 @@
 // ctl = {hot_top, warm_top, error bits, 0}.  Allocation pops from the top in
 // a fixed order (sequence, then logical block), so slot ids are deterministic.
 
+#include <algorithm>
+
 #include "quantize.h"
 
 namespace tierkv {
@@ -173,46 +175,119 @@ __device__ __forceinline__ uint4 rope8(const __half* row, const __half* cosr, co
   return ov;
 }
 
+// K / V item e of an append, e in [0, B * 2 * kv_heads * T * D / 8): eight
+// elements [8c, 8c + 8) of token t of head h of K (kv 0) or V (kv 1) of
+// sequence b.
+struct KVItem {
+  int b, kv, h, t, c;
+};
+
+__device__ __forceinline__ KVItem kv_item(int e, int H, int T, int C) {
+  KVItem it;
+  const int per_seq = 2 * H * T * C;
+  it.b = e / per_seq;
+  int r = e - it.b * per_seq;
+  it.c = r % C;
+  r /= C;
+  it.t = r % T;
+  r /= T;
+  it.h = r % H;
+  it.kv = r / H;
+  return it;
+}
+
+// The 16 bytes item `it` writes into the pool: the source row's elements,
+// rotated for K when the append carries the rotary embedding.
+__device__ __forceinline__ uint4 kv_value(const AppendParams& a, const KVItem& it) {
+  const __half* row = a.src[it.kv] + it.b * a.ss_b[it.kv] + it.h * a.ss_h[it.kv] + it.t * a.ss_t[it.kv];
+  if (a.rope && it.kv == 0)
+    return rope8(row, a.cos + it.b * a.cs_b + it.t * a.cs_t, a.sin + it.b * a.cs_b + it.t * a.cs_t, it.c, a.D);
+  return reinterpret_cast<const uint4*>(row)[it.c];
+}
+
+constexpr int APPEND_PF = 4;                          // K / V items per thread fetched before the bookkeeping
+constexpr int APPEND_NIT = APPEND_MAX_BATCH / RT;     // sequences per thread, at most
+
+// Workgroup 0 does the bookkeeping and the K / V copies: it loads (and
+// rotates) its first APPEND_PF K / V items per thread before the table
+// round trips, since only their destination depends on them, reads each
+// sequence's state once, and keeps the slot of the first block each
+// sequence writes in LDS.  With the rotary embedding, workgroups 1.. rotate
+// the query rows, which depend on nothing else.
 __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
-  __shared__ int sh[RT / 64 + 1];
-  __shared__ int s_ok;
-  __shared__ int s_fb[APPEND_MAX_BATCH];   // first block receiving a token, per sequence
-  __shared__ int s_fp[APPEND_MAX_BATCH];   // row of the first new token in it
   const int tid = threadIdx.x;
   const int B = a.batch, bs = a.bs, T = a.T;
-  // The open block of sequence b (flagged, last, HOT, not full): its free rows.
-  auto open_room = [&](int b, int nb, int& len_open) {
-    len_open = 0;
-    if (nb <= 0 || a.open[b] == 0) return 0;
-    const int64_t o = int64_t(b) * a.stride + nb - 1;
-    const int len = min(max(a.lengths[o], 0), bs);
-    if (a.states[o] != HOT) {
-      if (len < bs) atomicOr(a.ctl + 2, ERR_OPEN_STATE);
-      return 0;
+  const int D = a.D, C = D / 8, H = a.kv_heads;
+  if (blockIdx.x > 0) {
+    const int per_seq = a.heads * T * C;
+    const int total = B * per_seq;
+    for (int e = (blockIdx.x - 1) * RT + tid; e < total; e += (gridDim.x - 1) * RT) {
+      const int b = e / per_seq;
+      int r = e - b * per_seq;
+      const int c = r % C;
+      r /= C;
+      const int t = r % T;
+      const int qh = r / T;
+      const __half* row = a.q + b * a.qs_b + qh * a.qs_h + t * a.qs_t;
+      const __half* cr = a.cos + b * a.cs_b + t * a.cs_t;
+      const __half* sr = a.sin + b * a.cs_b + t * a.cs_t;
+      reinterpret_cast<uint4*>(a.q_out + ((int64_t(b) * a.heads + qh) * T + t) * D)[c] = rope8(row, cr, sr, c, D);
     }
-    len_open = len;
-    return bs - len;
-  };
-  // Phase 1: new blocks needed in total (all-or-nothing check).
+    return;
+  }
+  __shared__ int sh[RT / 64 + 1];
+  __shared__ int s_ok;
+  __shared__ int s_fb[APPEND_MAX_BATCH];     // first block receiving a token, per sequence
+  __shared__ int s_fp[APPEND_MAX_BATCH];     // row of the first new token in it
+  __shared__ int s_slot[APPEND_MAX_BATCH];   // HOT slot of that block
+  const int top = a.ctl[0];
+  const int total_kv = B * 2 * H * T * C;
+  uint4 pf[APPEND_PF];
+#pragma unroll
+  for (int k = 0; k < APPEND_PF; ++k) {
+    const int e = tid + k * RT;
+    if (e < total_kv) pf[k] = kv_value(a, kv_item(e, H, T, C));
+  }
+  // Phase 1: per sequence, the open block (flagged, last, HOT, not full) and
+  // the new blocks needed; all-or-nothing check over the batch.
   if (tid == 0) s_ok = 1;
-  __syncthreads();
-  int run = 0;
-  for (int b0 = 0; b0 < B; b0 += RT) {
-    const int b = b0 + tid;
-    int need = 0;
-    if (b < B) {
-      const int nb = a.nblocks[b];
-      int len_open;
-      const int room = open_room(b, nb, len_open);
-      need = T > room ? (T - room + bs - 1) / bs : 0;
-      if (nb < 0 || nb + need > a.stride) s_ok = 0;
+  int nb[APPEND_NIT], room[APPEND_NIT], len_open[APPEND_NIT], slot_open[APPEND_NIT], need[APPEND_NIT];
+  int excl[APPEND_NIT];
+  const int nit = (B + RT - 1) / RT;
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    nb[it] = room[it] = len_open[it] = need[it] = excl[it] = 0;
+    slot_open[it] = -1;
+    const int b = it * RT + tid;
+    if (it < nit && b < B) {
+      nb[it] = a.nblocks[b];
+      if (nb[it] > 0 && a.open[b] != 0) {
+        const int64_t o = int64_t(b) * a.stride + nb[it] - 1;
+        const int len = min(max(a.lengths[o], 0), bs);
+        if (a.states[o] != HOT) {
+          if (len < bs) atomicOr(a.ctl + 2, ERR_OPEN_STATE);
+        } else {
+          len_open[it] = len;
+          room[it] = bs - len;
+          slot_open[it] = a.table[o];
+        }
+      }
+      need[it] = T > room[it] ? (T - room[it] + bs - 1) / bs : 0;
     }
-    int tot;
-    block_scan(need, sh, &tot);
-    run += tot;
   }
   __syncthreads();
-  const int top = a.ctl[0];
+  int run = 0;
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    if (it < nit) {
+      const int b = it * RT + tid;
+      if (b < B && (nb[it] < 0 || nb[it] + need[it] > a.stride)) s_ok = 0;
+      int tot;
+      excl[it] = run + block_scan(need[it], sh, &tot) - need[it];
+      run += tot;
+    }
+  }
+  __syncthreads();
   if (!s_ok) {
     if (tid == 0) atomicOr(a.ctl + 2, ERR_TABLE_FULL);
     return;
@@ -222,79 +297,53 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
     return;
   }
   // Phase 2: table entries; new blocks pop the stack in sequence order.
-  int base = 0;
-  for (int b0 = 0; b0 < B; b0 += RT) {
-    const int b = b0 + tid;
-    int need = 0, nb = 0, room = 0, len_open = 0;
-    if (b < B) {
-      nb = a.nblocks[b];
-      room = open_room(b, nb, len_open);
-      need = T > room ? (T - room + bs - 1) / bs : 0;
-    }
-    int tot;
-    const int incl = block_scan(need, sh, &tot);
-    if (b < B) {
-      const int off = base + incl - need;
-      const int take_open = min(room, T);
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    const int b = it * RT + tid;
+    if (it < nit && b < B) {
+      const int take_open = min(room[it], T);
       if (take_open > 0) {
-        a.lengths[int64_t(b) * a.stride + nb - 1] = len_open + take_open;
-        s_fb[b] = nb - 1;
-        s_fp[b] = len_open;
+        a.lengths[int64_t(b) * a.stride + nb[it] - 1] = len_open[it] + take_open;
+        s_fb[b] = nb[it] - 1;
+        s_fp[b] = len_open[it];
+        s_slot[b] = slot_open[it];
       } else {
-        s_fb[b] = nb;
+        s_fb[b] = nb[it];
         s_fp[b] = 0;
+        s_slot[b] = need[it] > 0 ? a.hot_free[top - 1 - excl[it]] : -1;
       }
-      for (int j = 0; j < need; ++j) {
-        const int64_t o = int64_t(b) * a.stride + nb + j;
-        a.table[o] = a.hot_free[top - 1 - (off + j)];
+      for (int j = 0; j < need[it]; ++j) {
+        const int64_t o = int64_t(b) * a.stride + nb[it] + j;
+        a.table[o] = a.hot_free[top - 1 - (excl[it] + j)];
         a.states[o] = HOT;
         a.lengths[o] = min(T - take_open - j * bs, bs);
       }
-      a.nblocks[b] = nb + need;
-      const int last_len = need > 0 ? min(T - take_open - (need - 1) * bs, bs) : len_open + take_open;
+      a.nblocks[b] = nb[it] + need[it];
+      const int last_len = need[it] > 0 ? min(T - take_open - (need[it] - 1) * bs, bs) : len_open[it] + take_open;
       a.open[b] = last_len < bs ? 1 : 0;
     }
-    base += tot;
   }
   __syncthreads();
   if (tid == 0) a.ctl[0] = top - run;
-  // Phase 3: copy the new tokens.  Token t of sequence b lands at row
+  // Phase 3: store the K / V items.  Token t of sequence b lands at row
   // fp + t counted from row 0 of its first touched block.  Rows past a
   // block's length are not cleared: pools start zeroed and only ever hold
   // finite fp16 values, and every consumer masks rows by length.
-  const int D = a.D, C = D / 8;
-  const int H = a.kv_heads;
-  const int per_seq_kv = 2 * H * T * C;
-  const int per_seq = per_seq_kv + (a.rope ? a.heads * T * C : 0);
-  const int total = B * per_seq;
-  for (int e = tid; e < total; e += RT) {
-    const int b = e / per_seq;
-    int r = e - b * per_seq;
-    const int c = r % C;
-    r /= C;
-    const int t = r % T;
-    r /= T;
-    if (r >= 2 * H) {                          // rotated query row -> q_out
-      const int qh = r - 2 * H;
-      const __half* row = a.q + b * a.qs_b + qh * a.qs_h + t * a.qs_t;
-      const __half* cr = a.cos + b * a.cs_b + t * a.cs_t;
-      const __half* sr = a.sin + b * a.cs_b + t * a.cs_t;
-      reinterpret_cast<uint4*>(a.q_out + ((int64_t(b) * a.heads + qh) * T + t) * D)[c] = rope8(row, cr, sr, c, D);
-      continue;
-    }
-    const int h = r % H;
-    const int kv = r / H;
-    const int g = s_fp[b] + t;
-    const int tb = s_fb[b] + g / bs;
-    const int64_t slot = a.table[int64_t(b) * a.stride + tb];
-    if (slot < 0 || slot >= a.hot_slots) continue;
-    uint4* dst = reinterpret_cast<uint4*>(a.hot[kv] + ((slot * H + h) * int64_t(bs) + g % bs) * D) + c;
-    const __half* row = a.src[kv] + b * a.ss_b[kv] + h * a.ss_h[kv] + t * a.ss_t[kv];
-    if (a.rope && kv == 0) {
-      *dst = rope8(row, a.cos + b * a.cs_b + t * a.cs_t, a.sin + b * a.cs_b + t * a.cs_t, c, D);
-    } else {
-      *dst = reinterpret_cast<const uint4*>(row)[c];
-    }
+  auto store = [&](const KVItem& it, const uint4& v) {
+    const int g = s_fp[it.b] + it.t;
+    const int blk = g / bs;
+    const int64_t slot = blk == 0 ? s_slot[it.b] : a.table[int64_t(it.b) * a.stride + s_fb[it.b] + blk];
+    if (slot < 0 || slot >= a.hot_slots) return;
+    reinterpret_cast<uint4*>(a.hot[it.kv] + ((slot * H + it.h) * int64_t(bs) + g % bs) * D)[it.c] = v;
+  };
+#pragma unroll
+  for (int k = 0; k < APPEND_PF; ++k) {
+    const int e = tid + k * RT;
+    if (e < total_kv) store(kv_item(e, H, T, C), pf[k]);
+  }
+  for (int e = tid + APPEND_PF * RT; e < total_kv; e += RT) {
+    const KVItem it = kv_item(e, H, T, C);
+    store(it, kv_value(a, it));
   }
 }
 
@@ -731,7 +780,10 @@ extern "C" int32_t tierkv_runtime_append_rope(
   a.sin = reinterpret_cast<const __half*>(sin);
   a.cs_b = cs_stride_b;
   a.cs_t = cs_stride_t;
-  hipLaunchKernelGGL(append_tokens_kernel, dim3(1), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
+  // Workgroup 0: bookkeeping and K / V; the rest: query rotation.
+  const int64_t q_items = int64_t(batch) * num_heads * tokens * (head_dim / 8);
+  const int q_groups = static_cast<int>(std::min<int64_t>((q_items + RT - 1) / RT, 256));
+  hipLaunchKernelGGL(append_tokens_kernel, dim3(1 + q_groups), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
   return check_launch("append_tokens_kernel");
 }
 
