@@ -33,7 +33,6 @@
 #include "tierkv_common.h"
 
 #include <algorithm>
-#include <atomic>
 #include <type_traits>
 #include <cfloat>
 #include <cmath>
@@ -43,6 +42,10 @@ namespace tierkv {
 constexpr int FBS = 16;            // tokens per block on the fast path
 constexpr int MAX_LIST = 512;      // resident blocks per workgroup (LDS list)
 constexpr int MAX_WAVES = 8;
+constexpr int PRE_CHUNKS = 4;      // table-row chunks loaded together by the list build
+constexpr int MERGE_UNROLL = 8;    // split partials loaded together by the merge
+constexpr int SCORE_UNROLL = 4;    // score elements per thread whose loads are in flight together
+constexpr int MAX_SPLIT_UNITS = 1 << 16;   // units per launch when a unit is split
 constexpr float PBOOST = 64.f;     // P is scaled by 2^6 before its fp16 cast
 constexpr float LAZY_T = 8.f;      // log2 headroom of the running maximum
 constexpr float FOLD_MAX = 2.f;    // WARM V scales above this are applied to V
@@ -73,30 +76,21 @@ struct DecodeParams {
   float scale_log2;   // scaling * log2(e)
   float scaling;
   int32_t splits;
+  uint32_t split_magic;   // ceil(2^32 / splits) when num_blocks * splits < 2^32, else 0
   float* ws_acc;      // [units][splits][G][D]
   float* ws_ml;       // [units][splits][G][2]
   float* ws_stage;    // [B][H][num_blocks][2]  (block reference max, block sum)
-  unsigned long long* ws_cnt;   // [units] split arrival counters: (stamp << 32) | arrivals
-  uint32_t stamp;     // launch stamp (never 0)
+  uint32_t* ws_cnt;   // [MAX_SPLIT_UNITS] split arrival counters, zero between launches
   int32_t* ws_err;
   float* score_sums;  // [B][H][table_stride] or null
 };
 
-// Arrival on a split counter whose word holds (launch stamp << 32) | count.
-// A word with another stamp is a leftover of an earlier launch, or bytes of
-// another shape's layout of the shared workspace, and counts as zero: the
-// counters need no reset between launches.  Returns the arrivals before this
-// one in this launch.  The caller has waited for its partial's stores.
-__device__ __forceinline__ int arrive_stamped(unsigned long long* c, uint32_t stamp) {
-  unsigned long long old = __hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  while (true) {
-    const bool fresh = uint32_t(old >> 32) == stamp;
-    const uint32_t before = fresh ? uint32_t(old) : 0u;
-    const unsigned long long nv = (static_cast<unsigned long long>(stamp) << 32) | (before + 1u);
-    if (__hip_atomic_compare_exchange_strong(c, &old, nv, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT))
-      return int(before);
-  }
+// Arrival of a split workgroup on its unit's counter; returns the arrivals
+// before this one.  The counters live in a region of the workspace that no
+// other data shares and are zero between launches: the last arrival of each
+// unit resets its counter.  The caller has waited for its partial's stores.
+__device__ __forceinline__ uint32_t arrive(uint32_t* c) {
+  return __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ int seq_blocks(const DecodeParams& p, int b) {
@@ -445,29 +439,9 @@ __device__ __forceinline__ void cold_adjust(float& M, float& L, float& f, float 
   }
 }
 
-// Per-block probability sum of (head qh, block blk) of sequence b
-// (tierkv_triton.py:121-145) from the final M, L.
-template <bool COLD_ZERO>
-__device__ __forceinline__ float block_score(const DecodeParams& p, int b, int qh, int blk, int nb, float M, float L) {
-  if (blk >= nb || !(L > 0.f)) return 0.f;
-  const int64_t o = int64_t(b) * p.table_stride + blk;
-  const int st = p.states[o];
-  const int len = min(max(p.lengths[o], 0), FBS);
-  if (st == COLD) return COLD_ZERO ? float(len) * __builtin_amdgcn_exp2f(-M) / L : 0.f;
-  if ((st == HOT || st == WARM) && len > 0) {
-    const int64_t slot = p.table[o];
-    const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-    if (slot >= 0 && slot < cap) {
-      const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
-      return load_dev(sp + 1) * __builtin_amdgcn_exp2f(load_dev(sp) - M) / L;
-    }
-  }
-  return 0.f;
-}
-
 // The arguments the list build needs first come ahead of the parameter block
 // so that they can be preloaded into scalar registers at wave launch.
-template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT, int NW>
+template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT, int NW, bool LONG>
 __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     const int32_t* __restrict__ a_table, const int32_t* __restrict__ a_states,
     const int32_t* __restrict__ a_lengths, const void* __restrict__ a_q,
@@ -476,17 +450,19 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   constexpr int DS = D / 16;
   extern __shared__ float s_dyn[];               // [NW][G][D] wave accumulators
   __shared__ int4 s_list[MAX_LIST];              // (block, slot, len, state)
-  __shared__ int s_wcnt[2 * MAX_WAVES];
+  __shared__ int s_wcnt[2][PRE_CHUNKS * MAX_WAVES];   // per (chunk, wave): HOT / WARM counts
   __shared__ int s_wcold[MAX_WAVES];
   __shared__ int s_last;
   __shared__ int s_next[2];                      // next WARM / HOT list position to hand out
   __shared__ float s_m[MAX_WAVES][16];
   __shared__ float s_l[MAX_WAVES][16];
+  __shared__ float s_hm[16];                     // per head: resident (M, L) of the whole unit
+  __shared__ float s_hl[16];
 
   const int G = p.groups;
   const int splits = a_splits;
   const int split = blockIdx.x % splits;
-  const int unit = blockIdx.x / splits;
+  const int unit = int(blockIdx.x) / splits;
   const int b = unit / a_kv_heads;
   const int kvh = unit % a_kv_heads;
   const int tid = threadIdx.x;
@@ -527,60 +503,159 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   int nb = a_num_blocks;
   int seen_hot = 0, seen_warm = 0;
   int cold_part = 0;
-  for (int c0 = 0; c0 < a_num_blocks; c0 += nthreads) {
-    const int idx = c0 + tid;
-    int st = COLD, len = 0, slot = -1;
-    if (idx < a_num_blocks) {
-      const int64_t o = int64_t(b) * a_stride + idx;
-      st = a_states[o];
-      len = a_lengths[o];
-      slot = a_table[o];
-      __builtin_amdgcn_sched_barrier(0);   // all three in flight before any use
+  int bad = 0;   // error bits of this lane's entries (kept in a vector register)
+  const uint32_t hot_cap = uint32_t(min(p.hot_slots, int64_t(0x7fffffff)));
+  const uint32_t warm_cap = uint32_t(min(p.warm_slots, int64_t(0x7fffffff)));
+  // Whether rank r belongs to this split (r % splits == split), and its list
+  // position q = r / splits: one multiply-high by ceil(2^32 / splits) and a
+  // correction (exact while r * splits < 2^32, which the host checks).
+  auto mine = [&](int r, int& q) -> bool {
+    if (splits == 1) {
+      q = r;
+      return true;
     }
-    if (c0 == 0) nb = uniform(min(max(nb_ld, 0), a_num_blocks));
-    len = min(max(len, 0), FBS);
-    bool hot = false, warm = false;
-    const int4 ent = make_int4(idx, slot, len, st);
-    if (idx < nb) {
-      if (st == HOT || st == WARM) {
-        const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-        const bool slot_ok = slot >= 0 && slot < cap;
-        if (!slot_ok && len > 0) atomicOr(p.ws_err, 1);
-        hot = slot_ok && len > 0 && st == HOT;
-        warm = slot_ok && len > 0 && st == WARM;
-      } else if (st == COLD) {
-        cold_part += COLD_ZERO ? len : 0;
-      } else {
-        atomicOr(p.ws_err, 2);
+    if (p.split_magic != 0) {
+      uint32_t qq = __umulhi(uint32_t(r), p.split_magic);
+      if (qq * uint32_t(splits) > uint32_t(r)) qq -= 1u;
+      q = int(qq);
+    } else {
+      q = r / splits;
+    }
+    return r - q * splits == split;
+  };
+  if constexpr (LONG) {
+    // Long rows: PRE_CHUNKS chunks of nthreads entries are loaded before any
+    // is ranked, so a row of up to PRE_CHUNKS * nthreads blocks costs one
+    // memory round trip and one barrier (the long-context rows of 2048
+    // blocks included); the (chunk, wave) counts are scanned across lanes.
+    for (int c0 = 0; c0 < a_num_blocks; c0 += PRE_CHUNKS * nthreads) {
+      const int nch = uniform(min(PRE_CHUNKS, (a_num_blocks - c0 + nthreads - 1) / nthreads));
+      int st[PRE_CHUNKS], len[PRE_CHUNKS], slot[PRE_CHUNKS];
+  #pragma unroll
+      for (int k = 0; k < PRE_CHUNKS; ++k) {
+        st[k] = COLD;
+        len[k] = 0;
+        slot[k] = -1;
+        if (k < nch) {
+          // Past the row's end the last entry is re-read and ignored: the
+          // loads of a chunk need no per-lane branch.
+          const int idx = min(c0 + k * nthreads + tid, a_num_blocks - 1);
+          const int64_t o = int64_t(b) * a_stride + idx;
+          st[k] = a_states[o];
+          len[k] = a_lengths[o];
+          slot[k] = a_table[o];
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);   // every load in flight before any use
+      if (c0 == 0) nb = uniform(min(max(nb_ld, 0), a_num_blocks));
+      // Class of each entry: 1 HOT, 2 WARM, 0 neither.  It is kept per lane
+      // and the ballots are taken again after the barrier, so no lane masks
+      // stay live across it.
+      int cls[PRE_CHUNKS];
+  #pragma unroll
+      for (int k = 0; k < PRE_CHUNKS; ++k) {
+        cls[k] = 0;
+        if (k >= nch) continue;
+        const bool in_row = c0 + k * nthreads + tid < nb;
+        len[k] = min(max(len[k], 0), FBS);
+        const bool tiered = st[k] == HOT || st[k] == WARM;
+        const bool slot_ok = uint32_t(slot[k]) < ((st[k] == HOT) ? hot_cap : warm_cap);
+        const bool use = in_row && tiered && slot_ok && len[k] > 0;
+        cls[k] = use ? ((st[k] == HOT) ? 1 : 2) : 0;
+        bad |= (in_row && tiered && !slot_ok && len[k] > 0) ? 1 : 0;
+        bad |= (in_row && !tiered && st[k] != COLD) ? 2 : 0;
+        if (COLD_ZERO) cold_part += (in_row && st[k] == COLD) ? len[k] : 0;
+        const int nh = __popcll(__ballot(cls[k] == 1));
+        const int nwm = __popcll(__ballot(cls[k] == 2));
+        if (lane == 0) {
+          s_wcnt[0][k * nw + w] = nh;
+          s_wcnt[1][k * nw + w] = nwm;
+        }
+      }
+      __syncthreads();
+      // Exclusive prefix of the (chunk, wave) counts in logical order: lane j
+      // holds count j, a wave-wide scan gives every wave every base.
+      const int nj = nch * nw;
+      const int ch = (lane < nj) ? s_wcnt[0][lane] : 0;
+      const int cw = (lane < nj) ? s_wcnt[1][lane] : 0;
+      const int ih = wave_inclusive_scan(ch);
+      const int iw = wave_inclusive_scan(cw);
+      const uint64_t below = (1ull << lane) - 1ull;
+  #pragma unroll
+      for (int k = 0; k < PRE_CHUNKS; ++k) {
+        if (k >= nch) continue;
+        const int j = uniform(k * nw + w);
+        const int hb = seen_hot + __builtin_amdgcn_readlane(ih - ch, j);
+        const int wb = seen_warm + __builtin_amdgcn_readlane(iw - cw, j);
+        const int4 ent = make_int4(c0 + k * nthreads + tid, slot[k], len[k], st[k]);
+        const uint64_t mh = __ballot(cls[k] == 1);
+        const uint64_t mw = __ballot(cls[k] == 2);
+        int q;
+        if (cls[k] == 1) {
+          if (mine(hb + __popcll(mh & below), q)) s_list[q] = ent;
+        } else if (cls[k] == 2) {
+          if (mine(wb + __popcll(mw & below), q)) s_list[MAX_LIST - 1 - q] = ent;
+        }
+      }
+      seen_hot += __builtin_amdgcn_readlane(ih, 63);
+      seen_warm += __builtin_amdgcn_readlane(iw, 63);
+      if (c0 + PRE_CHUNKS * nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
     }
-    const uint64_t mh = __ballot(hot);
-    const uint64_t mw = __ballot(warm);
-    if (lane == 0) {
-      s_wcnt[w] = __popcll(mh);
-      s_wcnt[MAX_WAVES + w] = __popcll(mw);
-    }
-    __syncthreads();
-    int hb = seen_hot, wb = seen_warm;
+  } else {
+    // Short rows: one chunk of nthreads entries per pass (load, classify,
+    // rank); the per-wave counts are summed from LDS.
+    for (int c0 = 0; c0 < a_num_blocks; c0 += nthreads) {
+      const int idx = c0 + tid;
+      int st = COLD, len = 0, slot = -1;
+      if (idx < a_num_blocks) {
+        const int64_t o = int64_t(b) * a_stride + idx;
+        st = a_states[o];
+        len = a_lengths[o];
+        slot = a_table[o];
+        __builtin_amdgcn_sched_barrier(0);   // all three in flight before any use
+      }
+      if (c0 == 0) nb = uniform(min(max(nb_ld, 0), a_num_blocks));
+      len = min(max(len, 0), FBS);
+      bool hot = false, warm = false;
+      if (idx < nb) {
+        if (st == HOT || st == WARM) {
+          const bool slot_ok = uint32_t(slot) < ((st == HOT) ? hot_cap : warm_cap);
+          bad |= (!slot_ok && len > 0) ? 1 : 0;
+          hot = slot_ok && len > 0 && st == HOT;
+          warm = slot_ok && len > 0 && st == WARM;
+        } else if (st == COLD) {
+          cold_part += COLD_ZERO ? len : 0;
+        } else {
+          bad |= 2;
+        }
+      }
+      const uint64_t mh = __ballot(hot);
+      const uint64_t mw = __ballot(warm);
+      if (lane == 0) {
+        s_wcnt[0][w] = __popcll(mh);
+        s_wcnt[1][w] = __popcll(mw);
+      }
+      __syncthreads();
+      int hb = seen_hot, wb = seen_warm;
 #pragma unroll
-    for (int i = 0; i < nw; ++i) {
-      const int ch = s_wcnt[i], cw = s_wcnt[MAX_WAVES + i];
-      hb += (i < w) ? ch : 0;
-      wb += (i < w) ? cw : 0;
-      seen_hot += ch;
-      seen_warm += cw;
+      for (int i = 0; i < nw; ++i) {
+        const int ch = s_wcnt[0][i], cw = s_wcnt[1][i];
+        hb += (i < w) ? ch : 0;
+        wb += (i < w) ? cw : 0;
+        seen_hot += ch;
+        seen_warm += cw;
+      }
+      const uint64_t below = (1ull << lane) - 1ull;
+      const int4 ent = make_int4(idx, slot, len, st);
+      int q;
+      if (hot && mine(hb + __popcll(mh & below), q)) s_list[q] = ent;
+      if (warm && mine(wb + __popcll(mw & below), q)) s_list[MAX_LIST - 1 - q] = ent;
+      if (c0 + nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
     }
-    const uint64_t below = (1ull << lane) - 1ull;
-    if (hot) {
-      const int r = hb + __popcll(mh & below);
-      if (r % splits == split) s_list[r / splits] = ent;
-    }
-    if (warm) {
-      const int r = wb + __popcll(mw & below);
-      if (r % splits == split) s_list[MAX_LIST - 1 - r / splits] = ent;
-    }
-    if (c0 + nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
   }
+  // Bit 1: a resident block with an out-of-range slot (skipped); bit 2: a
+  // state that is none of HOT, WARM, COLD.
+  if (bad) atomicOr(p.ws_err, bad);
   if (COLD_ZERO) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) cold_part += __shfl_xor(cold_part, m, 64);
@@ -764,6 +839,54 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   };
   QT* out = reinterpret_cast<QT*>(p.out) + (int64_t(b) * p.num_heads + kvh * G) * D;
 
+  // Per-block probability sums of this unit's heads (tierkv_triton.py:121-145)
+  // from each head's resident (M, L) in s_hm / s_hl.  The loads of
+  // SCORE_UNROLL elements per thread are in flight together.
+  auto finalize_scores = [&]() {
+    const int stride = int(p.table_stride);
+    const int total = G * stride;
+    const int last_blk = max(nb - 1, 0);
+    for (int c0 = 0; c0 < total; c0 += SCORE_UNROLL * nthreads) {
+      int stv[SCORE_UNROLL], lnv[SCORE_UNROLL], slv[SCORE_UNROLL];
+      float smv[SCORE_UNROLL], ssv[SCORE_UNROLL];
+#pragma unroll
+      for (int k = 0; k < SCORE_UNROLL; ++k) {
+        // Clamped indices: every load is in bounds and none needs a branch.
+        const int i = min(c0 + k * nthreads + tid, total - 1);
+        const int h = i / stride;
+        const int blk = min(i - h * stride, last_blk);
+        const int64_t o = int64_t(b) * p.table_stride + blk;
+        stv[k] = p.states[o];
+        lnv[k] = p.lengths[o];
+        slv[k] = p.table[o];
+        const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + kvh * G + h) * p.num_blocks + blk) * 2;
+        smv[k] = load_dev(sp);
+        ssv[k] = load_dev(sp + 1);
+      }
+#pragma unroll
+      for (int k = 0; k < SCORE_UNROLL; ++k) {
+        const int i = c0 + k * nthreads + tid;
+        if (i >= total) continue;
+        const int h = i / stride;
+        const int blk = i - h * stride;
+        float M = s_hm[h], L = s_hl[h], f;
+        cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
+        float v = 0.f;
+        if (blk < nb && L > 0.f) {
+          const int st = stv[k];
+          const int len = min(max(lnv[k], 0), FBS);
+          if (st == COLD) {
+            v = COLD_ZERO ? float(len) * __builtin_amdgcn_exp2f(-M) / L : 0.f;
+          } else if ((st == HOT || st == WARM) && len > 0) {
+            const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
+            if (slv[k] >= 0 && slv[k] < cap) v = ssv[k] * __builtin_amdgcn_exp2f(smv[k] - M) / L;
+          }
+        }
+        p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] = v;
+      }
+    }
+  };
+
   if (splits == 1) {
     for (int i = tid; i < G * D; i += nthreads) {
       const int h = i / D;
@@ -774,16 +897,14 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
     }
     if (SCORES) {
-      const int stride = int(p.table_stride);
-      for (int i = tid; i < G * stride; i += nthreads) {
-        const int h = i / stride;
-        const int blk = i - h * stride;
-        float M, L, f, fw[NW];
-        wave_ml(h, M, L, fw);
-        cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
-        p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] =
-            block_score<COLD_ZERO>(p, b, kvh * G + h, blk, nb, M, L);
+      if (tid < G) {
+        float M, L, fw[NW];
+        wave_ml(tid, M, L, fw);
+        s_hm[tid] = M;
+        s_hl[tid] = L;
       }
+      __syncthreads();
+      finalize_scores();
     }
     return;
   }
@@ -804,45 +925,60 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    const int prev = arrive_stamped(p.ws_cnt + unit, p.stamp);
-    s_last = (prev == splits - 1) ? 1 : 0;
+    uint32_t* cnt = p.ws_cnt + unit;
+    const bool last = arrive(cnt) == uint32_t(splits - 1);
+    if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
   }
   __syncthreads();
   if (!s_last) return;
-  auto split_ml = [&](int h, float& M, float& L) {
-    M = -INFINITY;
-    for (int sp = 0; sp < splits; ++sp) M = fmaxf(M, load_dev(p.ws_ml + ((int64_t(unit) * splits + sp) * G + h) * 2));
-    L = 0.f;
-    for (int sp = 0; sp < splits; ++sp) {
-      const float* ml = p.ws_ml + ((int64_t(unit) * splits + sp) * G + h) * 2;
-      const float ms = load_dev(ml);
-      L += (ms == -INFINITY) ? 0.f : load_dev(ml + 1) * __builtin_amdgcn_exp2f(ms - M);
-    }
-  };
+  // Log-sum-exp merge of the splits' partials (tierkv_triton.py:231-264).
+  // Each output element loads every split's (m, l, acc) at once (MERGE_UNROLL
+  // splits per round trip) and merges them in registers; the threads of
+  // dimension 0 keep their head's (M, L) for the scores.
   for (int i = tid; i < G * D; i += nthreads) {
     const int h = i / D;
-    float M, L, f;
-    split_ml(h, M, L);
-    float A = 0.f;
-    for (int sp = 0; sp < splits; ++sp) {
-      const int64_t pi = (int64_t(unit) * splits + sp) * G + h;
-      const float ms = load_dev(p.ws_ml + pi * 2);
-      if (ms != -INFINITY) A += load_dev(p.ws_acc + pi * D + (i - h * D)) * __builtin_amdgcn_exp2f(ms - M);
+    const int d = i - h * D;
+    float M = -INFINITY, L = 0.f, A = 0.f;
+    for (int sp0 = 0; sp0 < splits; sp0 += MERGE_UNROLL) {
+      float av[MERGE_UNROLL], mv[MERGE_UNROLL], lv[MERGE_UNROLL];
+#pragma unroll
+      for (int k = 0; k < MERGE_UNROLL; ++k) {
+        const int64_t pi = (int64_t(unit) * splits + min(sp0 + k, splits - 1)) * G + h;
+        av[k] = load_dev(p.ws_acc + pi * D + d);
+        mv[k] = load_dev(p.ws_ml + pi * 2);
+        lv[k] = load_dev(p.ws_ml + pi * 2 + 1);
+      }
+      float Mn = M;
+#pragma unroll
+      for (int k = 0; k < MERGE_UNROLL; ++k)
+        if (sp0 + k < splits) Mn = fmaxf(Mn, mv[k]);
+      if (Mn != -INFINITY) {
+        const float rescale = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+        A *= rescale;
+        L *= rescale;
+#pragma unroll
+        for (int k = 0; k < MERGE_UNROLL; ++k) {
+          if (sp0 + k < splits && mv[k] != -INFINITY) {
+            const float wgt = __builtin_amdgcn_exp2f(mv[k] - Mn);
+            A += av[k] * wgt;
+            L += lv[k] * wgt;
+          }
+        }
+        M = Mn;
+      }
     }
+    if (SCORES && d == 0) {
+      s_hm[h] = M;
+      s_hl[h] = L;
+    }
+    float f;
     cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
     out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
   }
   if (SCORES) {
-    const int stride = int(p.table_stride);
-    for (int i = tid; i < G * stride; i += nthreads) {
-      const int h = i / stride;
-      const int blk = i - h * stride;
-      float M, L, f;
-      split_ml(h, M, L);
-      cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
-      p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] =
-          block_score<COLD_ZERO>(p, b, kvh * G + h, blk, nb, M, L);
-    }
+    __syncthreads();
+    finalize_scores();
   }
 }
 
@@ -1034,8 +1170,10 @@ static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks
   if (fast_path_ok(block_size, head_dim, groups)) {
     const Plan pl = plan_launch(batch, kv_heads, num_blocks, groups, splits_hint);
     const int64_t units = int64_t(batch) * kv_heads;
+    // The arrival counters come first and have the same place and size in
+    // every layout, so a launch of any shape finds them zero.
     l.cnt = off;
-    off = up(off + units * 8);
+    off = up(off + int64_t(MAX_SPLIT_UNITS) * 4);
     l.acc = off;
     if (pl.splits > 1) off = up(off + units * pl.splits * groups * head_dim * 4);
     l.ml = off;
@@ -1049,16 +1187,25 @@ static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks
   return l;
 }
 
-template <int D, int WF, bool SC, bool CZ, typename QT>
-static void launch_fast(const DecodeParams& p, int nw, int grid, hipStream_t stream) {
-  const size_t shmem = size_t(nw) * p.groups * D * sizeof(float);
+template <int D, int WF, bool SC, bool CZ, typename QT, int NW>
+static void launch_nw(const DecodeParams& p, bool long_rows, int grid, hipStream_t stream) {
+  const size_t shmem = size_t(NW) * p.groups * D * sizeof(float);
   const int32_t stride = int32_t(p.table_stride);
-  if (nw == 8)
-    hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, 8>), dim3(grid), dim3(8 * 64), shmem, stream,
+  if (long_rows)
+    hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, true>), dim3(grid), dim3(NW * 64), shmem, stream,
                        p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, p.kv_heads, p.splits, p);
   else
-    hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, 4>), dim3(grid), dim3(4 * 64), shmem, stream,
+    hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, false>), dim3(grid), dim3(NW * 64), shmem, stream,
                        p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, p.kv_heads, p.splits, p);
+}
+
+// Rows longer than one chunk of the workgroup's threads take the long-row
+// list build.
+template <int D, int WF, bool SC, bool CZ, typename QT>
+static void launch_fast(const DecodeParams& p, int nw, int grid, hipStream_t stream) {
+  const bool long_rows = p.num_blocks > nw * 64;
+  if (nw == 8) launch_nw<D, WF, SC, CZ, QT, 8>(p, long_rows, grid, stream);
+  else launch_nw<D, WF, SC, CZ, QT, 4>(p, long_rows, grid, stream);
 }
 
 template <int D, int WF, typename QT>
@@ -1174,7 +1321,7 @@ extern "C" int32_t tierkv_decode_attention(
   p.scale_log2 = scaling * LOG2E;
   char* ws = reinterpret_cast<char*>(workspace);
   p.ws_err = reinterpret_cast<int32_t*>(ws + wl.err);
-  p.ws_cnt = reinterpret_cast<unsigned long long*>(ws + wl.cnt);
+  p.ws_cnt = reinterpret_cast<uint32_t*>(ws + wl.cnt);
   p.ws_acc = reinterpret_cast<float*>(ws + wl.acc);
   p.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   p.ws_stage = reinterpret_cast<float*>(ws + wl.stage);
@@ -1193,16 +1340,40 @@ extern "C" int32_t tierkv_decode_attention(
     }
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, p.groups, splits_hint);
     p.splits = pl.splits;
-    // Launch stamp: a bijection of the launch count (odd multiplier mod 2^32),
-    // never 0; the split counters carry it.
-    static std::atomic<uint32_t> launches{0};
-    uint32_t c = launches.fetch_add(1) + 1;
-    if (c == 0) c = launches.fetch_add(1) + 1;
-    p.stamp = c * 0x9E3779B1u;
-    const int64_t grid = int64_t(batch) * num_kv_heads * pl.splits;
-    if (grid > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
-    if (bf16) dispatch_fast<__hip_bfloat16>(p, warm_format, scores, cz, pl.nw, int(grid), stream);
-    else dispatch_fast<__half>(p, warm_format, scores, cz, pl.nw, int(grid), stream);
+    p.split_magic = 0;
+    if (pl.splits > 1 && int64_t(num_blocks) * pl.splits < (int64_t(1) << 32))
+      p.split_magic = uint32_t(((uint64_t(1) << 32) + uint64_t(pl.splits) - 1) / uint64_t(pl.splits));
+    // Split launches go out in chunks of whole sequences, at most
+    // MAX_SPLIT_UNITS units each (the size of the workspace's counter
+    // region): each chunk is launched on offset pointers, so the kernel sees
+    // a batch of its own.  Unsplit launches need no counters.
+    int64_t seqs_per_chunk = batch;
+    if (pl.splits > 1) {
+      seqs_per_chunk = MAX_SPLIT_UNITS / num_kv_heads;
+      if (seqs_per_chunk < 1) return fail(TIERKV_ERR_UNSUPPORTED, "too many kv heads for a split launch");
+    }
+    if (std::min<int64_t>(seqs_per_chunk, batch) * num_kv_heads * pl.splits > 0x7fffffff)
+      return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
+    const size_t qsz = bf16 ? sizeof(__hip_bfloat16) : sizeof(__half);
+    for (int64_t b0 = 0; b0 < batch; b0 += seqs_per_chunk) {
+      const int64_t nbat = std::min<int64_t>(seqs_per_chunk, batch - b0);
+      DecodeParams pc = p;
+      const int64_t u0 = b0 * num_kv_heads;
+      pc.batch = int32_t(nbat);
+      pc.q = reinterpret_cast<const char*>(p.q) + b0 * num_heads * head_dim * qsz;
+      pc.out = reinterpret_cast<char*>(p.out) + b0 * num_heads * head_dim * qsz;
+      pc.table = p.table + b0 * table_stride;
+      pc.states = p.states + b0 * table_stride;
+      pc.lengths = p.lengths + b0 * table_stride;
+      if (p.seq_nblocks) pc.seq_nblocks = p.seq_nblocks + b0;
+      if (p.score_sums) pc.score_sums = p.score_sums + b0 * num_heads * table_stride;
+      pc.ws_stage = p.ws_stage + b0 * num_heads * int64_t(num_blocks) * 2;
+      pc.ws_acc = p.ws_acc + u0 * pl.splits * p.groups * head_dim;
+      pc.ws_ml = p.ws_ml + u0 * pl.splits * p.groups * 2;
+      const int grid = int(nbat * num_kv_heads * pl.splits);
+      if (bf16) dispatch_fast<__hip_bfloat16>(pc, warm_format, scores, cz, pl.nw, grid, stream);
+      else dispatch_fast<__half>(pc, warm_format, scores, cz, pl.nw, grid, stream);
+    }
     return check_launch("tiered_decode_kernel");
   }
   p.splits = 1;

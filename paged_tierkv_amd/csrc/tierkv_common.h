@@ -55,6 +55,21 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave (lane i gets the sum of
+// lanes 0..i) in DPP moves: four row shifts within each 16-lane row (lanes
+// whose source lies outside the row add 0), then the row totals are carried
+// by the row broadcasts of lane 15 (into rows 1 and 3) and lane 31 (into
+// rows 2 and 3).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);    // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);    // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);    // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);    // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);   // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);   // row_bcast:31
+  return v;
+}
+
 __device__ __forceinline__ f16x4 as_f16x4(uint32_t lo, uint32_t hi);
 
 // v_perm_b32: byte i of the result is byte sel_i of the 8-byte value

@@ -293,9 +293,8 @@ class DecodeGraphRunner:
 
     * The first step runs eagerly (it sizes every workspace); the next two
       are captured and replayed.  Policy steps run eagerly.
-    * Two graphs alternate: the decode kernel's split-arrival counters need
-      consecutive launches on a workspace to carry different stamps, and a
-      graph replays the stamps it captured.
+    * Two graphs alternate, so the logits a step returns stay valid while
+      the next step is replayed.
     * ``step`` returns the graph's static logits tensor: read it before the
       same graph is replayed again (two steps later).
     * Everything runs on the current stream; sequences must be unpadded.

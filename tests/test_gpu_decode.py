@@ -105,6 +105,29 @@ def test_split_invariance(device, splits):
                  what="split vs auto")
 
 
+@pytest.mark.parametrize("cold", ["masked", "zero_logit"])
+def test_scores_many_splits(device, cold):
+    # More splits than a wave has lanes: the merge's per-head (M, L) reduction
+    # takes its strided path, and the score finalisation batches its loads
+    # over many blocks per thread.
+    lengths = torch.full((2, 300), 16, dtype=torch.int32)
+    lengths[:, 7::13] = 5
+    case = W.make_tiered_case("many_splits", 2, 8, 2, 64, 300, 40, 150, seed=41, lengths=lengths,
+                              max_blocks=310)
+    _check(case, "absmax_i8", device, cold_mode=cold, return_scores=True, splits=70)
+
+
+@pytest.mark.parametrize("groups", [4, 16])
+def test_long_row_list_build(device, groups):
+    # A table row longer than the list build's preloaded chunks (4 x 512
+    # entries with 8 waves, 4 x 256 with 4 waves at group 16): the build
+    # loops, and ranks continue across its iterations.
+    case = W.make_tiered_case(f"long_row_g{groups}", 1, groups, 1, 64, 2600, 100, 900, seed=43 + groups,
+                              recent_hot=4)
+    _check(case, "absmax_i8", device, return_scores=True)
+    _check(case, "ref_u8", device, cold_mode="zero_logit", return_scores=True)
+
+
 def test_seq_num_blocks_ragged(device):
     case = W.make_tiered_case("ragged", 4, 16, 4, 64, 48, 8, 24, seed=11)
     snb = [48, 1, 17, 30]
@@ -192,9 +215,10 @@ def test_reference_preservation_geometry(device, states):
 
 def test_workspace_reuse_across_shapes(device):
     # The per-device workspace is shared by launches of every shape; split
-    # launches (several workgroups per unit, arrival counters stamped per
-    # launch) and score launches are interleaved with single-split ones: no
-    # launch may depend on what another layout left in the workspace.
+    # launches (several workgroups per unit, arrival counters that each
+    # launch's last arrivals reset) and score launches are interleaved with
+    # single-split ones: no launch may depend on what another layout left in
+    # the workspace.
     big = W.make_tiered_case("reuse_big", 16, 32, 8, 128, 64, 6, 40, seed=31)
     small = W.make_tiered_case("reuse_small", 3, 16, 4, 128, 48, 4, 30, seed=32)
     split = W.make_tiered_case("reuse_split", 2, 32, 8, 128, 100, 12, 60, seed=33)
