@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c4", "c2a", "c2b", "c5"], default="c3",
+    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "c2b", "c5"], default="c3",
                    help="c2a / c2b: demotion / scoring microbenchmarks, c5: end-to-end random-init "
                         "Llama-3-8B decode through the HF hooks (each its own JSON line)")
     p.add_argument("--c5-steps", type=int, default=256)
@@ -145,11 +145,12 @@ def copy_calibration(device):
                       "GBps_read_plus_write": 2 * n / t / 1e9}))
 
 
-def graph_timed(fn, n_variants, steps, warmup):
+def graph_timed(fn, n_variants, steps, warmup, passes=1):
     """Average device time of fn(i) over `steps` calls (i cycling over
-    n_variants input buffers): the launches of one pass over the variants are
-    captured once in a HIP graph, and replays are timed with HIP events on
-    the current stream, so host launch cost stays outside the measurement."""
+    n_variants input buffers): the launches of `passes` passes over the
+    variants are captured once in a HIP graph, and replays are timed with HIP
+    events on the current stream, so host launch cost stays outside the
+    measurement."""
     import torch
 
     for i in range(max(warmup, n_variants)):
@@ -157,8 +158,10 @@ def graph_timed(fn, n_variants, steps, warmup):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        for i in range(n_variants):
-            fn(i)
+        for _ in range(passes):
+            for i in range(n_variants):
+                fn(i)
+    n_variants *= passes
     reps = max(1, steps // n_variants)
     for _ in range(3):
         g.replay()
@@ -178,6 +181,85 @@ def _line(metric, value, unit, steps, warmup, sec, dtype, config, **extra):
             "vs_baseline": None, "dtype": dtype, "data": "synthetic", "config": config}
     line.update(extra)
     return line
+
+
+C1_METRIC = "tiered decode-attn µs per launch, TinyLlama shape, batch 1, 512-token context (latency-bound)"
+
+
+def run_c1(args, device):
+    """TinyLlama shape (32 q / 4 kv heads, head_dim
+    64), batch 1, 512-token context: 8 HOT fp16 / 16 WARM int8-absmax / 8 COLD
+    (masked) blocks in a dense pool of 64 blocks (physical ids shuffled).  It
+    moves 271 KB, so a launch is latency-bound: the value is the time of one
+    launch replayed from a HIP graph (host launch cost outside); the eager
+    time (host launch included) is reported beside it."""
+    import torch
+
+    from paged_tierkv_amd import kernels, workloads as W
+    from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention, workspace_error_word
+
+    case = W.config1()
+    hot_k, hot_v = case.hot_k.to(device), case.hot_v.to(device)
+    src_k, src_v = case.warm_src_k.to(device), case.warm_src_v.to(device)
+    ns = src_k.shape[0]
+    warm_k = torch.empty(src_k.shape, dtype=torch.int8, device=device)
+    warm_v = torch.empty_like(warm_k)
+    k_scale = torch.empty((ns, case.kv_heads), device=device)
+    v_scale = torch.empty_like(k_scale)
+    idx = torch.arange(ns, dtype=torch.int32, device=device)
+    kernels.demote_to_warm(src_k, src_v, idx, idx, torch.full((ns,), case.block_size, dtype=torch.int32),
+                           warm_k, warm_v, k_scale, None, v_scale, None, warm_format="absmax_i8")
+    dargs = dict(query_states=case.query.to(device), block_table=case.block_table.to(device),
+                 block_states=case.block_states.to(device), block_lengths=case.block_lengths.to(device),
+                 hot_k_pool=hot_k, hot_v_pool=hot_v, warm_k_pool=warm_k, warm_v_pool=warm_v,
+                 k_scale=k_scale, k_zero=None, v_scale=v_scale, v_zero=None,
+                 num_blocks=case.num_blocks, num_key_value_groups=case.groups, scaling=case.scaling)
+
+    def step(i):
+        tierkv_decode_attention(**dargs, cold_mode="masked")
+
+    # 50 launches per graph: a one-launch graph would time the graph launch.
+    sec, steps = graph_timed(step, 1, args.steps, 20, passes=50)
+    for _ in range(20):
+        step(0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        step(0)
+    e1.record()
+    torch.cuda.synchronize()
+    eager = e0.elapsed_time(e1) / 1e3 / args.steps
+    assert workspace_error_word(device) == 0, "kernel flagged an out-of-range slot"
+    nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim)
+    gbs = nbytes / sec / 1e9
+    log(f"[c1] {sec * 1e6:.2f} us per launch (graph), {eager * 1e6:.2f} us eager; {gbs:.1f} GB/s algorithmic")
+    cpu = None
+    if not args.no_cpu_baseline:
+        sys.path.insert(0, os.path.join(ROOT, "tests"))
+        from helpers import oracle_decode, oracle_warm
+
+        warm = oracle_warm(case, "absmax_i8")
+        oracle_decode(case, warm, "absmax_i8", "masked")
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < args.cpu_seconds / 2:
+            oracle_decode(case, warm, "absmax_i8", "masked")
+            reps += 1
+        per = (time.perf_counter() - t0) / reps
+        cpu = {"value": round(per * 1e6, 1), "unit": "µs per launch", "cores": 1, "kind": "port",
+               "sample": f"the whole C1 step, {reps} reps (oracle NumPy decode, single thread)"}
+    cfg = {"workload": case.name, "batch": case.batch, "num_heads": case.num_heads, "kv_heads": case.kv_heads,
+           "head_dim": case.head_dim, "block_size": case.block_size, "blocks_per_seq": case.num_blocks,
+           "tiers_per_seq": list(case.tier_counts()[0]), "warm_format": "int8 absmax per (block, kv head)",
+           "cold": "masked", "pool": "dense, 64 blocks"}
+    line = _line(C1_METRIC, round(sec * 1e6, 3), "µs", steps, 20, sec, "f16", cfg,
+                 us_eager=round(eager * 1e6, 3), ideal_bytes_per_step=nbytes,
+                 roofline={"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4),
+                           "traffic": _profile_traffic("tiered_decode_kernel", case.name)},
+                 cpu_baseline=cpu)
+    line["higher_is_better"] = False
+    print(json.dumps(line), flush=True)
 
 
 C2A_METRIC = "demotion HOT fp16 -> WARM int8 absmax GB/s (% peak), Llama-3-8B KV shape, 2048 of 4096 blocks"
@@ -491,6 +573,9 @@ def main():
         return
     if args.workload == "c5":
         run_c5(args, device)
+        return
+    if args.workload == "c1":
+        run_c1(args, device)
         return
     if args.workload == "c2a":
         run_c2a(args, device)

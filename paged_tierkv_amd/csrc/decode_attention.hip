@@ -1137,7 +1137,10 @@ static bool fast_path_ok(int block_size, int head_dim, int groups) {
 
 // Eight waves per workgroup (four for GQA groups above 8, to bound the LDS
 // accumulators); enough splits to put about 2048 waves (two per SIMD) on the
-// chip, at least 2*nw list entries per split, and at most MAX_LIST.
+// chip, but no more than one per 4*nw blocks of the row (a split costs a
+// partial publish, an arrival and a merge, three dependent memory round
+// trips, which only pays off when each split streams several tiles per
+// wave), and enough that no split's list exceeds MAX_LIST.
 static Plan plan_launch(int batch, int kv_heads, int num_blocks, int groups, int splits_hint) {
   Plan pl;
   pl.nw = groups <= 8 ? 8 : 4;
@@ -1148,7 +1151,7 @@ static Plan plan_launch(int batch, int kv_heads, int num_blocks, int groups, int
   } else {
     const int64_t target_waves = 2048;
     splits = int(std::max<int64_t>(1, (target_waves + units * pl.nw - 1) / (units * pl.nw)));
-    splits = std::min(splits, std::max(1, num_blocks / (2 * pl.nw)));
+    splits = std::min(splits, std::max(1, num_blocks / (4 * pl.nw)));
   }
   splits = std::max(splits, (num_blocks + MAX_LIST - 1) / MAX_LIST);
   splits = std::min(splits, std::max(1, num_blocks));

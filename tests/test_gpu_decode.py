@@ -88,6 +88,9 @@ def test_gqa_dims_formats(device, groups, head_dim, fmt):
                               seed=groups + head_dim, lengths=lengths, max_blocks=nb + 5)
     for cold in ("masked", "zero_logit"):
         _check(case, fmt, device, cold_mode=cold, return_scores=True)
+    # The same case split over two workgroups per unit (partials merged by the
+    # last arrival, score sums finalised from the staged block statistics).
+    _check(case, fmt, device, cold_mode="zero_logit", return_scores=True, splits=2)
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3, 7])
