@@ -103,46 +103,59 @@ __global__ __launch_bounds__(256) void scores_from_sums_kernel(const float* __re
 }
 
 constexpr int LABEL_MAX_BLOCKS = 8192;
+constexpr int LABEL_T = 1024;   // threads per sequence
 
-__global__ __launch_bounds__(256) void tier_labels_kernel(const float* __restrict__ scores,
-                                                          const int32_t* __restrict__ cur,
-                                                          int32_t* __restrict__ out, int64_t stride,
-                                                          int n, int hot_budget, int warm_budget,
-                                                          int mode, int demoted_state) {
+// One workgroup per sequence.  Each candidate's rank is counted by `par`
+// adjacent lanes (par = 1, 2, 4 or 8, as many as the 1024 threads allow),
+// lane k of the group counting the candidates j = 1 + k, 1 + k + par, ...,
+// so the lanes of a wave read consecutive keys; the partial counts are summed
+// over the group with lane shuffles.
+__global__ __launch_bounds__(LABEL_T) void tier_labels_kernel(const float* __restrict__ scores,
+                                                              const int32_t* __restrict__ cur,
+                                                              int32_t* __restrict__ out, int64_t stride,
+                                                              int n, int hot_budget, int warm_budget,
+                                                              int mode, int demoted_state) {
   __shared__ __align__(16) uint64_t key[LABEL_MAX_BLOCKS];
   const int b = blockIdx.x;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) key[i] = label_key(scores[int64_t(b) * n + i], i);
+  const int tid = threadIdx.x;
+  for (int i = tid; i < n; i += LABEL_T) key[i] = label_key(scores[int64_t(b) * n + i], i);
   __syncthreads();
   const int extra_hot = max(hot_budget - 2, 0);
   const int warm = max(warm_budget, 0);
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int c = cur[int64_t(b) * stride + i];
-    int desired;
-    if (mode == 0) {
-      desired = c;                       // hot_only: enforce_policy returns early
-    } else if (n <= 2 || i == 0 || i == n - 1) {
-      desired = HOT;                     // reserved {0, n-1}; n <= 2 -> all HOT
-    } else {
-      // rank among the candidates j in [1, n - 1): every lane walks the same
-      // j, so each LDS read is a broadcast (two keys per read).
+  int lpar = 0;
+  while (lpar < 3 && (n << (lpar + 1)) <= LABEL_T) ++lpar;
+  const int par = 1 << lpar;
+  for (int t0 = 0; t0 < n * par; t0 += LABEL_T) {
+    const int t = t0 + tid;
+    const int i = t >> lpar;
+    const int part = t & (par - 1);
+    const bool ranked = i < n && mode != 0 && n > 2 && i != 0 && i != n - 1;
+    int rank = 0;
+    if (ranked) {
+      // rank among the candidates j in [1, n - 1)
       const uint64_t ki = key[i];
-      int rank = 0;
-      int j = 1;
-      if (n - 1 > 1) rank += key[1] > ki ? 1 : 0;   // leading odd candidate, then aligned pairs
-      j = 2;
-#pragma unroll 8
-      for (; j + 1 < n - 1; j += 2) {
-        const uint64_t* kp = key + j;
-        const uint64_t a0 = kp[0], a1 = kp[1];
-        rank += (a0 > ki ? 1 : 0) + (a1 > ki ? 1 : 0);
-      }
-      for (; j < n - 1; ++j) rank += key[j] > ki ? 1 : 0;
-      if (rank < extra_hot) desired = HOT;
-      else if (mode == 2) desired = (rank < extra_hot + warm) ? WARM : COLD;
-      else desired = demoted_state;
+      int j = 1 + part;
+#pragma unroll 4
+      for (; j < n - 1; j += par) rank += key[j] > ki ? 1 : 0;
     }
-    if (mode != 0 && n > 2 && c == COLD && desired != COLD) desired = COLD;   // COLD is sticky
-    out[int64_t(b) * stride + i] = desired;
+    for (int m = 1; m < par; m <<= 1) rank += __shfl_xor(rank, m, 64);
+    if (i < n && part == 0) {
+      const int c = cur[int64_t(b) * stride + i];
+      int desired;
+      if (mode == 0) {
+        desired = c;                       // hot_only: enforce_policy returns early
+      } else if (!ranked) {
+        desired = HOT;                     // reserved {0, n-1}; n <= 2 -> all HOT
+      } else if (rank < extra_hot) {
+        desired = HOT;
+      } else if (mode == 2) {
+        desired = (rank < extra_hot + warm) ? WARM : COLD;
+      } else {
+        desired = demoted_state;
+      }
+      if (mode != 0 && n > 2 && c == COLD && desired != COLD) desired = COLD;   // COLD is sticky
+      out[int64_t(b) * stride + i] = desired;
+    }
   }
 }
 
@@ -201,7 +214,7 @@ extern "C" int32_t tierkv_tier_labels(const float* scores, const int32_t* cur_st
   if (mode == 1 && demoted_state != WARM && demoted_state != COLD)
     return fail(TIERKV_ERR_INVALID, "demoted_state must be WARM_STATE or COLD_STATE.");
   if (num_blocks > LABEL_MAX_BLOCKS) return fail(TIERKV_ERR_UNSUPPORTED, "too many blocks per sequence for the label kernel");
-  hipLaunchKernelGGL(tier_labels_kernel, dim3(batch), dim3(256), 0, reinterpret_cast<hipStream_t>(stream_), scores,
+  hipLaunchKernelGGL(tier_labels_kernel, dim3(batch), dim3(LABEL_T), 0, reinterpret_cast<hipStream_t>(stream_), scores,
                      cur_states, new_states, states_stride, num_blocks, hot_budget, warm_budget, mode,
                      demoted_state);
   return check_launch("tier_labels_kernel");
