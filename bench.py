@@ -44,7 +44,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "c2b", "c5"], default="c3",
+    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "c2b", "c5", "prefill"], default="c3",
                    help="c2a / c2b: demotion / scoring microbenchmarks, c5: end-to-end random-init "
                         "Llama-3-8B decode through the HF hooks (each its own JSON line)")
     p.add_argument("--c5-steps", type=int, default=256)
@@ -260,6 +260,72 @@ def run_c1(args, device):
                  cpu_baseline=cpu)
     line["higher_is_better"] = False
     print(json.dumps(line), flush=True)
+
+
+PREFILL_METRIC = ("prefill block-score kernel TFLOP/s (% of the fp16 MFMA peak), C5 prefill shape: batch 16, "
+                  "2048 tokens, 32 / 8 heads, head_dim 128")
+PEAK_MFMA_F16_TFLOPS = 2500.0
+
+
+def run_prefill(args, device):
+    """The prefill block-score kernel (tierkv_prefill_block_mass: per-block
+    causal attention mass of one layer's prefill, without materialised
+    probabilities) at C5's prefill shape.  One step = one call for the whole
+    batch.  Algorithmic FLOPs: two passes of q . k over the causal pairs,
+    2 * 2 * B * H * T(T+1)/2 * D."""
+    import torch
+
+    from paged_tierkv_amd import kernels
+
+    B, H, Hkv, T, D = args.c5_batch, 32, 8, args.c5_prompt, 128
+    gen = torch.Generator(device=device).manual_seed(4000)
+    qs = [torch.randn((B, H, T, D), generator=gen, device=device, dtype=torch.float16) for _ in range(2)]
+    ks = [torch.randn((B, Hkv, T, D), generator=gen, device=device, dtype=torch.float16) for _ in range(2)]
+    scaling = D ** -0.5
+
+    def step(i):
+        kernels.prefill_block_mass(qs[i % 2], ks[i % 2], 16, scaling)
+
+    for i in range(3):
+        step(i)
+    torch.cuda.synchronize()
+    steps = max(4, min(args.steps, 20))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3 / steps
+    flops = 2 * 2 * B * H * (T * (T + 1) // 2) * D
+    tf = flops / sec / 1e12
+    log(f"[prefill] {sec * 1e3:.3f} ms per call, {tf:.1f} TFLOP/s ({tf / PEAK_MFMA_F16_TFLOPS:.1%} of the fp16 peak)")
+    cpu = None
+    if not args.no_cpu_baseline:
+        import numpy as np
+        from threadpoolctl import threadpool_limits
+
+        from oracle.policy import prefill_block_mass as oracle_mass
+
+        G = H // Hkv
+        qn = qs[0][:1, :G].float().cpu().numpy()
+        kn = ks[0][:1, :1].float().cpu().numpy()
+        with threadpool_limits(1):
+            t0 = time.perf_counter()
+            oracle_mass(qn, kn, scaling, 16)
+            per = time.perf_counter() - t0
+        sflops = 2 * 2 * G * (T * (T + 1) // 2) * D
+        cpu = {"value": round(sflops / per / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+               "sample": f"one sequence, one kv head ({G} q heads) of the batch, {per:.1f} s "
+                         "(oracle NumPy float64 probabilities, single thread)"}
+    cfg = {"workload": "prefill_block_mass_c5", "batch": B, "num_heads": H, "kv_heads": Hkv, "tokens": T,
+           "head_dim": D, "block_size": 16}
+    print(json.dumps(_line(PREFILL_METRIC, round(tf, 2), "TFLOP/s", steps, 3, sec, "f16", cfg,
+                           ms_per_call=round(sec * 1e3, 4), algorithmic_flops=flops,
+                           roofline={"kernel": "prefill_block_mass_kernel", "bound": "mfma", "achieved": round(tf, 2),
+                                     "peak": PEAK_MFMA_F16_TFLOPS, "unit": "TFLOP/s",
+                                     "frac": round(tf / PEAK_MFMA_F16_TFLOPS, 4), "traffic": None},
+                           cpu_baseline=cpu)), flush=True)
 
 
 C2A_METRIC = "demotion HOT fp16 -> WARM int8 absmax GB/s (% peak), Llama-3-8B KV shape, 2048 of 4096 blocks"
@@ -576,6 +642,9 @@ def main():
         return
     if args.workload == "c1":
         run_c1(args, device)
+        return
+    if args.workload == "prefill":
+        run_prefill(args, device)
         return
     if args.workload == "c2a":
         run_c2a(args, device)

@@ -42,7 +42,9 @@ HIP_SOURCES = {
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
     "runtime.hip": ["-ffp-contract=off"],
-    "prefill_score.hip": [],
+    # MFMA accumulators in ordinary VGPRs: the logits are consumed by VALU
+    # code right away, and accumulators in AGPRs cost a copy per element.
+    "prefill_score.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 CXX_SOURCES = ["block_manager.cpp"]
 

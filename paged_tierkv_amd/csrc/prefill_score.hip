@@ -13,23 +13,27 @@
 // SDPA it falls back to a sink + recency proxy (modeling_llama.py:294-302).
 // Here the probabilities are recomputed on MFMA in two passes over K:
 //   pass 1: per (head, query) log-sum-exp, each lane keeping a running
-//           (max, sum) over the key columns it owns, merged across the 16
-//           lanes of a row once at the end;
-//   pass 2: p = exp2(x - lse2), summed per 16-key tile, a fixed-order wave
-//           reduction per tile into LDS.
+//           (max, sum) over the keys it owns; the maximum is re-based only
+//           when a logit exceeds it by more than PS_LAZY (log2 units), and
+//           the four key-row owners of a query are merged once at the end;
+//   pass 2: p = exp2(x - lse2), summed per 16-key tile in the lane, then one
+//           fixed-order wave reduction per tile into LDS.
 // Workgroup = (sequence, kv head, 64 queries), 4 waves of 16 queries, each
 // wave serving the whole GQA group for its queries with one pass over each
-// K tile.  Partial tile sums go to a workspace [B, H_kv, T/64, T/16] and a
-// second kernel reduces them in a fixed order, so results are deterministic.
+// K tile; the next K tile is loaded while the current one is processed.
+// Partial tile sums go to a workspace [B, H_kv, T/64, T/16] and a second
+// kernel reduces them in a fixed order, so results are deterministic.
 //
-// MFMA 16x16x16: A = Q rows (lane l: query l%16), B = K^T (lane l: key l%16),
-// both with the head dimension visited in the same permuted order
-// d = 32*(s/2) + 8*(l/16) + 4*(s%2) + i, so each lane loads 16-byte runs; the
-// accumulator holds S[q = 4*(l/16) + j][key = l%16].
+// MFMA 16x16x32 (gfx950): A = K tile (lane l: key l%16), B = Q^T (lane l:
+// query l%16), both with the head dimension visited in the same order
+// d = 32*s + 8*(l/16) + i (16-byte loads); the accumulator holds
+// S^T[key = 4*(l/16) + j][query = l%16], so a lane's four logits belong to
+// one query and the per-query sums need no shuffles until the end.
 
 #include "tierkv_common.h"
 
 #include <cmath>
+#include <type_traits>
 
 namespace tierkv {
 
@@ -38,25 +42,25 @@ constexpr int PS_QB = 16 * PS_WAVES;       // queries per workgroup
 constexpr int PS_MAX_TILES = 2048;         // 16-key tiles: T <= 32768
 constexpr int PS_MAX_GROUP = 8;            // GQA group
 
-typedef short bf16x4 __attribute__((ext_vector_type(4)));
+constexpr float PS_LAZY = 8.f;             // log2 headroom of the running maximum
+constexpr float PS_FLOOR = -1e30f;         // initial running maximum (finite)
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 template <typename T>
-__device__ __forceinline__ f32x4 mfma16(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4 c);
+__device__ __forceinline__ f32x4 mfma32(const uint4& a, const uint4& b, f32x4 c);
 
 template <>
-__device__ __forceinline__ f32x4 mfma16<__half>(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(a0, a1), as_f16x4(b0, b1), c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma32<__half>(const uint4& a, const uint4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
 }
 
 template <>
-__device__ __forceinline__ f32x4 mfma16<__hip_bfloat16>(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
-                                                        f32x4 c) {
-  union { uint32_t u[2]; bf16x4 v; } a, b;
-  a.u[0] = a0;
-  a.u[1] = a1;
-  b.u[0] = b0;
-  b.u[1] = b1;
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a.v, b.v, c, 0, 0, 0);
+__device__ __forceinline__ f32x4 mfma32<__hip_bfloat16>(const uint4& a, const uint4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
 }
 
 struct PrefillParams {
@@ -65,146 +69,170 @@ struct PrefillParams {
   int64_t qs_b, qs_h, qs_t;      // element strides of q [B, H, T, D]
   int64_t ks_b, ks_h, ks_t;      // element strides of k [B, H_kv, T, D]
   float* partial;                // [B, H_kv, nqb, ntiles]
-  int32_t heads, kv_heads, tokens, nqb, ntiles;
+  int32_t heads, kv_heads, tokens, nqb, ntiles, batch;
   float scale_log2;
 };
 
-template <int D, typename T, int GMAX>
+// EXACT: the GQA group is exactly GMAX (no per-head guards).
+template <int D, typename T, int GMAX, bool EXACT>
 __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(PrefillParams p) {
-  constexpr int C = D / 32;          // 16-byte loads per row
-  constexpr int DS = D / 16;         // MFMA steps
+  constexpr int KS = D / 32;         // MFMA k-steps (one 16-byte load each)
   __shared__ float s_blk[PS_WAVES][PS_MAX_TILES];
-  const int qb = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // Workgroup -> (query block, kv head, sequence).  The hardware deals
+  // consecutive workgroups to the 8 XCDs in turn; when the (sequence, kv
+  // head) pairs come in multiples of 8, all query blocks of one pair go to
+  // the same XCD, so its K stays in that XCD's L2.  Query blocks run in
+  // reverse: the longest causal rows are dispatched first.
+  const int wg = int(blockIdx.x);
+  const int npairs = p.kv_heads * p.batch;
+  int pair, qi;
+  if ((npairs & 7) == 0) {
+    const int slot = wg >> 3;
+    pair = (slot / p.nqb) * 8 + (wg & 7);
+    qi = slot % p.nqb;
+  } else {
+    pair = wg / p.nqb;
+    qi = wg % p.nqb;
+  }
+  const int qb = p.nqb - 1 - qi, kvh = pair % p.kv_heads, b = pair / p.kv_heads;
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
-  const int G = p.heads / p.kv_heads;
+  const int G = EXACT ? GMAX : p.heads / p.kv_heads;
   const int Tn = p.tokens;
   const int q0 = qb * PS_QB + 16 * w;
 
   for (int i = threadIdx.x; i < PS_WAVES * PS_MAX_TILES; i += 64 * PS_WAVES) (&s_blk[0][0])[i] = 0.f;
 
-  // Q A-operands: row q0 + n (clamped), head kvh * G + gh.
-  uint32_t qa[GMAX][C * 4];
+  // Q^T B-operands: query q0 + n (clamped), head kvh * G + gh.
+  uint4 qv[GMAX][KS];
   {
     const int qrow = min(q0 + n, Tn - 1);
     const T* qbase = reinterpret_cast<const T*>(p.q) + b * p.qs_b + qrow * p.qs_t;
 #pragma unroll
     for (int gh = 0; gh < GMAX; ++gh) {
-      if (gh < G) {
+      if (EXACT || gh < G) {
         const T* row = qbase + int64_t(kvh * G + gh) * p.qs_h;
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-          const uint4 v = *reinterpret_cast<const uint4*>(row + 32 * c + 8 * g);
-          qa[gh][4 * c + 0] = v.x;
-          qa[gh][4 * c + 1] = v.y;
-          qa[gh][4 * c + 2] = v.z;
-          qa[gh][4 * c + 3] = v.w;
-        }
+        for (int s = 0; s < KS; ++s) qv[gh][s] = *reinterpret_cast<const uint4*>(row + 32 * s + 8 * g);
       } else {
 #pragma unroll
-        for (int c = 0; c < 4 * C; ++c) qa[gh][c] = 0u;
+        for (int s = 0; s < KS; ++s) qv[gh][s] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
   }
   __syncthreads();
   // Waves whose queries all lie past the prompt add nothing (their LDS slots stay zero).
   const int last_tile = min((q0 + 15) >> 4, (Tn - 1) >> 4);
+  const int diag = q0 >> 4;                  // the one tile that needs the causal mask
+  const bool row_ok = q0 + n < Tn;
+  const bool rows_ok = q0 + 15 < Tn;        // every query of the wave lies in the prompt
   const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.ks_b + int64_t(kvh) * p.ks_h;
+  const float sl = p.scale_log2;
 
-  auto load_k = [&](int kt, uint32_t* kb) {
+  auto load_k = [&](int kt, uint4* kb) {
     const int krow = min(kt * 16 + n, Tn - 1);
     const T* row = kbase + int64_t(krow) * p.ks_t;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      const uint4 v = *reinterpret_cast<const uint4*>(row + 32 * c + 8 * g);
-      kb[4 * c + 0] = v.x;
-      kb[4 * c + 1] = v.y;
-      kb[4 * c + 2] = v.z;
-      kb[4 * c + 3] = v.w;
-    }
+    for (int s = 0; s < KS; ++s) kb[s] = *reinterpret_cast<const uint4*>(row + 32 * s + 8 * g);
   };
-  auto scores = [&](const uint32_t* kb, int gh) {
+  // The four raw logits q . k of keys kt*16 + 4g + j for this lane's query;
+  // MASK: -inf where masked (past the query, or a query past the prompt).
+  auto logits = [&](auto MASK, const uint4* kb, int gh, int kt, float* x) {
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < DS; ++s) {
-      const int c = s >> 1, h = s & 1;
-      acc = mfma16<T>(qa[gh][4 * c + 2 * h], qa[gh][4 * c + 2 * h + 1], kb[4 * c + 2 * h], kb[4 * c + 2 * h + 1],
-                      acc);
+    for (int s = 0; s < KS; ++s) acc = mfma32<T>(kb[s], qv[gh][s], acc);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = acc[j];
+    if constexpr (decltype(MASK)::value) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[j] = (row_ok && (kt != diag || 4 * g + j <= n)) ? x[j] : -INFINITY;
     }
-    return acc;
+  };
+  using NoMask = std::integral_constant<bool, false>;
+  using Mask = std::integral_constant<bool, true>;
+
+  // Both passes walk the tiles over two named K buffers (a dynamically
+  // indexed register array would live in scratch memory), issuing the next
+  // tile's load before the current tile is processed.  Tiles below the
+  // diagonal need no mask; the diagonal tile (and every tile of a wave with
+  // queries past the prompt) is processed with it.
+  auto walk = [&](auto&& tile) {
+    uint4 ka[KS], kc[KS];
+    const int kend = rows_ok ? last_tile : 0;   // tiles [0, kend) are unmasked
+    load_k(0, ka);
+    int kt = 0;
+    for (; kt + 1 < kend; kt += 2) {
+      load_k(kt + 1, kc);
+      tile(NoMask{}, kt, ka);
+      load_k(kt + 2, ka);
+      tile(NoMask{}, kt + 1, kc);
+    }
+    for (; kt <= last_tile; ++kt) {
+      if (kt < kend) tile(NoMask{}, kt, ka);
+      else tile(Mask{}, kt, ka);
+      if (kt < last_tile) load_k(kt + 1, ka);
+    }
   };
 
-  // Pass 1: log-sum-exp (base 2) per (head, query row).
-  float m[GMAX][4], l[GMAX][4];
+  // Pass 1: log-sum-exp (base 2) per (head, query), lazily re-based.  The
+  // running maximum starts at a finite floor, so a lane that has seen only
+  // masked keys (-inf) adds exp2(-inf) = 0 rather than exp2(-inf + inf).
+  float m[GMAX], l[GMAX];
 #pragma unroll
-  for (int gh = 0; gh < GMAX; ++gh)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      m[gh][j] = -INFINITY;
-      l[gh][j] = 0.f;
-    }
+  for (int gh = 0; gh < GMAX; ++gh) {
+    m[gh] = PS_FLOOR;
+    l[gh] = 0.f;
+  }
   if (q0 < Tn) {
-    for (int kt = 0; kt <= last_tile; ++kt) {
-      uint32_t kb[C * 4];
-      load_k(kt, kb);
-      const int key = kt * 16 + n;
+    walk([&](auto MASK, int kt, const uint4* kb) {
 #pragma unroll
       for (int gh = 0; gh < GMAX; ++gh) {
-        if (gh >= G) continue;
-        const f32x4 acc = scores(kb, gh);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int q = q0 + 4 * g + j;
-          if (key <= q && q < Tn) {
-            const float x = acc[j] * p.scale_log2;
-            if (x > m[gh][j]) {
-              l[gh][j] = l[gh][j] * exp2f(m[gh][j] - x) + 1.f;
-              m[gh][j] = x;
-            } else {
-              l[gh][j] += exp2f(x - m[gh][j]);
-            }
-          }
+        if (!EXACT && gh >= G) continue;
+        float x[4];
+        logits(MASK, kb, gh, kt, x);
+        const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) * sl;
+        // Re-base where a logit exceeds the running maximum by more than
+        // PS_LAZY (a wave-uniform test; rare after the first tiles).
+        if (__any(tm > m[gh] + PS_LAZY)) {
+          const bool up = tm > m[gh] + PS_LAZY;
+          l[gh] *= up ? __builtin_amdgcn_exp2f(m[gh] - tm) : 1.f;
+          m[gh] = up ? tm : m[gh];
         }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) l[gh] += __builtin_amdgcn_exp2f(fmaf(x[j], sl, -m[gh]));
       }
-    }
+    });
   }
-  // Merge the 16 key-column owners of each row (lanes with equal l / 16).
-  float lse[GMAX][4];
+  // Merge the four key-row owners of each query (lanes n, n+16, n+32, n+48).
+  float lse[GMAX];
 #pragma unroll
-  for (int gh = 0; gh < GMAX; ++gh)
+  for (int gh = 0; gh < GMAX; ++gh) {
+    float mm = m[gh], ll = l[gh];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float mm = m[gh][j], ll = l[gh][j];
-#pragma unroll
-      for (int d = 1; d < 16; d <<= 1) {
-        const float mo = shfl_xor_f(mm, d), lo = shfl_xor_f(ll, d);
-        const float M = fmaxf(mm, mo);
-        ll = (M == -INFINITY) ? 0.f : ll * exp2f(mm - M) + lo * exp2f(mo - M);
-        mm = M;
-      }
-      lse[gh][j] = (ll > 0.f) ? mm + log2f(ll) : INFINITY;
+    for (int d = 16; d < 64; d <<= 1) {
+      const float mo = shfl_xor_f(mm, d), lo = shfl_xor_f(ll, d);
+      const float M = fmaxf(mm, mo);
+      ll = ll * __builtin_amdgcn_exp2f(mm - M) + lo * __builtin_amdgcn_exp2f(mo - M);
+      mm = M;
     }
+    lse[gh] = (ll > 0.f) ? mm + log2f(ll) : INFINITY;
+  }
 
   // Pass 2: probability mass per 16-key tile.
   if (q0 < Tn) {
-    for (int kt = 0; kt <= last_tile; ++kt) {
-      uint32_t kb[C * 4];
-      load_k(kt, kb);
-      const int key = kt * 16 + n;
+    walk([&](auto MASK, int kt, const uint4* kb) {
       float part = 0.f;
 #pragma unroll
       for (int gh = 0; gh < GMAX; ++gh) {
-        if (gh >= G) continue;
-        const f32x4 acc = scores(kb, gh);
+        if (!EXACT && gh >= G) continue;
+        float x[4];
+        logits(MASK, kb, gh, kt, x);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int q = q0 + 4 * g + j;
-          if (key <= q && q < Tn) part += exp2f(acc[j] * p.scale_log2 - lse[gh][j]);
-        }
+        for (int j = 0; j < 4; ++j) part += __builtin_amdgcn_exp2f(fmaf(x[j], sl, -lse[gh]));
       }
-      part = wave_sum(part);
+      part = wave_sum_dpp(part);
       if (lane == 0) s_blk[w][kt] = part;
-    }
+    });
   }
   __syncthreads();
   float* out = p.partial + ((int64_t(b) * p.kv_heads + kvh) * p.nqb + qb) * p.ntiles;
@@ -217,31 +245,43 @@ __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(Prefi
 }
 
 // mass[b, blk] = sum over kv heads, query blocks and the block's tiles, in a
-// fixed order, / (H * T) / len(blk).
-__global__ __launch_bounds__(256) void prefill_mass_reduce_kernel(const float* partial, float* mass, int kv_heads,
-                                                                   int nqb, int ntiles, int heads, int tokens,
-                                                                   int block_size, int nblk) {
+// fixed order (lane i of the block's wave takes elements i, i + 64, ... of
+// the (kv head, query block, tile) enumeration, then a fixed DPP reduction),
+// / (H * T) / len(blk).  One wave per (sequence, block).
+__global__ __launch_bounds__(64) void prefill_mass_reduce_kernel(const float* partial, float* mass, int kv_heads,
+                                                                  int nqb, int ntiles, int heads, int tokens,
+                                                                  int block_size, int nblk) {
   const int b = blockIdx.y;
-  const int blk = blockIdx.x * 256 + threadIdx.x;
-  if (blk >= nblk) return;
+  const int blk = blockIdx.x;
+  const int lane = threadIdx.x;
   const int tpb = block_size / 16;
+  const int t0 = blk * tpb;
+  const int tn = min(tpb, ntiles - t0);
+  const int total = kv_heads * nqb * tn;
   float acc = 0.f;
-  for (int h = 0; h < kv_heads; ++h)
-    for (int qb = 0; qb < nqb; ++qb) {
-      const float* row = partial + ((int64_t(b) * kv_heads + h) * nqb + qb) * ntiles;
-      for (int t = blk * tpb; t < min((blk + 1) * tpb, ntiles); ++t) acc += row[t];
-    }
-  const int len = min(block_size, tokens - blk * block_size);
-  mass[int64_t(b) * nblk + blk] = acc / (float(heads) * float(tokens)) / float(max(len, 1));
+  for (int e = lane; e < total; e += 64) {
+    const int t = e % tn;
+    const int hq = e / tn;                      // h * nqb + qb
+    acc += partial[(int64_t(b) * kv_heads * nqb + hq) * ntiles + t0 + t];
+  }
+  acc = wave_sum_dpp(acc);
+  if (lane == 0) {
+    const int len = min(block_size, tokens - blk * block_size);
+    mass[int64_t(b) * nblk + blk] = acc / (float(heads) * float(tokens)) / float(max(len, 1));
+  }
 }
 
 template <int D, typename T>
 static hipError_t launch_prefill(const PrefillParams& p, int batch, int G, hipStream_t stream) {
-  const dim3 grid(p.nqb, p.kv_heads, batch);
-  if (G <= 4)
-    hipLaunchKernelGGL((prefill_block_mass_kernel<D, T, 4>), grid, dim3(64 * PS_WAVES), 0, stream, p);
+  const dim3 grid(unsigned(int64_t(p.nqb) * p.kv_heads * batch));
+  if (G == 4)
+    hipLaunchKernelGGL((prefill_block_mass_kernel<D, T, 4, true>), grid, dim3(64 * PS_WAVES), 0, stream, p);
+  else if (G == PS_MAX_GROUP)
+    hipLaunchKernelGGL((prefill_block_mass_kernel<D, T, PS_MAX_GROUP, true>), grid, dim3(64 * PS_WAVES), 0, stream, p);
+  else if (G < 4)
+    hipLaunchKernelGGL((prefill_block_mass_kernel<D, T, 4, false>), grid, dim3(64 * PS_WAVES), 0, stream, p);
   else
-    hipLaunchKernelGGL((prefill_block_mass_kernel<D, T, PS_MAX_GROUP>), grid, dim3(64 * PS_WAVES), 0, stream, p);
+    hipLaunchKernelGGL((prefill_block_mass_kernel<D, T, PS_MAX_GROUP, false>), grid, dim3(64 * PS_WAVES), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -265,6 +305,7 @@ extern "C" int32_t tierkv_prefill_block_mass(
   if (!q || !k || !mass || !workspace) return fail(TIERKV_ERR_INVALID, "null pointer");
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || tokens <= 0)
     return fail(TIERKV_ERR_INVALID, "empty prefill");
+  if (batch > 65535) return fail(TIERKV_ERR_UNSUPPORTED, "batch too large");
   if (num_heads % num_kv_heads != 0) return fail(TIERKV_ERR_INVALID, "num_heads must be a multiple of num_kv_heads");
   const int G = num_heads / num_kv_heads;
   if (G > PS_MAX_GROUP) return fail(TIERKV_ERR_UNSUPPORTED, "GQA group above 8");
@@ -294,6 +335,8 @@ extern "C" int32_t tierkv_prefill_block_mass(
   p.tokens = tokens;
   p.nqb = (tokens + PS_QB - 1) / PS_QB;
   p.ntiles = (tokens + 15) / 16;
+  p.batch = batch;
+  if (int64_t(p.nqb) * num_kv_heads * batch > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "prefill grid too large");
   p.scale_log2 = scaling * 1.4426950408889634f;
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
   hipError_t e;
@@ -304,7 +347,7 @@ extern "C" int32_t tierkv_prefill_block_mass(
                         : launch_prefill<64, __hip_bfloat16>(p, batch, G, stream);
   if (e != hipSuccess) return fail(TIERKV_ERR_HIP, std::string("prefill_block_mass_kernel: ") + hipGetErrorString(e));
   const int nblk = (tokens + block_size - 1) / block_size;
-  hipLaunchKernelGGL(prefill_mass_reduce_kernel, dim3((nblk + 255) / 256, batch), dim3(256), 0, stream, p.partial,
+  hipLaunchKernelGGL(prefill_mass_reduce_kernel, dim3(nblk, batch), dim3(64), 0, stream, p.partial,
                      mass, num_kv_heads, p.nqb, p.ntiles, num_heads, tokens, block_size, nblk);
   return check_launch("prefill_mass_reduce_kernel");
 }
