@@ -131,6 +131,31 @@ def test_long_row_list_build(device, groups):
     _check(case, "ref_u8", device, cold_mode="zero_logit", return_scores=True)
 
 
+def test_split_launch_in_sequence_chunks(device):
+    # More (sequence, kv head) units than the split-arrival counter region
+    # holds (65536): the host launches the batch in chunks of whole
+    # sequences on offset pointers.  Every sequence shares one table row and
+    # the pools, with its own scaled query; sequences on both sides of the
+    # chunk boundary are checked against the oracle.
+    one = W.make_tiered_case("chunks", 1, 2, 1, 64, 40, 10, 20, seed=51, max_blocks=44)
+    warm = oracle_warm(one, "absmax_i8")
+    B = 65536 + 5
+    scale = 1.0 + 0.05 * (torch.arange(B) % 13).to(torch.float16)
+    args = to_gpu_inputs(one, warm, device)
+    args["query_states"] = (args["query_states"] * scale.to(device).view(B, 1, 1, 1)).contiguous()
+    for k in ("block_table", "block_states", "block_lengths"):
+        args[k] = args[k].expand(B, -1).contiguous()
+    out, sc = tierkv_decode_attention(**args, return_scores=True, cold_mode="masked", splits=2)
+    torch.cuda.synchronize()
+    assert workspace_error_word(device) == 0
+    for b in (0, 1, 65534, 65535, 65536, 65537, B - 1):
+        sub = W.make_tiered_case("chunks", 1, 2, 1, 64, 40, 10, 20, seed=51, max_blocks=44)
+        sub.query = (sub.query * scale[b]).to(torch.float16)
+        exp_out, exp_sc = oracle_decode(sub, warm, "absmax_i8", "masked", True)
+        assert_close(out[b, 0].float().cpu().numpy(), exp_out[0], what=f"seq {b} out")
+        assert_close(sc[b].cpu().numpy(), exp_sc[0], what=f"seq {b} scores")
+
+
 def test_seq_num_blocks_ragged(device):
     case = W.make_tiered_case("ragged", 4, 16, 4, 64, 48, 8, 24, seed=11)
     snb = [48, 1, 17, 30]
