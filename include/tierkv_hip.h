@@ -73,8 +73,12 @@ TIERKV_API int32_t tierkv_abi_version(void);
  * seq_num_blocks  NULL (every sequence has num_blocks blocks) or device
  *   int32 [batch] (each clamped to num_blocks).
  * workspace  device scratch of at least tierkv_decode_workspace_bytes(...)
- *   bytes; its first 4 bytes are an error word the kernels set non-zero when
- *   they skip a block whose slot or state is out of range.
+ *   bytes, zero-filled before its first use; its first 4 bytes are an error
+ *   word the kernels set non-zero when they skip a block whose slot or state
+ *   is out of range.  It also holds the split-arrival counters, which every
+ *   launch leaves at zero, so one workspace serves launches of any shape
+ *   (and graph replays) on one stream; launches that share it must not
+ *   overlap.
  * scaling  softmax scale (head_dim ** -0.5 in modeling_llama.py:315).
  */
 TIERKV_API int32_t tierkv_decode_attention(
