@@ -44,13 +44,15 @@ def parse():
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "c2b", "c5", "prefill"], default="c3",
+    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "c2b", "c5", "prefill", "ref"], default="c3",
                    help="c2a / c2b: demotion / scoring microbenchmarks, c5: end-to-end random-init "
                         "Llama-3-8B decode through the HF hooks (each its own JSON line)")
     p.add_argument("--c5-steps", type=int, default=256)
     p.add_argument("--c5-batch", type=int, default=16)
     p.add_argument("--c5-prompt", type=int, default=2048)
     p.add_argument("--no-dense-baseline", action="store_true")
+    p.add_argument("--ref-prompt", type=int, default=512, help="ref workload: prompt tokens (512/1024/1536/1900)")
+    p.add_argument("--ref-steps", type=int, default=128, help="ref workload: greedy decode steps")
     p.add_argument("--c5-eager", action="store_true",
                    help="c5: run decode steps eagerly only (no HIP-graph replay, no eager comparison run)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -537,6 +539,86 @@ def c5_generate(model, prompt, cache, steps, runtime=None):
     return torch.cat(toks, dim=1), sec, cache
 
 
+REF_METRIC = ("reference-API drop-in end-to-end decode tokens/s, TinyLlama-1.1B shape, batch 1, HOT+WARM, "
+              "hot budget 8, policy every 64")
+# The reference's own number for this setting (TierKV Triton path, HOT+WARM,
+# hot budget 8, policy interval 64, TinyLlama-1.1B, ctx 512 / 1024 / 1536 /
+# 1900) on one NVIDIA A10G: FINAL_EVALUATION_RESULTS.md:83-88.
+REF_PUBLISHED_A10G = {512: 50.15, 1024: 49.22, 1536: 49.63, 1900: 46.51}
+
+
+def run_ref(args, device):
+    """The reference's end-to-end setting through this build's drop-in for
+    its Python API: a random-init TinyLlama-1.1B-shaped model (22 layers,
+    hidden 2048, 32 / 4 heads, head_dim 64, FFN 5632, vocab 32000, fp16),
+    batch 1, a uniform-random prompt, greedy decode through the HF hooks and
+    the drop-in TieredKVRuntime (reference warm format, zero-logit COLD,
+    HOT+WARM policy with hot budget 8, re-evaluated every 64 tokens).  Each
+    decode step runs eagerly, as the reference's does.  Stock transformers
+    with its dense DynamicCache on the same model and prompt is timed
+    beside it."""
+    import torch
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+
+    from paged_tierkv_amd import hf_llama, tierkv_policy as tp
+    from paged_tierkv_amd.block_manager import BlockManager
+
+    T, steps = args.ref_prompt, args.ref_steps
+    cfg = LlamaConfig(hidden_size=2048, intermediate_size=5632, num_hidden_layers=22, num_attention_heads=32,
+                      num_key_value_heads=4, head_dim=64, vocab_size=32000, max_position_embeddings=4096,
+                      rope_theta=10000.0, initializer_range=0.02, rms_norm_eps=1e-5, tie_word_embeddings=False)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(device):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    hf_llama.install()
+    prompt = torch.randint(0, cfg.vocab_size, (1, T), generator=torch.Generator().manual_seed(2)).to(device)
+
+    def runtime():
+        tp.reset_global_tierkv()
+        return tp.TieredKVRuntime(block_manager=BlockManager(total_blocks=8192), num_layers=cfg.num_hidden_layers,
+                                  block_size=16, hot_budget=8, max_seq_len=T + steps + 16, attention_backend="triton",
+                                  policy_interval=64, policy_mode="hot_warm")
+
+    log(f"[ref] warm-up (kernels, GEMM heuristics) on {torch.cuda.get_device_name(0)}")
+    c5_generate(model, prompt[:, :64], runtime().cache, 8)
+    log(f"[ref] drop-in runtime: prompt {T}, {steps} greedy steps")
+    rt = runtime()
+    toks, sec, _ = c5_generate(model, prompt, rt.cache, steps)
+    tps = steps / sec
+    metrics = rt.collect_memory_metrics() if hasattr(rt, "collect_memory_metrics") else {}
+    log(f"[ref] drop-in: {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step)")
+    dense = None
+    if not args.no_dense_baseline:
+        c5_generate(model, prompt[:, :64], DynamicCache(config=cfg), 8)
+        _, dsec, _ = c5_generate(model, prompt, DynamicCache(config=cfg), steps)
+        dense = {"tokens_per_s": round(steps / dsec, 1), "ms_per_step": round(dsec / steps * 1e3, 3)}
+        log(f"[ref] dense: {dense['tokens_per_s']} tok/s")
+    hf_llama.uninstall()
+    tp.reset_global_tierkv()
+    pub = REF_PUBLISHED_A10G.get(T)
+    line = _line(REF_METRIC, round(tps, 1), "tokens/s", steps, 8, sec / steps, "f16",
+                 {"workload": "ref_tinyllama_b1_e2e", "batch": 1, "prompt": T, "decode_steps": steps,
+                  "block_size": 16, "hot_budget": 8, "policy_interval": 64, "policy_mode": "hot_warm",
+                  "warm_format": "reference uint8 per-token asymmetric", "cold": "zero_logit",
+                  "runtime": "reference-API drop-in (tierkv_policy.TieredKVRuntime) through the HF hooks",
+                  "decode_steps_as": "eager"},
+                 dense_hf_baseline=dense,
+                 reference_published=({"tokens_per_s": pub, "hardware": "NVIDIA A10G",
+                                       "source": "FINAL_EVALUATION_RESULTS.md:83-88"} if pub else None))
+    line["data"] = "synthetic: random-init weights N(0, 0.02), uniform random prompt ids"
+    line["ms_per_step"] = round(sec / steps * 1e3, 3)
+    line["vs_baseline"] = round(tps / pub, 3) if pub else None
+    if metrics:
+        line["kv_metrics"] = {k: v for k, v in metrics.items() if isinstance(v, (int, float))}
+    print(json.dumps(line), flush=True)
+
+
 def run_c5(args, device):
     import torch
     from transformers import DynamicCache
@@ -645,6 +727,9 @@ def main():
         return
     if args.workload == "prefill":
         run_prefill(args, device)
+        return
+    if args.workload == "ref":
+        run_ref(args, device)
         return
     if args.workload == "c2a":
         run_c2a(args, device)

@@ -166,7 +166,14 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device) -> int:
+    """Handle of torch's current stream on ``device`` (launches go there)."""
+    if _raw_stream is not None:
+        idx = device.index if isinstance(device, torch.device) else None
+        return _raw_stream(torch.cuda.current_device() if idx is None else idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

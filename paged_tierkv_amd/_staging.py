@@ -33,7 +33,8 @@ class _Ring:
         self.host = torch.empty((_SLOTS, _SLOT_INTS), dtype=torch.int32, pin_memory=True)
         self.host_np = self.host.numpy()
         self.dev = torch.empty((_SLOTS, _SLOT_INTS), dtype=torch.int32, device=device)
-        self.events: list = [None] * _SLOTS
+        self.events = [torch.cuda.Event() for _ in range(_SLOTS)]
+        self.recorded = [False] * _SLOTS
         self.next = 0
         self.big = collections.deque()     # (event, pinned buffer) of one-off copies in flight
 
@@ -56,14 +57,13 @@ class _Ring:
         i = self.next
         self.next = (i + 1) % _SLOTS
         ev = self.events[i]
-        if ev is not None:
+        if self.recorded[i]:
             ev.synchronize()
         self.host_np[i, :n] = arr
         out = self.dev[i, :n]
         out.copy_(self.host[i, :n], non_blocking=True)
-        ev = torch.cuda.Event()
         ev.record()
-        self.events[i] = ev
+        self.recorded[i] = True
         return out
 
 
@@ -74,11 +74,14 @@ def stage_i32(arr, device) -> torch.Tensor:
     """Copy an int32 host array to a device tensor valid for the kernels
     launched next on the current stream (see module docstring)."""
     device = torch.device(device)
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    cur = torch.cuda.current_device()
+    key = (device.type, device.index if device.index is not None else cur)
     ring = _rings.get(key)
     if ring is None:
         with torch.cuda.device(key[1]):
             ring = _Ring(torch.device("cuda", key[1]))
         _rings[key] = ring
+    if key[1] == cur:
+        return ring.stage(np.asarray(arr))
     with torch.cuda.device(key[1]):
         return ring.stage(np.asarray(arr))
