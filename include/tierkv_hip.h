@@ -152,6 +152,16 @@ TIERKV_API int32_t tierkv_write_hot_tokens(
     void* hot_k, void* hot_v, int64_t hot_slots,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
 
+/* The same copy for at most 4 jobs given in HOST memory, jobs_host = int32
+ * [n][5] = {src_seq, src_tok, count, dst_slot, dst_pos}: the jobs travel in
+ * the kernel's arguments, so a decode step's single-token append needs no
+ * host-to-device copy of its plan (write_hot_tokens, tierkv_policy.py:934-967,
+ * as called once per layer and step by append_to_layer, 1768-1816). */
+TIERKV_API int32_t tierkv_write_hot_tokens_inline(
+    const void* src_k, const void* src_v, int64_t src_seqs, int32_t src_tokens, const int32_t* jobs_host, int32_t n,
+    int32_t zero_tail, void* hot_k, void* hot_v, int64_t hot_slots,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
+
 /* Batched runtime (one layer of B sequences whose tables live on the device).
  * Free-slot stacks: int32 [capacity] arrays whose first `top` entries are free
  * slots; ctl is int32 [4] = {hot_top, warm_top, error bits, 0}.  Error bits:
@@ -257,6 +267,12 @@ TIERKV_API int32_t tierkv_tier_counts(const int32_t* block_states, const int32_t
  * 450-477), which the reference issues as one launch per table entry. */
 TIERKV_API int32_t tierkv_scatter_i32(int32_t* dst, int64_t dst_len, const int32_t* pairs, int32_t n,
                                       void* stream);
+
+/* The same writes for at most 16 pairs given in HOST memory (int32 [n][2]),
+ * carried in the kernel's arguments: a decode step's table update (the open
+ * block's length, a new block's entries) needs no host-to-device copy. */
+TIERKV_API int32_t tierkv_scatter_i32_inline(int32_t* dst, int64_t dst_len, const int32_t* pairs_host, int32_t n,
+                                             void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Block scores.  Per-block probability mass from softmax probabilities

@@ -98,6 +98,11 @@ SIGNATURES = {
     "tierkv_runtime_tick_scratch_bytes": (c_int64, [c_int32, c_int64, c_int32, c_int32]),
     "tierkv_scatter_i32": (c_int32, [_P, c_int64, _P, c_int32, _P]),
     "tierkv_tier_counts": (c_int32, [_P, _P, c_int64, _P, c_int32, _P, _P]),
+    "tierkv_scatter_i32_inline": (c_int32, [_P, c_int64, _P, c_int32, _P]),
+    "tierkv_write_hot_tokens_inline": (c_int32, [
+        _P, _P, c_int64, c_int32, _P, c_int32,
+        c_int32, _P, _P, c_int64,
+        c_int32, c_int32, c_int32, _P]),
     "tierkv_prefill_block_mass_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "tierkv_prefill_block_mass": (c_int32, [
         _P, c_int64, c_int64, c_int64,

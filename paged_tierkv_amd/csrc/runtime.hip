@@ -66,6 +66,9 @@ __device__ int block_scan(int v, int* sh, int* total) {
 // [dst_pos, dst_pos + count); with zero_tail the block's positions past the
 // written range are zeroed (tierkv_policy.py:955-960).
 // ---------------------------------------------------------------------------
+constexpr int INLINE_JOBS = 4;     // copy jobs carried by value in the kernel arguments
+constexpr int INLINE_PAIRS = 16;   // table writes carried by value
+
 struct CopyJobs {
   const __half* src[2];
   int64_t src_seqs;
@@ -78,17 +81,22 @@ struct CopyJobs {
   __half* hot[2];
   int64_t hot_slots;
   int32_t kv_heads, bs, D, zero_tail;
+  // inl_n > 0: the jobs are inl[i] = {src_seq, src_tok, count, dst_slot,
+  // dst_pos} (the pointers above are unused).
+  int32_t inl_n;
+  int32_t inl[INLINE_JOBS][5];
 };
 
 __global__ __launch_bounds__(CT) void write_hot_kernel(CopyJobs c) {
   const int job = blockIdx.x;
   const int h = blockIdx.y;
   const int kv = blockIdx.z;
-  const int64_t sq = c.src_seq[job];
-  const int64_t slot = c.dst_slot[job];
-  const int t0 = c.src_tok[job];
-  const int n = c.count[job];
-  const int p0 = c.dst_pos[job];
+  const bool inl = c.inl_n > 0;
+  const int64_t sq = inl ? c.inl[job][0] : c.src_seq[job];
+  const int64_t slot = inl ? c.inl[job][3] : c.dst_slot[job];
+  const int t0 = inl ? c.inl[job][1] : c.src_tok[job];
+  const int n = inl ? c.inl[job][2] : c.count[job];
+  const int p0 = inl ? c.inl[job][4] : c.dst_pos[job];
   if (sq < 0 || sq >= c.src_seqs || slot < 0 || slot >= c.hot_slots) return;
   if (n < 0 || t0 < 0 || t0 + n > c.src_tokens || p0 < 0 || p0 + n > c.bs) return;
   const int D = c.D;
@@ -565,6 +573,19 @@ __global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
 // coalesces its writes per position, so positions are distinct and the
 // launch order of the pairs does not matter.
 // ---------------------------------------------------------------------------
+struct InlinePairs {
+  int32_t n;
+  int32_t v[2 * INLINE_PAIRS];
+};
+
+// The same writes with the pairs carried by value (at most INLINE_PAIRS).
+__global__ __launch_bounds__(64) void scatter_i32_inline_kernel(int32_t* dst, int64_t len, InlinePairs p) {
+  const int i = threadIdx.x;
+  if (i >= p.n) return;
+  const int pos = p.v[2 * i], val = p.v[2 * i + 1];
+  if (pos >= 0 && pos < len) dst[pos] = val;
+}
+
 __global__ __launch_bounds__(CT) void scatter_i32_kernel(int32_t* dst, int64_t len, const int32_t* pairs, int n) {
   const int i = blockIdx.x * CT + threadIdx.x;
   if (i >= n) return;
@@ -631,6 +652,60 @@ extern "C" int32_t tierkv_scatter_i32(int32_t* dst, int64_t dst_len, const int32
   hipLaunchKernelGGL(scatter_i32_kernel, dim3((n + CT - 1) / CT), dim3(CT), 0,
                      reinterpret_cast<hipStream_t>(stream), dst, dst_len, pairs, n);
   return check_launch("scatter_i32_kernel");
+}
+
+extern "C" int32_t tierkv_scatter_i32_inline(int32_t* dst, int64_t dst_len, const int32_t* pairs_host, int32_t n,
+                                             void* stream) {
+  clear_error();
+  if (n < 0 || n > INLINE_PAIRS) return fail(TIERKV_ERR_INVALID, "inline scatter takes 0..16 pairs");
+  if (n == 0) return TIERKV_OK;
+  if (!dst || !pairs_host) return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (dst_len > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "scatter target above 2^31 entries");
+  InlinePairs p{};
+  p.n = n;
+  for (int i = 0; i < 2 * n; ++i) p.v[i] = pairs_host[i];
+  hipLaunchKernelGGL(scatter_i32_inline_kernel, dim3(1), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), dst,
+                     dst_len, p);
+  return check_launch("scatter_i32_inline_kernel");
+}
+
+static int32_t check_write_geometry(const void* src_k, const void* src_v, const void* hot_k, const void* hot_v,
+                                    int32_t src_tokens, int32_t num_kv_heads, int32_t block_size, int32_t head_dim) {
+  if (!src_k || !src_v || !hot_k || !hot_v) return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (num_kv_heads <= 0 || block_size <= 0 || block_size > 64 || head_dim <= 0 || head_dim > 256 || src_tokens <= 0)
+    return fail(TIERKV_ERR_UNSUPPORTED, "block_size must be in [1, 64] and head_dim in [1, 256]");
+  if (num_kv_heads > 65535) return fail(TIERKV_ERR_UNSUPPORTED, "too many kv heads");
+  return TIERKV_OK;
+}
+
+extern "C" int32_t tierkv_write_hot_tokens_inline(
+    const void* src_k, const void* src_v, int64_t src_seqs, int32_t src_tokens, const int32_t* jobs_host, int32_t n,
+    int32_t zero_tail, void* hot_k, void* hot_v, int64_t hot_slots,
+    int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
+  clear_error();
+  if (n < 0 || n > INLINE_JOBS) return fail(TIERKV_ERR_INVALID, "inline write takes 0..4 jobs");
+  if (n == 0) return TIERKV_OK;
+  if (!jobs_host) return fail(TIERKV_ERR_INVALID, "null pointer");
+  const int32_t rc = check_write_geometry(src_k, src_v, hot_k, hot_v, src_tokens, num_kv_heads, block_size, head_dim);
+  if (rc != TIERKV_OK) return rc;
+  CopyJobs c{};
+  c.src[0] = reinterpret_cast<const __half*>(src_k);
+  c.src[1] = reinterpret_cast<const __half*>(src_v);
+  c.src_seqs = src_seqs;
+  c.src_tokens = src_tokens;
+  c.hot[0] = reinterpret_cast<__half*>(hot_k);
+  c.hot[1] = reinterpret_cast<__half*>(hot_v);
+  c.hot_slots = hot_slots;
+  c.kv_heads = num_kv_heads;
+  c.bs = block_size;
+  c.D = head_dim;
+  c.zero_tail = zero_tail;
+  c.inl_n = n;
+  for (int i = 0; i < n; ++i)
+    for (int f = 0; f < 5; ++f) c.inl[i][f] = jobs_host[5 * i + f];
+  hipLaunchKernelGGL(write_hot_kernel, dim3(n, num_kv_heads, 2), dim3(CT), 0,
+                     reinterpret_cast<hipStream_t>(stream), c);
+  return check_launch("write_hot_kernel");
 }
 
 extern "C" int32_t tierkv_write_hot_tokens(

@@ -52,6 +52,9 @@ from . import _lib
 from ._staging import stage_i32
 from .kernels import LABEL_MODES, WARM_FORMATS
 
+_INLINE_JOBS = 4     # copy jobs the inline write entry point carries (tierkv_write_hot_tokens_inline)
+_INLINE_PAIRS = 16   # table writes the inline scatter carries (tierkv_scatter_i32_inline)
+
 try:
     from transformers.cache_utils import Cache as HFCache
 except Exception:  # transformers absent: the cache is a plain object, as in the reference
@@ -209,14 +212,25 @@ class _Tables:
         n = len(self.pending)
         pairs = np.fromiter((x for kv in self.pending.items() for x in kv), dtype=np.int32, count=2 * n)
         self.pending.clear()
-        d = stage_i32(pairs, self.dev.device)
-        rc = _lib.lib().tierkv_scatter_i32(_lib.ptr(self.dev), self.dev.numel(), _lib.ptr(d), n,
-                                           _lib.stream_of(self.dev.device))
-        _lib.check(rc, "tierkv_scatter_i32")
+        _scatter(self.dev, pairs, n)
 
     def view(self, k: int) -> torch.Tensor:
         self.flush()
         return self.dev[:, k, :]
+
+
+def _scatter(dev: torch.Tensor, pairs: np.ndarray, n: int) -> None:
+    """dev[pairs[2i]] = pairs[2i + 1]: up to 16 pairs ride in the kernel's
+    arguments, more go through the pinned staging ring."""
+    lib = _lib.lib()
+    stream = _lib.stream_of(dev.device)
+    if n <= _INLINE_PAIRS:
+        rc = lib.tierkv_scatter_i32_inline(_lib.ptr(dev), dev.numel(), pairs.ctypes.data, n, stream)
+        _lib.check(rc, "tierkv_scatter_i32_inline")
+        return
+    d = stage_i32(pairs, dev.device)
+    rc = lib.tierkv_scatter_i32(_lib.ptr(dev), dev.numel(), _lib.ptr(d), n, stream)
+    _lib.check(rc, "tierkv_scatter_i32")
 
 
 class _Vector:
@@ -256,10 +270,7 @@ class _Vector:
         n = len(self.pending)
         pairs = np.fromiter((x for kv in self.pending.items() for x in kv), dtype=np.int32, count=2 * n)
         self.pending.clear()
-        d = stage_i32(pairs, self.dev.device)
-        rc = _lib.lib().tierkv_scatter_i32(_lib.ptr(self.dev), self.dev.numel(), _lib.ptr(d), n,
-                                           _lib.stream_of(self.dev.device))
-        _lib.check(rc, "tierkv_scatter_i32")
+        _scatter(self.dev, pairs, n)
 
     def tensor(self) -> torch.Tensor:
         self.flush()
@@ -356,6 +367,17 @@ class _QueuedStorage:
 
     def _launch_writes(self, lib, src_k, src_v, rows, dst_k, dst_v, stream) -> None:
         n = len(rows)
+        if n <= _INLINE_JOBS:
+            # A decode step's few jobs ride in the kernel's arguments.
+            jobs = np.zeros((n, 5), np.int32)     # src_seq, src_tok, count, dst_slot, dst_pos
+            for i, (tok0, count, slot, pos) in enumerate(rows):
+                jobs[i, 1], jobs[i, 2], jobs[i, 3], jobs[i, 4] = tok0, count, slot, pos
+            rc = lib.tierkv_write_hot_tokens_inline(
+                _lib.ptr(src_k), _lib.ptr(src_v), int(src_k.shape[0]), int(src_k.shape[2]), jobs.ctypes.data, n, 1,
+                _lib.ptr(dst_k), _lib.ptr(dst_v), int(dst_k.shape[0]),
+                self.kv_heads, self.block_size, self.head_dim, stream)
+            _lib.check(rc, "tierkv_write_hot_tokens_inline")
+            return
         arr = np.zeros((5, n), np.int32)          # src_seq, src_tok, count, dst_slot, dst_pos
         for i, (tok0, count, slot, pos) in enumerate(rows):
             arr[1, i], arr[2, i], arr[3, i], arr[4, i] = tok0, count, slot, pos
