@@ -1,0 +1,69 @@
+"""Property tests of the tiered decode kernel against the CPU oracle over
+random tier mixes (hypothesis, derandomized so every run draws the same
+cases): batch, kv heads, GQA group, head_dim, row length, HOT/WARM/COLD
+fractions, ragged block lengths, dense or compact pools, both WARM formats,
+both COLD modes, score sums on or off, and automatic or forced splits.
+
+Tolerance: BASELINE's 2e-3 absolute / 1e-2 relative vs the fp32 oracle for
+outputs and per-block probability sums (the same bar as test_gpu_decode)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+hypothesis = pytest.importorskip("hypothesis")
+from hypothesis import HealthCheck, given, settings, strategies as st  # noqa: E402
+
+from paged_tierkv_amd import workloads as W  # noqa: E402
+from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention, workspace_error_word  # noqa: E402
+
+from helpers import assert_close, oracle_decode, oracle_warm, to_gpu_inputs  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@st.composite
+def tier_cases(draw):
+    batch = draw(st.integers(1, 3))
+    kv = draw(st.sampled_from([1, 2, 4]))
+    groups = draw(st.sampled_from([1, 2, 4, 8]))
+    head_dim = draw(st.sampled_from([64, 128]))
+    nb = draw(st.integers(1, 80))
+    hot_frac = draw(st.floats(0.0, 1.0))
+    warm_frac = draw(st.floats(0.0, 1.0 - hot_frac))
+    n_hot = min(nb, int(round(nb * hot_frac)))
+    n_warm = min(nb - n_hot, int(round(nb * warm_frac)))
+    seed = draw(st.integers(0, 2 ** 16))
+    ragged = draw(st.booleans())
+    lengths = None
+    if ragged:
+        g = torch.Generator().manual_seed(seed)
+        lengths = torch.randint(0, 17, (batch, nb), generator=g)
+    case = W.make_tiered_case("prop", batch, kv * groups, kv, head_dim, nb, n_hot, n_warm, seed=seed,
+                              lengths=lengths, max_blocks=nb + draw(st.integers(0, 5)),
+                              layout=draw(st.sampled_from(["compact", "dense"])),
+                              recent_hot=draw(st.integers(0, 2)))
+    return dict(case=case, fmt=draw(st.sampled_from(["absmax_i8", "ref_u8"])),
+                cold=draw(st.sampled_from(["masked", "zero_logit"])), scores=draw(st.booleans()),
+                splits=draw(st.sampled_from([None, 1, 2, 3])))
+
+
+@settings(max_examples=40, deadline=None, derandomize=True, database=None,
+          suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+@given(tier_cases())
+def test_decode_matches_oracle_on_random_tier_mixes(device, c):
+    case = c["case"]
+    print(f"[prop] B={case.batch} H={case.num_heads} Hkv={case.kv_heads} D={case.head_dim} nb={case.num_blocks} "
+          f"tiers={case.tier_counts()} fmt={c['fmt']} cold={c['cold']} scores={c['scores']} splits={c['splits']}",
+          flush=True)
+    warm = oracle_warm(case, c["fmt"])
+    out, sums = tierkv_decode_attention(**to_gpu_inputs(case, warm, device), return_scores=c["scores"],
+                                        cold_mode=c["cold"], splits=c["splits"])
+    torch.cuda.synchronize()
+    assert workspace_error_word(device) == 0
+    res = oracle_decode(case, warm, c["fmt"], c["cold"], c["scores"])
+    exp_out, exp_sc = res if c["scores"] else (res, None)
+    assert_close(out[:, 0].float().cpu().numpy(), exp_out, what="output")
+    if c["scores"]:
+        assert_close(sums.cpu().numpy(), exp_sc, what="score sums")
