@@ -68,7 +68,7 @@ struct PrefillParams {
   const void* k;
   int64_t qs_b, qs_h, qs_t;      // element strides of q [B, H, T, D]
   int64_t ks_b, ks_h, ks_t;      // element strides of k [B, H_kv, T, D]
-  float* partial;                // [B, H_kv, nqb, ntiles]
+  float* partial;                // [B, H_kv, nqb, PS_WAVES, ntiles]
   int32_t heads, kv_heads, tokens, nqb, ntiles, batch;
   float scale_log2;
 };
@@ -77,7 +77,10 @@ struct PrefillParams {
 template <int D, typename T, int GMAX, bool EXACT>
 __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(PrefillParams p) {
   constexpr int KS = D / 32;         // MFMA k-steps (one 16-byte load each)
-  __shared__ float s_blk[PS_WAVES][PS_MAX_TILES];
+  constexpr int RC = D / 8;          // 16-byte chunks per K row
+  constexpr int RP = RC + 1;         // LDS row pitch in chunks (one pad chunk against bank conflicts)
+  // The workgroup's current and next K tile, staged once for its four waves.
+  __shared__ uint4 s_k[2][16 * RP];
   // Workgroup -> (query block, kv head, sequence).  The hardware deals
   // consecutive workgroups to the 8 XCDs in turn; when the (sequence, kv
   // head) pairs come in multiples of 8, all query blocks of one pair go to
@@ -101,8 +104,6 @@ __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(Prefi
   const int Tn = p.tokens;
   const int q0 = qb * PS_QB + 16 * w;
 
-  for (int i = threadIdx.x; i < PS_WAVES * PS_MAX_TILES; i += 64 * PS_WAVES) (&s_blk[0][0])[i] = 0.f;
-
   // Q^T B-operands: query q0 + n (clamped), head kvh * G + gh.
   uint4 qv[GMAX][KS];
   {
@@ -120,27 +121,31 @@ __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(Prefi
       }
     }
   }
-  __syncthreads();
-  // Waves whose queries all lie past the prompt add nothing (their LDS slots stay zero).
+  // Waves whose queries all lie past the prompt compute nothing (the reduce
+  // kernel skips their tiles).
   const int last_tile = min((q0 + 15) >> 4, (Tn - 1) >> 4);
+  const int wg_last = min((qb * PS_QB + PS_QB - 1) >> 4, (Tn - 1) >> 4);
   const int diag = q0 >> 4;                  // the one tile that needs the causal mask
   const bool row_ok = q0 + n < Tn;
   const bool rows_ok = q0 + 15 < Tn;        // every query of the wave lies in the prompt
+  const bool active = q0 < Tn;
+  const int kend = rows_ok ? last_tile : 0;  // tiles [0, kend) need no mask
   const T* kbase = reinterpret_cast<const T*>(p.k) + b * p.ks_b + int64_t(kvh) * p.ks_h;
   const float sl = p.scale_log2;
-
-  auto load_k = [&](int kt, uint4* kb) {
-    const int krow = min(kt * 16 + n, Tn - 1);
-    const T* row = kbase + int64_t(krow) * p.ks_t;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) kb[s] = *reinterpret_cast<const uint4*>(row + 32 * s + 8 * g);
+  // Cooperative K staging: thread t moves 16 bytes, chunk t % RC of row t / RC.
+  const int lrow = threadIdx.x / RC, lchunk = threadIdx.x % RC;
+  constexpr int LOADERS = 16 * RC;           // 256 (D = 128) or 128 (D = 64) threads
+  auto fetch_k = [&](int kt) -> uint4 {
+    const int krow = min(kt * 16 + lrow, Tn - 1);
+    return *reinterpret_cast<const uint4*>(kbase + int64_t(krow) * p.ks_t + 8 * lchunk);
   };
+
   // The four raw logits q . k of keys kt*16 + 4g + j for this lane's query;
   // MASK: -inf where masked (past the query, or a query past the prompt).
-  auto logits = [&](auto MASK, const uint4* kb, int gh, int kt, float* x) {
+  auto logits = [&](auto MASK, const uint4* sk, int gh, int kt, float* x) {
     f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s) acc = mfma32<T>(kb[s], qv[gh][s], acc);
+    for (int s = 0; s < KS; ++s) acc = mfma32<T>(sk[n * RP + 4 * s + g], qv[gh][s], acc);
 #pragma unroll
     for (int j = 0; j < 4; ++j) x[j] = acc[j];
     if constexpr (decltype(MASK)::value) {
@@ -151,26 +156,24 @@ __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(Prefi
   using NoMask = std::integral_constant<bool, false>;
   using Mask = std::integral_constant<bool, true>;
 
-  // Both passes walk the tiles over two named K buffers (a dynamically
-  // indexed register array would live in scratch memory), issuing the next
-  // tile's load before the current tile is processed.  Tiles below the
-  // diagonal need no mask; the diagonal tile (and every tile of a wave with
-  // queries past the prompt) is processed with it.
+  // Both passes walk the workgroup's tiles [0, wg_last]: each tile is loaded
+  // from global memory one tile ahead, written into the other LDS buffer
+  // after the current one is processed, with one barrier per tile.  A wave
+  // processes the tiles up to its own last one (below the diagonal without
+  // masks, the diagonal tile with them).
   auto walk = [&](auto&& tile) {
-    uint4 ka[KS], kc[KS];
-    const int kend = rows_ok ? last_tile : 0;   // tiles [0, kend) are unmasked
-    load_k(0, ka);
-    int kt = 0;
-    for (; kt + 1 < kend; kt += 2) {
-      load_k(kt + 1, kc);
-      tile(NoMask{}, kt, ka);
-      load_k(kt + 2, ka);
-      tile(NoMask{}, kt + 1, kc);
-    }
-    for (; kt <= last_tile; ++kt) {
-      if (kt < kend) tile(NoMask{}, kt, ka);
-      else tile(Mask{}, kt, ka);
-      if (kt < last_tile) load_k(kt + 1, ka);
+    uint4 nxt = make_uint4(0u, 0u, 0u, 0u);
+    if (threadIdx.x < LOADERS) s_k[0][lrow * RP + lchunk] = fetch_k(0);
+    __syncthreads();
+    for (int kt = 0; kt <= wg_last; ++kt) {
+      const int cur = kt & 1;
+      if (kt < wg_last && threadIdx.x < LOADERS) nxt = fetch_k(kt + 1);
+      if (active && kt <= last_tile) {
+        if (kt < kend) tile(NoMask{}, kt, s_k[cur]);
+        else tile(Mask{}, kt, s_k[cur]);
+      }
+      if (kt < wg_last && threadIdx.x < LOADERS) s_k[cur ^ 1][lrow * RP + lchunk] = nxt;
+      __syncthreads();
     }
   };
 
@@ -183,26 +186,24 @@ __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(Prefi
     m[gh] = PS_FLOOR;
     l[gh] = 0.f;
   }
-  if (q0 < Tn) {
-    walk([&](auto MASK, int kt, const uint4* kb) {
+  walk([&](auto MASK, int kt, const uint4* sk) {
 #pragma unroll
-      for (int gh = 0; gh < GMAX; ++gh) {
-        if (!EXACT && gh >= G) continue;
-        float x[4];
-        logits(MASK, kb, gh, kt, x);
-        const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) * sl;
-        // Re-base where a logit exceeds the running maximum by more than
-        // PS_LAZY (a wave-uniform test; rare after the first tiles).
-        if (__any(tm > m[gh] + PS_LAZY)) {
-          const bool up = tm > m[gh] + PS_LAZY;
-          l[gh] *= up ? __builtin_amdgcn_exp2f(m[gh] - tm) : 1.f;
-          m[gh] = up ? tm : m[gh];
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) l[gh] += __builtin_amdgcn_exp2f(fmaf(x[j], sl, -m[gh]));
+    for (int gh = 0; gh < GMAX; ++gh) {
+      if (!EXACT && gh >= G) continue;
+      float x[4];
+      logits(MASK, sk, gh, kt, x);
+      const float tm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])) * sl;
+      // Re-base where a logit exceeds the running maximum by more than
+      // PS_LAZY (a wave-uniform test; rare after the first tiles).
+      if (__any(tm > m[gh] + PS_LAZY)) {
+        const bool up = tm > m[gh] + PS_LAZY;
+        l[gh] *= up ? __builtin_amdgcn_exp2f(m[gh] - tm) : 1.f;
+        m[gh] = up ? tm : m[gh];
       }
-    });
-  }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) l[gh] += __builtin_amdgcn_exp2f(fmaf(x[j], sl, -m[gh]));
+    }
+  });
   // Merge the four key-row owners of each query (lanes n, n+16, n+32, n+48).
   float lse[GMAX];
 #pragma unroll
@@ -218,36 +219,31 @@ __global__ __launch_bounds__(64 * PS_WAVES) void prefill_block_mass_kernel(Prefi
     lse[gh] = (ll > 0.f) ? mm + log2f(ll) : INFINITY;
   }
 
-  // Pass 2: probability mass per 16-key tile.
-  if (q0 < Tn) {
-    walk([&](auto MASK, int kt, const uint4* kb) {
-      float part = 0.f;
+  // Pass 2: probability mass per 16-key tile, one value per (wave, tile)
+  // into the workspace.
+  float* out = p.partial + (((int64_t(b) * p.kv_heads + kvh) * p.nqb + qb) * PS_WAVES + w) * p.ntiles;
+  walk([&](auto MASK, int kt, const uint4* sk) {
+    float part = 0.f;
 #pragma unroll
-      for (int gh = 0; gh < GMAX; ++gh) {
-        if (!EXACT && gh >= G) continue;
-        float x[4];
-        logits(MASK, kb, gh, kt, x);
+    for (int gh = 0; gh < GMAX; ++gh) {
+      if (!EXACT && gh >= G) continue;
+      float x[4];
+      logits(MASK, sk, gh, kt, x);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) part += __builtin_amdgcn_exp2f(fmaf(x[j], sl, -lse[gh]));
-      }
-      part = wave_sum_dpp(part);
-      if (lane == 0) s_blk[w][kt] = part;
-    });
-  }
-  __syncthreads();
-  float* out = p.partial + ((int64_t(b) * p.kv_heads + kvh) * p.nqb + qb) * p.ntiles;
-  for (int kt = threadIdx.x; kt < p.ntiles; kt += 64 * PS_WAVES) {
-    float acc = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < PS_WAVES; ++ww) acc += s_blk[ww][kt];
-    out[kt] = acc;
-  }
+      for (int j = 0; j < 4; ++j) part += __builtin_amdgcn_exp2f(fmaf(x[j], sl, -lse[gh]));
+    }
+    part = wave_sum_dpp(part);
+    if (lane == 0) out[kt] = part;
+  });
 }
 
-// mass[b, blk] = sum over kv heads, query blocks and the block's tiles, in a
-// fixed order (lane i of the block's wave takes elements i, i + 64, ... of
-// the (kv head, query block, tile) enumeration, then a fixed DPP reduction),
-// / (H * T) / len(blk).  One wave per (sequence, block).
+// mass[b, blk] = sum over kv heads, query blocks, waves and the block's
+// tiles of the per-(wave, tile) sums, in a fixed order (lane i of the
+// block's wave takes elements i, i + 64, ... of the (kv head, query block,
+// wave, tile) enumeration, then a fixed DPP reduction), / (H * T) / len(blk).
+// A wave's sums exist for its tiles up to its diagonal (tile <= 4 * query
+// block + wave) and only if its first query lies in the prompt.  One wave per
+// (sequence, block).
 __global__ __launch_bounds__(64) void prefill_mass_reduce_kernel(const float* partial, float* mass, int kv_heads,
                                                                   int nqb, int ntiles, int heads, int tokens,
                                                                   int block_size, int nblk) {
@@ -257,12 +253,15 @@ __global__ __launch_bounds__(64) void prefill_mass_reduce_kernel(const float* pa
   const int tpb = block_size / 16;
   const int t0 = blk * tpb;
   const int tn = min(tpb, ntiles - t0);
-  const int total = kv_heads * nqb * tn;
+  const int total = kv_heads * nqb * PS_WAVES * tn;
   float acc = 0.f;
   for (int e = lane; e < total; e += 64) {
-    const int t = e % tn;
-    const int hq = e / tn;                      // h * nqb + qb
-    acc += partial[(int64_t(b) * kv_heads * nqb + hq) * ntiles + t0 + t];
+    const int t = t0 + e % tn;
+    const int hqw = e / tn;                     // (h * nqb + qb) * PS_WAVES + w
+    const int w = hqw % PS_WAVES;
+    const int qb = (hqw / PS_WAVES) % nqb;
+    if (t <= PS_WAVES * qb + w && qb * PS_QB + 16 * w < tokens)
+      acc += partial[(int64_t(b) * kv_heads * nqb * PS_WAVES + hqw) * ntiles + t];
   }
   acc = wave_sum_dpp(acc);
   if (lane == 0) {
@@ -293,7 +292,7 @@ extern "C" int64_t tierkv_prefill_block_mass_workspace_bytes(int32_t batch, int3
   if (batch <= 0 || num_kv_heads <= 0 || tokens <= 0) return -1;
   const int64_t nqb = (tokens + PS_QB - 1) / PS_QB;
   const int64_t ntiles = (tokens + 15) / 16;
-  return int64_t(batch) * num_kv_heads * nqb * ntiles * 4;
+  return int64_t(batch) * num_kv_heads * nqb * PS_WAVES * ntiles * 4;
 }
 
 extern "C" int32_t tierkv_prefill_block_mass(
