@@ -44,9 +44,12 @@ def parse():
     p.add_argument("--warmup", type=int, default=2000)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "c2b", "c5", "prefill", "ref"], default="c3",
-                   help="c2a / c2b: demotion / scoring microbenchmarks, c5: end-to-end random-init "
+    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "promote", "c2b", "c5", "prefill", "ref"],
+                   default="c3",
+                   help="c2a / promote / c2b: demotion / promotion / scoring microbenchmarks, c5: end-to-end random-init "
                         "Llama-3-8B decode through the HF hooks (each its own JSON line)")
+    p.add_argument("--warm-format", choices=["absmax_i8", "ref_u8"], default="absmax_i8",
+                   help="c2a / promote: WARM codec (BASELINE's int8 absmax, or the reference's uint8 per-token)")
     p.add_argument("--c5-steps", type=int, default=256)
     p.add_argument("--c5-batch", type=int, default=16)
     p.add_argument("--c5-prompt", type=int, default=2048)
@@ -331,18 +334,33 @@ def run_prefill(args, device):
 
 
 C2A_METRIC = "demotion HOT fp16 -> WARM int8 absmax GB/s (% peak), Llama-3-8B KV shape, 2048 of 4096 blocks"
+CODEC_METRICS = {
+    ("demote", "ref_u8"): "demotion HOT fp16 -> WARM uint8 (reference per-token codec) GB/s (% peak), Llama-3-8B "
+                          "KV shape, 2048 of 4096 blocks",
+    ("promote", "absmax_i8"): "promotion WARM int8 absmax -> HOT fp16 GB/s (% peak), Llama-3-8B KV shape, 2048 blocks",
+    ("promote", "ref_u8"): "promotion WARM uint8 (reference per-token codec) -> HOT fp16 GB/s (% peak), Llama-3-8B "
+                           "KV shape, 2048 blocks",
+}
 C2B_METRIC = "block-score + tier-label µs per call, probs [32, 32, 4096] -> per-block mass [32, 256] + labels"
 
 
 def run_c2a(args, device):
     """BASELINE.json configs[1](a): quantize a seeded 50 % of a 4096-block
-    fp16 pool (8 kv heads, 16 x 128) into int8 absmax WARM slots with fp32
-    per-(block, head) scales, table/state rewrite fused.  One step = one
-    demotion launch; 3 source pools are rotated (805 MB)."""
+    fp16 pool (8 kv heads, 16 x 128) into WARM slots, table/state rewrite
+    fused.  One step = one launch; 3 source pools are rotated (805 MB).
+
+    ``--warm-format`` picks the codec: int8 absmax with fp32 per-(block,
+    head) scales (BASELINE's), or the reference's uint8 with fp16 per-token
+    scale and zero point (quantize_fp16_to_int8, tierkv_policy.py:21-36).
+    ``--workload promote`` times the way back (promote_to_hot,
+    tierkv_policy.py:1087-1115): the same 2048 blocks dequantized from 3
+    rotated WARM sets into HOT slots, table/state rewrite fused."""
     import torch
 
     from paged_tierkv_amd import kernels, workloads as W
 
+    fmt = args.warm_format
+    op = "promote" if args.workload == "promote" else "demote"
     case = W.config2a()
     n = len(case.demote_logical)
     H, bs, D = 8, 16, 128
@@ -359,55 +377,95 @@ def run_c2a(args, device):
     lens = torch.full((n,), bs, dtype=torch.int32, device=device)
     pos = case.demote_logical.to(torch.int32).to(device)
     table, states = case.table.to(device), case.states.to(device)
-    warm_k = torch.empty((n, H, bs, D), dtype=torch.int8, device=device)
-    warm_v = torch.empty_like(warm_k)
-    ks = torch.empty((n, H), device=device)
-    vs = torch.empty_like(ks)
 
-    def step(i):
-        kernels.demote_to_warm(pools[i][0], pools[i][1], src, dst, lens, warm_k, warm_v, ks, None, vs, None,
-                               warm_format="absmax_i8", block_table=table, block_states=states, table_pos=pos)
+    def warm_set():
+        wk = torch.empty((n, H, bs, D), dtype=torch.int8 if fmt == "absmax_i8" else torch.uint8, device=device)
+        if fmt == "absmax_i8":
+            meta = (torch.empty((n, H), device=device), None, torch.empty((n, H), device=device), None)
+        else:
+            meta = tuple(torch.empty((n, H, bs, 1), dtype=torch.float16, device=device) for _ in range(4))
+        return wk, torch.empty_like(wk), meta
+
+    def demote(i, w):
+        kernels.demote_to_warm(pools[i][0], pools[i][1], src, dst, lens, w[0], w[1], *w[2], warm_format=fmt,
+                               block_table=table, block_states=states, table_pos=pos)
+
+    if op == "demote":
+        w0 = warm_set()
+        step = lambda i: demote(i % len(pools), w0)
+        kernel = "demote_absmax_wave_kernel" if fmt == "absmax_i8" else "demote_ref_wave_kernel"
+        nbytes = W.codec_ideal_bytes(n, H, bs, D, fmt, "demote")
+    else:
+        sets = [warm_set() for _ in range(3)]
+        for i, w in enumerate(sets):
+            demote(i, w)
+        hot_dst = torch.arange(n, dtype=torch.int32, device=device)
+        out_k = pools[0][0]                      # promoted into the first n slots of a HOT pool
+
+        def step(i):
+            w = sets[i % len(sets)]
+            kernels.promote_to_hot(w[0], w[1], *w[2], dst, hot_dst, lens, out_k, pools[0][1], warm_format=fmt,
+                                   block_table=table, block_states=states, table_pos=pos)
+        kernel = "promote_wave_kernel"
+        nbytes = W.codec_ideal_bytes(n, H, bs, D, fmt, "promote")
 
     # Eager launches: the host enqueues faster than one launch runs (~38 us),
     # so back-to-back launches time the kernel itself.
     for i in range(200):
-        step(i % len(pools))
+        step(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for i in range(args.steps):
-        step(i % len(pools))
+        step(i)
     e1.record()
     torch.cuda.synchronize()
     sec, steps = e0.elapsed_time(e1) / 1e3 / args.steps, args.steps
-    nbytes = W.demote_ideal_bytes(n, H, bs, D)
     gbs = nbytes / sec / 1e9
-    log(f"[c2a] {sec * 1e6:.2f} us per demotion launch, {gbs:.1f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of peak)")
+    log(f"[{op} {fmt}] {sec * 1e6:.2f} us per launch, {gbs:.1f} GB/s ({gbs / PEAK_HBM_GBS:.1%} of peak)")
     cpu = None
     if not args.no_cpu_baseline:
         sys.path.insert(0, ROOT)
         from oracle import codec
 
         sample = pools[0][0][src[:128].long()].cpu().numpy()
-        codec.quantize_absmax_i8(sample)
+        if op == "demote":
+            fn = (lambda: codec.quantize_absmax_i8(sample)) if fmt == "absmax_i8" else \
+                (lambda: codec.quantize_ref_u8(sample))
+        else:
+            if fmt == "absmax_i8":
+                qs = codec.quantize_absmax_i8(sample)
+                fn = lambda: codec.dequantize_absmax_i8(*qs).astype("float16")
+            else:
+                qs = codec.quantize_ref_u8(sample)
+                fn = lambda: codec.dequantize_ref_u8(*qs)
+        fn()
         reps, t0 = 0, time.perf_counter()
         while time.perf_counter() - t0 < args.cpu_seconds / 2:
-            codec.quantize_absmax_i8(sample)
+            fn()
             reps += 1
         per_tile_set = (time.perf_counter() - t0) / reps
-        cpu_gbs = W.demote_ideal_bytes(128, H, bs, D) / 2 / per_tile_set / 1e9
+        cpu_gbs = W.codec_ideal_bytes(128, H, bs, D, fmt, op) / 2 / per_tile_set / 1e9
         cpu = {"value": round(cpu_gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-               "sample": f"K codes of 128 of the {n} demoted blocks, {reps} reps "
-                         f"({per_tile_set * 1e3:.1f} ms; oracle NumPy absmax codec, single thread)"}
-    cfg = {"workload": "c2a_demote_llama3_8b_kv", "pool_blocks": int(table.shape[1]), "demoted_blocks": n,
-           "kv_heads": H, "block_size": bs, "head_dim": D, "warm_format": "int8 absmax per (block, kv head)",
-           "source_pools_rotated": len(pools)}
-    print(json.dumps(_line(C2A_METRIC, round(gbs, 2), "GB/s", steps, 200, sec, "f16->i8", cfg,
+               "sample": f"K tiles of 128 of the {n} blocks, {reps} reps ({per_tile_set * 1e3:.1f} ms; oracle "
+                         f"NumPy {fmt} codec, {'quantize' if op == 'demote' else 'dequantize'}, single thread)"}
+    fmt_name = "int8 absmax per (block, kv head)" if fmt == "absmax_i8" else \
+        "reference uint8, fp16 scale and zero point per (token, kv head)"
+    if op == "demote" and fmt == "absmax_i8":
+        workload, metric = "c2a_demote_llama3_8b_kv", C2A_METRIC
+    else:
+        workload, metric = f"c2a_{op}_{fmt}_llama3_8b_kv", CODEC_METRICS[(op, fmt)]
+    cfg = {"workload": workload, "pool_blocks": int(table.shape[1]), f"{op}d_blocks": n,
+           "kv_heads": H, "block_size": bs, "head_dim": D, "warm_format": fmt_name,
+           ("source_pools_rotated" if op == "demote" else "warm_sets_rotated"): 3}
+    dtype = ("f16->i8" if fmt == "absmax_i8" else "f16->u8") if op == "demote" else \
+        ("i8->f16" if fmt == "absmax_i8" else "u8->f16")
+    print(json.dumps(_line(metric, round(gbs, 2), "GB/s", steps, 200, sec, dtype, cfg,
                            us_per_call=round(sec * 1e6, 3), ideal_bytes_per_step=nbytes,
-                           roofline={"kernel": "demote_absmax_wave_kernel", "bound": "hbm",
+                           roofline={"kernel": kernel, "bound": "hbm",
                                      "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS,
                                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                                     "traffic": _profile_traffic("demote_absmax_wave_kernel", cfg["workload"])},
+                                     "traffic": _profile_traffic(kernel, workload)},
                            cpu_baseline=cpu)), flush=True)
 
 
@@ -731,7 +789,7 @@ def main():
     if args.workload == "ref":
         run_ref(args, device)
         return
-    if args.workload == "c2a":
+    if args.workload in ("c2a", "promote"):
         run_c2a(args, device)
         return
     if args.workload == "c2b":

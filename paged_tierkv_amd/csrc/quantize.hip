@@ -13,6 +13,8 @@
 
 #include "quantize.h"
 
+#include <type_traits>
+
 namespace tierkv {
 
 constexpr int QT = 256;   // threads per quantize workgroup
@@ -372,6 +374,163 @@ __global__ __launch_bounds__(QT) void demote_ref_kernel(QuantJobs q) {
 }
 
 
+// REF_U8, one wave per (job, K|V, kv head) tile, four tiles per 256-thread
+// workgroup.  A token row of D fp16 values is held by R = D / 8 lanes (16
+// bytes each, R a power of two), so load i of the wave covers rows
+// [64 i / R, 64 (i + 1) / R) of the tile; each row's min and max are reduced
+// over its R lanes with xor shuffles, and each lane stores its eight codes as
+// one 8-byte run.  The per-element arithmetic is the same op chain as
+// demote_ref_kernel.  Needs bs * R <= 64 * NV.
+// x / s correctly rounded, given y = RN(1 / s), by Markstein's correction:
+// q0 = RN(x y) lies within an ulp of x / s, the residual r = x - q0 s is
+// exact by an FMA, and RN(q0 + r y) = RN(x / s); copysign keeps the sign of
+// a zero quotient.  tests/native/div_correction_check.c checks it bit for
+// bit against the IEEE division for every finite fp16 x and every positive
+// finite fp16 s.  x and s must be finite.
+__device__ __forceinline__ float div_rn_by(float x, float s, float y) {
+  const float q0 = x * y;
+  const float r = __builtin_fmaf(-q0, s, x);
+  return __builtin_copysignf(__builtin_fmaf(r, y, q0), q0);
+}
+
+constexpr float kRcp255 = 1.f / 255.f;   // RN(1 / 255)
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// Min and max of a token row held by 2^r_log2 consecutive lanes (8 fp16
+// values each), returned to every lane of the row.  Packed fp16 min/max
+// (minNum semantics, as fminf/fmaxf: a NaN is ignored) over the lane's
+// eight values, the max carried negated beside the min so that one packed
+// min reduces both; across lanes by DPP row permutes (xor 1 and xor 2 within
+// quads, then half-row and row mirrors, each pairing groups that already
+// agree), and a shuffle for a 32-lane row.
+__device__ __forceinline__ void row_min_max(const u32x4& w, int r_log2, float& mn, float& mx) {
+  // The words go through scalars: hipcc (ROCm 7.2) compiles
+  // __builtin_bit_cast of a vector element subscript (w[k]) as a read of
+  // element 0.
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  h2 lo = __builtin_bit_cast(h2, ws[0]), hi = lo;
+#pragma unroll
+  for (int k = 1; k < 4; ++k) {
+    const h2 v = __builtin_bit_cast(h2, ws[k]);
+    lo = __builtin_elementwise_min(lo, v);
+    hi = __builtin_elementwise_max(hi, v);
+  }
+  h2 m = {__builtin_elementwise_min(lo[0], lo[1]), -__builtin_elementwise_max(hi[0], hi[1])};
+  auto step = [&](auto ctrl) {
+    const uint32_t o = static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(__builtin_bit_cast(uint32_t, m)), decltype(ctrl)::value, 0xf,
+                                    0xf, false));
+    m = __builtin_elementwise_min(m, __builtin_bit_cast(h2, o));
+  };
+  if (r_log2 >= 1) step(std::integral_constant<int, 0xB1>{});    // quad_perm [1, 0, 3, 2]
+  if (r_log2 >= 2) step(std::integral_constant<int, 0x4E>{});    // quad_perm [2, 3, 0, 1]
+  if (r_log2 >= 3) step(std::integral_constant<int, 0x141>{});   // row_half_mirror
+  if (r_log2 >= 4) step(std::integral_constant<int, 0x140>{});   // row_mirror
+  if (r_log2 >= 5) {
+    const uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(__builtin_bit_cast(uint32_t, m)), 16, 64));
+    m = __builtin_elementwise_min(m, __builtin_bit_cast(h2, o));
+  }
+  mn = static_cast<float>(m[0]);
+  mx = -static_cast<float>(m[1]);
+}
+
+template <int NV>
+__global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_t n_jobs, int32_t r_log2) {
+  const int lane = threadIdx.x & 63;
+  const int tiles_per_job = 2 * q.kv_heads;
+  const int64_t tile = int64_t(blockIdx.x) * (QT / 64) + (threadIdx.x >> 6);
+  const int64_t job = tile / tiles_per_job;
+  if (job >= n_jobs) return;
+  if (q.n_dev && job >= *q.n_dev) return;
+  const int rem = static_cast<int>(tile - job * tiles_per_job);
+  const int kv = rem / q.kv_heads;
+  const int h = rem - kv * q.kv_heads;
+  const int64_t si = q.src_index[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.src_tiles || di < 0 || di >= q.warm_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int R = 1 << r_log2;
+  const int64_t E = int64_t(q.bs) * q.D;
+  const int nvec = q.bs * R;
+  const int valid_vec = len * R;
+  const u32x4* src = reinterpret_cast<const u32x4*>(q.src[kv] + (si * q.kv_heads + h) * E);
+  u32x2* dst = reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(q.warm[kv]) + (di * q.kv_heads + h) * E);
+  __half* scale = reinterpret_cast<__half*>(q.scale[kv]) + (di * q.kv_heads + h) * int64_t(q.bs);
+  __half* zero = reinterpret_cast<__half*>(q.zero[kv]) + (di * q.kv_heads + h) * int64_t(q.bs);
+
+  u32x4 x[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * 64 + lane;
+    x[i] = vi < valid_vec ? __builtin_nontemporal_load(src + vi) : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * 64 + lane;
+    const int row = vi >> r_log2;
+    float xs[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      xs[2 * k] = half_lo(x[i][k]);
+      xs[2 * k + 1] = half_hi(x[i][k]);
+    }
+    float mn, mx;
+    row_min_max(x[i], r_log2, mn, mx);
+    if (vi < valid_vec) {
+      // The quotients below are correctly rounded without an IEEE division
+      // each (div_rn_by: one reciprocal per row, an FMA correction per
+      // quotient); a non-finite operand takes the plain IEEE result.
+      const float a = r16(mx - mn);
+      float sc = __builtin_isfinite(a) ? div_rn_by(a, 255.f, kRcp255) : a;   // (max - min) / 255.0
+      sc = r16(sc);
+      if (sc == 0.f) sc = 1.f;                            // torch.where(scale == 0, 1, scale)
+      float qt[8], qm;
+      if (__builtin_isfinite(sc)) {
+        const float y = __fdiv_rn(1.f, sc);
+        qm = div_rn_by(mn, sc, y);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qt[e] = div_rn_by(xs[e], sc, y);
+      } else {   // a row holding an infinity
+        qm = __fdiv_rn(mn, sc);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qt[e] = __fdiv_rn(xs[e], sc);
+      }
+      const float zp = r16(-rintf(r16(qm)));              // -round(min / scale)
+      // round(x / scale) + zp, clamp(0, 255).  Both terms are integers of at
+      // most 65504 in magnitude, so the fp32 sum is exact, and the reference's
+      // fp16 rounding of it changes no value the clamp lets through (integers
+      // up to 2048 are exact in fp16, and rounding keeps larger sums above
+      // 255 and negative sums below 0); it is therefore left out.
+      uint32_t w[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = fminf(fmaxf(rintf(r16(qt[e])) + zp, 0.f), 255.f);
+        w[e >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(v, e & 3, w[e >> 2]);
+      }
+      __builtin_nontemporal_store(u32x2{w[0], w[1]}, dst + vi);
+      if ((lane & (R - 1)) == 0) {
+        scale[row] = __float2half_rn(sc);
+        zero[row] = __float2half_rn(zp);
+      }
+    } else if (q.pad_tail && vi < nvec) {
+      __builtin_nontemporal_store(u32x2{0u, 0u}, dst + vi);
+      if ((lane & (R - 1)) == 0) {
+        scale[row] = __float2half_rn(1.f);
+        zero[row] = __float2half_rn(0.f);
+      }
+    }
+  }
+  if (lane == 0 && q.table_pos && h == 0 && kv == 0) {
+    const int32_t pos = q.table_pos[job];
+    if (pos >= 0) {
+      q.table[pos] = static_cast<int32_t>(di);
+      q.states[pos] = WARM;
+    }
+  }
+}
+
+
 
 // promote_to_hot: dequantize the first `length` tokens of a WARM slot into
 // a HOT slot (dequantize_int8_to_fp16, tierkv_policy.py:39-44).
@@ -412,6 +571,100 @@ __global__ __launch_bounds__(QT) void promote_kernel(DequantJobs q) {
   }
 }
 
+// promote_to_hot, one wave per (job, K|V, kv head) tile, four tiles per
+// 256-thread workgroup: each lane turns eight codes (one 8-byte load) into
+// eight fp16 values (one 16-byte store), with the same per-element
+// arithmetic as promote_kernel.  D = 8 R with R a power of two (a vector
+// never crosses a token row) and bs * R <= 64 * NV.
+template <int NV, int FMT>
+__global__ __launch_bounds__(QT) void promote_wave_kernel(DequantJobs q, int32_t n_jobs, int32_t r_log2) {
+  const int lane = threadIdx.x & 63;
+  const int tiles_per_job = 2 * q.kv_heads;
+  const int64_t tile = int64_t(blockIdx.x) * (QT / 64) + (threadIdx.x >> 6);
+  const int64_t job = tile / tiles_per_job;
+  if (job >= n_jobs) return;
+  if (q.n_dev && job >= *q.n_dev) return;
+  const int rem = static_cast<int>(tile - job * tiles_per_job);
+  const int kv = rem / q.kv_heads;
+  const int h = rem - kv * q.kv_heads;
+  const int64_t si = q.src_slot[job];
+  const int64_t di = q.dst_slot[job];
+  if (si < 0 || si >= q.warm_slots || di < 0 || di >= q.hot_slots) return;
+  const int len = min(max(q.lengths[job], 0), q.bs);
+  const int valid_vec = len << r_log2;
+  const int64_t E = int64_t(q.bs) * q.D;
+  const int64_t src0 = (si * q.kv_heads + h) * int64_t(q.bs);
+  const u32x2* c = reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(q.warm[kv]) + src0 * q.D);
+  u32x4* out = reinterpret_cast<u32x4*>(q.hot[kv] + (di * q.kv_heads + h) * E);
+  // All loads (codes, and the rows' scales and zero points) are issued
+  // before any is used.
+  u32x2 cw[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * 64 + lane;
+    cw[i] = vi < valid_vec ? __builtin_nontemporal_load(c + vi) : u32x2{0u, 0u};
+  }
+  // Reference format: lane t < len loads row t's scale and zero point
+  // (bs <= 64); a vector's lanes take them from that lane by a shuffle.
+  float sc_row = 0.f, zp_row = 0.f;
+  if constexpr (FMT == TIERKV_WARM_REF_U8) {
+    if (lane < len) {
+      sc_row = __half2float(reinterpret_cast<const __half*>(q.scale[kv])[src0 + lane]);
+      zp_row = __half2float(reinterpret_cast<const __half*>(q.zero[kv])[src0 + lane]);
+    }
+  }
+  float s = 0.f;
+  if constexpr (FMT == TIERKV_WARM_ABSMAX_I8) s = reinterpret_cast<const float*>(q.scale[kv])[si * q.kv_heads + h];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int vi = i * 64 + lane;
+    float sc = 0.f, zp = 0.f;
+    if constexpr (FMT == TIERKV_WARM_REF_U8) {
+      const int row = min(vi >> r_log2, 63);
+      sc = __shfl(sc_row, row, 64);
+      zp = __shfl(zp_row, row, 64);
+    }
+    if (vi >= valid_vec) continue;
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t byte = (cw[i][e >> 2] >> (8 * (e & 3))) & 0xffu;
+      float v;
+      if constexpr (FMT == TIERKV_WARM_ABSMAX_I8) {
+        v = float(static_cast<int8_t>(byte)) * s;
+      } else {
+        v = r16(float(byte) - zp) * sc;                  // (q.to(f16) - zero_point) * scale
+      }
+      const uint32_t hb = __half_as_ushort(__float2half_rn(v));
+      if (e & 1) o[e >> 1] |= hb << 16;
+      else o[e >> 1] = hb;
+    }
+    __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, out + vi);
+  }
+  if (lane == 0 && q.table_pos && h == 0 && kv == 0) {
+    const int32_t pos = q.table_pos[job];
+    if (pos >= 0) {
+      q.table[pos] = static_cast<int32_t>(di);
+      q.states[pos] = HOT;
+    }
+  }
+}
+
+// log2(head_dim / 8) when head_dim / 8 is a power of two, else -1.
+static int row_lanes_log2(int D) {
+  if (D % 8 != 0) return -1;
+  const int r = D / 8;
+  if (r & (r - 1)) return -1;
+  int l = 0;
+  while ((1 << l) < r) ++l;
+  return l;
+}
+
+// NV (16-byte vectors per lane) for a tile of nvec vectors, or 0 if above 512.
+static int wave_nv(int64_t nvec) {
+  return nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 0;
+}
+
 int32_t launch_demote(const QuantJobs& q, int n_grid, int32_t warm_format, hipStream_t stream) {
   if (n_grid <= 0) return TIERKV_OK;
   dim3 grid(n_grid, q.kv_heads, 2);
@@ -439,16 +692,52 @@ int32_t launch_demote(const QuantJobs& q, int n_grid, int32_t warm_format, hipSt
     return check_launch("demote_absmax_kernel");
   }
   if (warm_format == TIERKV_WARM_REF_U8) {
-    hipLaunchKernelGGL(demote_ref_kernel, grid, dim3(QT), 0, stream, q);
-    return check_launch("demote_ref_kernel");
+    const int rl = row_lanes_log2(q.D);
+    const int64_t tiles = int64_t(n_grid) * 2 * q.kv_heads;
+    const int nv = rl < 0 ? 0 : wave_nv(int64_t(q.bs) << rl);
+    const bool vec = nv > 0 && q.bs <= 64 && tiles < (int64_t(1) << 25) && aligned16(q.src[0]) && aligned16(q.src[1]) &&
+                     reinterpret_cast<uintptr_t>(q.warm[0]) % 8 == 0 && reinterpret_cast<uintptr_t>(q.warm[1]) % 8 == 0;
+    if (!vec) {
+      hipLaunchKernelGGL(demote_ref_kernel, grid, dim3(QT), 0, stream, q);
+      return check_launch("demote_ref_kernel");
+    }
+    const dim3 wgrid(static_cast<unsigned>((tiles + QT / 64 - 1) / (QT / 64)));
+    if (nv == 1) hipLaunchKernelGGL(demote_ref_wave_kernel<1>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else if (nv == 2) hipLaunchKernelGGL(demote_ref_wave_kernel<2>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else if (nv == 4) hipLaunchKernelGGL(demote_ref_wave_kernel<4>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else hipLaunchKernelGGL(demote_ref_wave_kernel<8>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    return check_launch("demote_ref_wave_kernel");
   }
   return fail(TIERKV_ERR_INVALID, "unknown warm format");
 }
 
 int32_t launch_promote(const DequantJobs& q, int n_grid, hipStream_t stream) {
   if (n_grid <= 0) return TIERKV_OK;
-  hipLaunchKernelGGL(promote_kernel, dim3(n_grid, q.kv_heads, 2), dim3(QT), 0, stream, q);
-  return check_launch("promote_kernel");
+  const int rl = row_lanes_log2(q.D);
+  const int64_t tiles = int64_t(n_grid) * 2 * q.kv_heads;
+  const int nv = rl < 0 ? 0 : wave_nv(int64_t(q.bs) << rl);
+  const bool vec = nv > 0 && q.bs <= 64 && tiles < (int64_t(1) << 25) && aligned16(q.hot[0]) && aligned16(q.hot[1]) &&
+                   reinterpret_cast<uintptr_t>(q.warm[0]) % 8 == 0 && reinterpret_cast<uintptr_t>(q.warm[1]) % 8 == 0;
+  if (!vec) {
+    hipLaunchKernelGGL(promote_kernel, dim3(n_grid, q.kv_heads, 2), dim3(QT), 0, stream, q);
+    return check_launch("promote_kernel");
+  }
+  const dim3 wgrid(static_cast<unsigned>((tiles + QT / 64 - 1) / (QT / 64)));
+#define TIERKV_PROMOTE(NV_, FMT_) \
+  hipLaunchKernelGGL((promote_wave_kernel<NV_, FMT_>), wgrid, dim3(QT), 0, stream, q, n_grid, rl)
+  if (q.warm_format == TIERKV_WARM_ABSMAX_I8) {
+    if (nv == 1) TIERKV_PROMOTE(1, TIERKV_WARM_ABSMAX_I8);
+    else if (nv == 2) TIERKV_PROMOTE(2, TIERKV_WARM_ABSMAX_I8);
+    else if (nv == 4) TIERKV_PROMOTE(4, TIERKV_WARM_ABSMAX_I8);
+    else TIERKV_PROMOTE(8, TIERKV_WARM_ABSMAX_I8);
+  } else {
+    if (nv == 1) TIERKV_PROMOTE(1, TIERKV_WARM_REF_U8);
+    else if (nv == 2) TIERKV_PROMOTE(2, TIERKV_WARM_REF_U8);
+    else if (nv == 4) TIERKV_PROMOTE(4, TIERKV_WARM_REF_U8);
+    else TIERKV_PROMOTE(8, TIERKV_WARM_REF_U8);
+  }
+#undef TIERKV_PROMOTE
+  return check_launch("promote_wave_kernel");
 }
 
 }  // namespace tierkv

@@ -255,6 +255,18 @@ def demote_ideal_bytes(n_blocks, kv_heads, block_size, head_dim):
     return n_blocks * (2 * tile * 2 + 2 * tile + 2 * kv_heads * 4 + 4 * 4 + 2 * 4)
 
 
+def codec_ideal_bytes(n_blocks, kv_heads, block_size, head_dim, warm_format="absmax_i8", op="demote"):
+    """Algorithmic bytes of one demotion or promotion launch over n_blocks
+    full blocks (K and V): the fp16 tiles, the 1-byte codes, the codec's
+    metadata (absmax: one fp32 scale per (block, head); reference: fp16 scale
+    and zero point per (token, head)), four int32 job-list entries read and
+    two table entries (slot, state) written per block.  Demotion reads the
+    fp16 tiles and writes codes and metadata; promotion the reverse."""
+    tile = kv_heads * block_size * head_dim
+    meta = 2 * kv_heads * 4 if warm_format == "absmax_i8" else 2 * 2 * kv_heads * block_size * 2
+    return n_blocks * (2 * tile * 2 + 2 * tile + meta + 4 * 4 + 2 * 4)
+
+
 def score_ideal_bytes(batch, heads, tokens, block_size):
     """Algorithmic bytes of one scoring step: fp32 probabilities read, fp32
     block mass written, then mass and current states read and labels

@@ -152,32 +152,136 @@ def test_reference_codec_demote_matches_golden(device):
     _eq(hot.cpu().numpy(), g["deq"], "promote vs reference dequant golden")
 
 
+# (16, 64), (16, 128), (32, 128), (8, 256): the one-wave-per-tile kernels
+# (head_dim / 8 lanes per token row); (16, 12), (64, 128): the per-workgroup
+# fallback kernels (head_dim not a multiple of 8, tile above 512 vectors).
+@pytest.mark.parametrize("bs,dim", [(16, 64), (16, 128), (32, 128), (8, 256), (16, 12), (64, 128)])
 @pytest.mark.parametrize("pad_tail", [False, True])
-def test_reference_codec_partial_blocks(device, pad_tail):
+def test_reference_codec_partial_blocks(device, pad_tail, bs, dim):
+    print(f"[quant] ref_u8 partial blocks bs={bs} dim={dim} pad_tail={pad_tail}", flush=True)
     g = torch.Generator().manual_seed(9)
-    heads, bs, dim = 2, 16, 64
-    src = torch.randn((4, heads, bs, dim), generator=g).half()
-    lens = torch.tensor([16, 5, 1, 9], dtype=torch.int32)
+    heads = 2
+    src = (torch.randn((4, heads, bs, dim), generator=g) * 3).half()
+    src[3, 1, 0] = 0.5                                       # constant row: scale 0 -> 1
+    lens = torch.tensor([bs, 5, 1, min(9, bs)], dtype=torch.int32)
     idx = torch.arange(4, dtype=torch.int32)
+    dst = torch.tensor([2, 0, 3, 1], dtype=torch.int32)
     warm = torch.full((4, heads, bs, dim), 200, dtype=torch.uint8, device=device)
     warm_v = warm.clone()
     ks = torch.full((4, heads, bs, 1), 7.0, dtype=torch.float16, device=device)
     kz, vs, vz = ks.clone(), ks.clone(), ks.clone()
-    kernels.demote_to_warm(src.to(device), src.to(device), idx, idx, lens, warm, warm_v, ks, kz, vs, vz,
+    src_v = (src * -2).contiguous()
+    kernels.demote_to_warm(src.to(device), src_v.to(device), idx, dst, lens, warm, warm_v, ks, kz, vs, vz,
                            warm_format="ref_u8", pad_tail=pad_tail)
     torch.cuda.synchronize()
     for i in range(4):
-        n = int(lens[i])
-        q, s, z = codec.quantize_ref_u8(src[i, :, :n].numpy())
-        _eq(warm[i, :, :n].cpu().numpy(), q, f"codes {i}")
-        _eq(ks[i, :, :n].cpu().numpy(), s, f"scale {i}")
-        _eq(kz[i, :, :n].cpu().numpy(), z, f"zero {i}")
-        tail_codes = warm[i, :, n:].cpu().numpy()
-        if pad_tail:   # write_warm_block (tierkv_policy.py:989-995)
-            assert (tail_codes == 0).all() and (ks[i, :, n:].cpu().numpy() == 1).all()
-            assert (kz[i, :, n:].cpu().numpy() == 0).all()
-        else:          # compact demote_to_warm leaves the tail untouched
-            assert (tail_codes == 200).all() and (ks[i, :, n:].cpu().numpy() == 7).all()
+        n, d = int(lens[i]), int(dst[i])
+        for what, x, wc, sc, zc in (("K", src, warm, ks, kz), ("V", src_v, warm_v, vs, vz)):
+            q, s, z = codec.quantize_ref_u8(x[i, :, :n].numpy())
+            _eq(wc[d, :, :n].cpu().numpy(), q, f"{what} codes {i}")
+            _eq(sc[d, :, :n].cpu().numpy(), s, f"{what} scale {i}")
+            _eq(zc[d, :, :n].cpu().numpy(), z, f"{what} zero {i}")
+            tail_codes = wc[d, :, n:].cpu().numpy()
+            if pad_tail:   # write_warm_block (tierkv_policy.py:989-995)
+                assert (tail_codes == 0).all() and (sc[d, :, n:].cpu().numpy() == 1).all()
+                assert (zc[d, :, n:].cpu().numpy() == 0).all()
+            else:          # compact demote_to_warm leaves the tail untouched
+                assert (tail_codes == 200).all() and (sc[d, :, n:].cpu().numpy() == 7).all()
+    # Promotion back (dequantize_int8_to_fp16, tierkv_policy.py:39-44) of the
+    # first lengths[i] tokens; the HOT tail stays untouched.
+    hot = torch.full((5, heads, bs, dim), 9.0, dtype=torch.float16, device=device)
+    hot_v = hot.clone()
+    pdst = torch.tensor([4, 1, 0, 2], dtype=torch.int32)
+    kernels.promote_to_hot(warm, warm_v, ks, kz, vs, vz, dst, pdst, lens, hot, hot_v, warm_format="ref_u8")
+    torch.cuda.synchronize()
+    for i in range(4):
+        n, d, h = int(lens[i]), int(dst[i]), int(pdst[i])
+        for what, wc, sc, zc, out in (("K", warm, ks, kz, hot), ("V", warm_v, vs, vz, hot_v)):
+            exp = codec.dequantize_ref_u8(wc[d, :, :n].cpu().numpy(), sc[d, :, :n].cpu().numpy(),
+                                          zc[d, :, :n].cpu().numpy())
+            _eq(out[h, :, :n].cpu().numpy(), exp, f"{what} promote {i}")
+            assert (out[h, :, n:].cpu() == 9.0).all()
+    assert (hot[3].cpu() == 9.0).all()
+
+
+@pytest.mark.parametrize("dim", [128, 64, 12])
+def test_reference_codec_special_rows(device, dim):
+    """Rows that exercise every branch of the reference codec's arithmetic:
+    constant rows (scale 0 -> 1), a range that overflows fp16 (scale +inf,
+    the IEEE-division path), large offsets (quotients in the thousands,
+    where fp16 spacing is 2-4), subnormal fp16 values and ordinary rows.
+    head_dim 128 / 64 run the one-wave-per-tile kernel, 12 the fallback."""
+    print(f"[quant] ref_u8 special rows dim={dim}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    heads, bs = 2, 16
+    x = torch.randn((6, heads, bs, dim), generator=g) * 3
+    x[1, 0] = 0.5
+    x[1, 1] = 0.0
+    x[2] = torch.where(torch.arange(dim) % 2 == 0, 40000.0, -40000.0) + torch.randn((heads, bs, dim), generator=g)
+    x[3] = 10.0 + torch.randn((heads, bs, dim), generator=g) * 0.1
+    x[4] = torch.randn((heads, bs, dim), generator=g) * 1e-4
+    x[5, :, ::2] = -7.25
+    x = x.half()
+    n = x.shape[0]
+    idx = torch.arange(n, dtype=torch.int32)
+    warm = torch.zeros((n, heads, bs, dim), dtype=torch.uint8, device=device)
+    warm_v = warm.clone()
+    meta = [torch.zeros((n, heads, bs, 1), dtype=torch.float16, device=device) for _ in range(4)]
+    xd = x.to(device)
+    kernels.demote_to_warm(xd, xd, idx, idx, torch.full((n,), bs, dtype=torch.int32), warm, warm_v, *meta,
+                           warm_format="ref_u8")
+    torch.cuda.synchronize()
+    with np.errstate(all="ignore"):
+        q, sc, zp = codec.quantize_ref_u8(x.numpy())
+    _eq(warm.cpu().numpy(), q, "special rows codes")
+    _eq(warm_v.cpu().numpy(), q, "special rows V codes")
+    _eq(meta[0].cpu().numpy(), sc, "special rows scales")
+    _eq(meta[1].cpu().numpy(), zp, "special rows zero points")
+    assert np.isinf(sc[2].astype(np.float32)).all()          # the overflow tile took the IEEE path
+
+
+def test_c2_reference_codec_round_trip_bit_exact(device):
+    """C2's pool in the reference's WARM format: 512 of the demoted blocks
+    quantized, table rewritten, then promoted into fresh HOT slots."""
+    case = W.config2a()
+    n = 512
+    logical = case.demote_logical[:n]
+    print(f"[quant] C2 ref_u8 demote + promote of {n} blocks", flush=True)
+    src = case.table[0, logical]
+    slots = torch.randperm(n, generator=torch.Generator().manual_seed(5)).to(torch.int32)
+    warm_k = torch.empty((n, 8, 16, 128), dtype=torch.uint8, device=device)
+    warm_v = torch.empty_like(warm_k)
+    meta = [torch.empty((n, 8, 16, 1), dtype=torch.float16, device=device) for _ in range(4)]
+    table, states = case.table.to(device), case.states.to(device)
+    kernels.demote_to_warm(case.hot_k.to(device), case.hot_v.to(device), src, slots,
+                           torch.full((n,), 16, dtype=torch.int32), warm_k, warm_v, *meta,
+                           warm_format="ref_u8", block_table=table, block_states=states,
+                           table_pos=logical.to(torch.int32))
+    torch.cuda.synchronize()
+    for what, x, wc, sc, zc in (("K", case.hot_k, warm_k, meta[0], meta[1]), ("V", case.hot_v, warm_v, meta[2], meta[3])):
+        q, s, z = codec.quantize_ref_u8(x[src.long()].numpy())
+        _eq(wc.cpu()[slots.long()].numpy(), q, f"C2 ref {what} codes")
+        _eq(sc.cpu()[slots.long()].numpy(), s, f"C2 ref {what} scales")
+        _eq(zc.cpu()[slots.long()].numpy(), z, f"C2 ref {what} zeros")
+    exp_table, exp_states = case.table.clone(), case.states.clone()
+    exp_table[0, logical] = slots
+    exp_states[0, logical] = 1
+    _eq(table.cpu().numpy(), exp_table.numpy(), "C2 ref table")
+    _eq(states.cpu().numpy(), exp_states.numpy(), "C2 ref states")
+    hot_k = torch.empty((n, 8, 16, 128), dtype=torch.float16, device=device)
+    hot_v = torch.empty_like(hot_k)
+    kernels.promote_to_hot(warm_k, warm_v, *meta, slots, torch.arange(n, dtype=torch.int32),
+                           torch.full((n,), 16, dtype=torch.int32), hot_k, hot_v, warm_format="ref_u8",
+                           block_table=table, block_states=states, table_pos=logical.to(torch.int32))
+    torch.cuda.synchronize()
+    for what, wc, sc, zc, out in (("K", warm_k, meta[0], meta[1], hot_k), ("V", warm_v, meta[2], meta[3], hot_v)):
+        exp = codec.dequantize_ref_u8(wc.cpu()[slots.long()].numpy(), sc.cpu()[slots.long()].numpy(),
+                                      zc.cpu()[slots.long()].numpy())
+        _eq(out.cpu().numpy(), exp, f"C2 ref {what} promote")
+    exp_table[0, logical] = torch.arange(n, dtype=torch.int32)
+    exp_states[0, logical] = 0
+    _eq(table.cpu().numpy(), exp_table.numpy(), "C2 promote table")
+    _eq(states.cpu().numpy(), exp_states.numpy(), "C2 promote states")
 
 
 def test_absmax_promote_bit_exact(device):
