@@ -28,6 +28,8 @@ pytestmark = pytest.mark.gpu
     (1, 32, 4, 64, 128, 16, torch.bfloat16),
     (3, 4, 1, 1, 64, 16, torch.float16),
     (1, 16, 4, 513, 128, 16, torch.float16),
+    (1, 12, 2, 300, 128, 16, torch.float16),     # GQA group 6: the guarded 8-head variant
+    (2, 4, 2, 97, 64, 32, torch.bfloat16),       # GQA group 2: the guarded 4-head variant
 ])
 def test_prefill_block_mass_matches_oracle(device, B, H, Hkv, T, D, bs, dtype):
     print(f"[prefill] B={B} H={H} Hkv={Hkv} T={T} D={D} bs={bs} {dtype}", flush=True)
