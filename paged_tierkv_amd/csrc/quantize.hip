@@ -393,6 +393,14 @@ __device__ __forceinline__ float div_rn_by(float x, float s, float y) {
   return __builtin_copysignf(__builtin_fmaf(r, y, q0), q0);
 }
 
+// div_rn_by without restoring the sign of a zero quotient (x = -0 gives +0):
+// for the codes, whose next step adds the integer zero point and clamps at
+// 0, the sign of a zero makes no difference.
+__device__ __forceinline__ float div_rn_by_unsigned_zero(float x, float s, float y) {
+  const float q0 = x * y;
+  return __builtin_fmaf(__builtin_fmaf(-q0, s, x), y, q0);
+}
+
 constexpr float kRcp255 = 1.f / 255.f;   // RN(1 / 255)
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
@@ -490,24 +498,32 @@ __global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_
         const float y = __fdiv_rn(1.f, sc);
         qm = div_rn_by(mn, sc, y);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qt[e] = div_rn_by(xs[e], sc, y);
+        for (int e = 0; e < 8; ++e) qt[e] = div_rn_by_unsigned_zero(xs[e], sc, y);
       } else {   // a row holding an infinity
         qm = __fdiv_rn(mn, sc);
 #pragma unroll
         for (int e = 0; e < 8; ++e) qt[e] = __fdiv_rn(xs[e], sc);
       }
       const float zp = r16(-rintf(r16(qm)));              // -round(min / scale)
-      // round(x / scale) + zp, clamp(0, 255).  Both terms are integers of at
-      // most 65504 in magnitude, so the fp32 sum is exact, and the reference's
-      // fp16 rounding of it changes no value the clamp lets through (integers
-      // up to 2048 are exact in fp16, and rounding keeps larger sums above
-      // 255 and negative sums below 0); it is therefore left out.
-      uint32_t w[2] = {0u, 0u};
+      // round(x / scale) + zp, clamp(0, 255), in fp16 two at a time.  The
+      // quotient is rounded to fp16 and then to an integer (rndne on the fp16
+      // value equals rintf on it); both terms of the sum are integers of at
+      // most 65504 in magnitude, so the fp16 add equals the reference's
+      // fp32 add rounded to fp16.  A clamped value v in [0, 255] is the low
+      // byte of the fp16 encoding of v + 1024 (exponent 10, unit spacing).
+      const _Float16 zh = static_cast<_Float16>(zp);
+      uint32_t hb[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float v = fminf(fmaxf(rintf(r16(qt[e])) + zp, 0.f), 255.f);
-        w[e >> 2] = __builtin_amdgcn_cvt_pk_u8_f32(v, e & 3, w[e >> 2]);
+      for (int k = 0; k < 4; ++k) {
+        h2 t = {static_cast<_Float16>(qt[2 * k]), static_cast<_Float16>(qt[2 * k + 1])};
+        t = __builtin_elementwise_rint(t);
+        t = t + h2{zh, zh};
+        t = __builtin_elementwise_min(__builtin_elementwise_max(t, h2{0, 0}), h2{255, 255});
+        t = t + h2{1024, 1024};
+        hb[k] = __builtin_bit_cast(uint32_t, t);
       }
+      // Low bytes of the eight halves: bytes 0 and 2 of each word.
+      const uint32_t w[2] = {perm_b32(hb[1], hb[0], 0x06040200u), perm_b32(hb[3], hb[2], 0x06040200u)};
       __builtin_nontemporal_store(u32x2{w[0], w[1]}, dst + vi);
       if ((lane & (R - 1)) == 0) {
         scale[row] = __float2half_rn(sc);
