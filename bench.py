@@ -60,8 +60,9 @@ def parse():
                    help="c5: run decode steps eagerly only (no HIP-graph replay, no eager comparison run)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--mode", choices=["bench", "copy"], default="bench",
-                   help="copy: time a plain device copy of known size (PMC calibration)")
+    p.add_argument("--mode", choices=["bench", "copy", "ceiling"], default="bench",
+                   help="copy: time a plain device copy of known size (PMC calibration); ceiling: HBM "
+                        "stream-read and 4 KB-tile gather ceilings of the box")
     return p.parse_args()
 
 
@@ -148,6 +149,61 @@ def copy_calibration(device):
     t = e0.elapsed_time(e1) / 1e3 / 20
     print(json.dumps({"mode": "copy", "bytes_read": n, "bytes_written": n, "sec": t,
                       "GBps_read_plus_write": 2 * n / t / 1e9}))
+
+
+def ceiling(device, c3_bytes=216944640, stream_grids=(1024, 2048, 4096)):
+    """HBM read ceilings of this box (libtierkv_ceiling.so): a non-temporal
+    streaming read of 1 GiB, and a non-temporal gather of C3's ideal bytes
+    (rounded to whole 4 KB tiles: 256 workgroups x 207 tiles) in a shuffled
+    tile order out of the same 1 GiB buffer -- the decode kernel's access
+    pattern without its arithmetic.  Each is timed with HIP events over 50
+    launches after 20 untimed ones."""
+    import ctypes
+
+    import torch
+
+    from paged_tierkv_amd import _lib, build as B
+
+    lib = ctypes.CDLL(str(B.CEILING_LIB))
+    for f in (lib.tierkv_ceiling_stream_read, lib.tierkv_ceiling_gather):
+        f.restype = ctypes.c_int32
+    lib.tierkv_ceiling_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
+                                               ctypes.c_void_p]
+    lib.tierkv_ceiling_gather.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int32,
+                                          ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    n = 1 << 30
+    src = torch.full((n,), 1, dtype=torch.uint8, device=device)
+    sink = torch.zeros(4, dtype=torch.int32, device=device)
+    stream = _lib.stream_of(device)
+    n_wg = 256
+    per_wg = c3_bytes // 4096 // n_wg
+    gen = torch.Generator().manual_seed(7)
+    order = torch.randperm(n // 4096, generator=gen)[:n_wg * per_wg].to(torch.int32).to(device)
+
+    def timed(call, nbytes):
+        for _ in range(20):
+            assert call() == 0
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(50):
+            call()
+        e1.record()
+        e1.synchronize()
+        t = e0.elapsed_time(e1) / 1e3 / 50
+        return t, nbytes / t / 1e9
+
+    res = {"mode": "ceiling"}
+    for grid in stream_grids:
+        t, gbs = timed(lambda: lib.tierkv_ceiling_stream_read(src.data_ptr(), n, sink.data_ptr(), grid, stream), n)
+        res[f"stream_read_grid{grid}_GBps"] = round(gbs, 1)
+    gbytes = n_wg * per_wg * 4096
+    t, gbs = timed(lambda: lib.tierkv_ceiling_gather(src.data_ptr(), n // 4096, order.data_ptr(), n_wg, per_wg,
+                                                     sink.data_ptr(), stream), gbytes)
+    res.update(gather_4k_tiles_bytes=gbytes, gather_4k_tiles_us=round(t * 1e6, 2), gather_4k_tiles_GBps=round(gbs, 1))
+    del src, order
+    torch.cuda.empty_cache()
+    return res
 
 
 def graph_timed(fn, n_variants, steps, warmup, passes=1):
@@ -777,6 +833,9 @@ def main():
     if args.mode == "copy":
         copy_calibration(device)
         return
+    if args.mode == "ceiling":
+        print(json.dumps(ceiling(device)), flush=True)
+        return
     if args.workload == "c5":
         run_c5(args, device)
         return
@@ -830,6 +889,15 @@ def main():
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
         cpu = cpu_baseline(args, case.name)
+    # The box's own ceiling for this access pattern: the same bytes gathered
+    # as shuffled 4 KB tiles with the decode kernel's load policy, no
+    # arithmetic (bench.py --mode ceiling has the stream-read figures too).
+    ceil = ceiling(device, c3_bytes=nbytes, stream_grids=(4096,))
+    measured_ceiling = {"gather_4k_tiles_GBps": ceil["gather_4k_tiles_GBps"],
+                        "stream_read_GBps": ceil["stream_read_grid4096_GBps"],
+                        "frac_of_gather": round(gbs / ceil["gather_4k_tiles_GBps"], 4)}
+    log(f"[bench] measured ceilings: gather {ceil['gather_4k_tiles_GBps']} GB/s, stream read "
+        f"{ceil['stream_read_grid4096_GBps']} GB/s; decode at {measured_ceiling['frac_of_gather']:.1%} of the gather")
 
     line = {
         "metric": METRIC,
@@ -854,6 +922,7 @@ def main():
         "ideal_bytes_per_step": nbytes,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic},
+        "measured_ceiling": measured_ceiling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -18,6 +18,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libtierkv_hip.so"
+# bench.py's HBM ceiling measurement (its own library, outside the C ABI).
+CEILING_LIB = PKG / "libtierkv_ceiling.so"
 ARCH = os.environ.get("TIERKV_OFFLOAD_ARCH", "gfx950")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.environ.get("HIPCC", os.path.join(ROCM, "bin", "hipcc"))
@@ -84,6 +86,9 @@ def build(verbose: bool = False) -> Path:
     tmp = LIB.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)])
     os.replace(tmp, LIB)
+    tmp = CEILING_LIB.with_suffix(".so.tmp")
+    _run([HIPCC, *HIP_FLAGS, "-shared", "-o", str(tmp), str(CSRC / "ceiling.hip")])
+    os.replace(tmp, CEILING_LIB)
     return LIB
 
 
