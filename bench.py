@@ -39,9 +39,7 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=400)
-    # Untimed launches before the timed region: the first ~500 launches after
-    # idle run about 4% slower while the GPU's clocks settle.
-    p.add_argument("--warmup", type=int, default=2000)
+    p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
     p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "promote", "c2b", "c5", "prefill", "ref"],
@@ -49,7 +47,12 @@ def parse():
                    help="c2a / promote / c2b: demotion / promotion / scoring microbenchmarks, c5: end-to-end random-init "
                         "Llama-3-8B decode through the HF hooks (each its own JSON line)")
     p.add_argument("--warm-format", choices=["absmax_i8", "ref_u8"], default="absmax_i8",
-                   help="c2a / promote: WARM codec (BASELINE's int8 absmax, or the reference's uint8 per-token)")
+                   help="c3 / c4 / c2a / promote: WARM codec (BASELINE's int8 absmax, or the reference's uint8 "
+                        "per-token)")
+    p.add_argument("--cold", choices=["masked", "zero_logit"], default="masked",
+                   help="c3 / c4: COLD semantics (BASELINE's masked eviction, or the reference's zero-logit tokens)")
+    p.add_argument("--scores", action="store_true",
+                   help="c3 / c4: the policy-step launch that also returns per-block probability sums")
     p.add_argument("--c5-steps", type=int, default=256)
     p.add_argument("--c5-batch", type=int, default=16)
     p.add_argument("--c5-prompt", type=int, default=2048)
@@ -67,6 +70,10 @@ def parse():
 
 
 def build_layers(args, device):
+    """``--layers`` distinct layer buffers of the C3 / C4 workload, generated
+    on the GPU from seeded generators; WARM tiles quantized on the GPU into
+    the ``--warm-format`` pools (BASELINE's int8 absmax, or the reference's
+    uint8 per-token codec)."""
     import torch
 
     from paged_tierkv_amd import kernels, workloads as W
@@ -81,15 +88,24 @@ def build_layers(args, device):
         shp = (case.kv_heads, case.block_size, case.head_dim)
         hot_k = torch.randn((hs, *shp), generator=gen, device=device, dtype=torch.float16)
         hot_v = torch.randn((hs, *shp), generator=gen, device=device, dtype=torch.float16)
-        warm_k = torch.empty((ws, *shp), device=device, dtype=torch.int8)
-        warm_v = torch.empty((ws, *shp), device=device, dtype=torch.int8)
-        k_scale = torch.empty((ws, case.kv_heads), device=device, dtype=torch.float32)
-        v_scale = torch.empty((ws, case.kv_heads), device=device, dtype=torch.float32)
+        if args.warm_format == "absmax_i8":
+            warm_k = torch.empty((ws, *shp), device=device, dtype=torch.int8)
+            warm_v = torch.empty((ws, *shp), device=device, dtype=torch.int8)
+            k_scale = torch.empty((ws, case.kv_heads), device=device, dtype=torch.float32)
+            v_scale = torch.empty((ws, case.kv_heads), device=device, dtype=torch.float32)
+            k_zero = v_zero = None
+        else:
+            warm_k = torch.empty((ws, *shp), device=device, dtype=torch.uint8)
+            warm_v = torch.empty((ws, *shp), device=device, dtype=torch.uint8)
+            meta = (ws, case.kv_heads, case.block_size, 1)
+            k_scale, k_zero, v_scale, v_zero = (torch.empty(meta, device=device, dtype=torch.float16)
+                                                for _ in range(4))
         src_k = torch.randn((ws, *shp), generator=gen, device=device, dtype=torch.float16)
         src_v = torch.randn((ws, *shp), generator=gen, device=device, dtype=torch.float16)
         idx = torch.arange(ws, dtype=torch.int32, device=device)
         kernels.demote_to_warm(src_k, src_v, idx, idx, torch.full((ws,), case.block_size, dtype=torch.int32),
-                               warm_k, warm_v, k_scale, None, v_scale, None, warm_format="absmax_i8")
+                               warm_k, warm_v, k_scale, k_zero, v_scale, v_zero, warm_format=args.warm_format,
+                               pad_tail=True)
         torch.cuda.synchronize()
         del src_k, src_v
         layers.append(dict(
@@ -97,37 +113,95 @@ def build_layers(args, device):
             args=dict(query_states=case.query.to(device), block_table=case.block_table.to(device),
                       block_states=case.block_states.to(device), block_lengths=case.block_lengths.to(device),
                       hot_k_pool=hot_k, hot_v_pool=hot_v, warm_k_pool=warm_k, warm_v_pool=warm_v,
-                      k_scale=k_scale, k_zero=None, v_scale=v_scale, v_zero=None,
+                      k_scale=k_scale, k_zero=k_zero, v_scale=v_scale, v_zero=v_zero,
                       num_blocks=case.num_blocks, num_key_value_groups=case.groups, scaling=case.scaling)))
     return layers
 
 
-def cpu_baseline(args, case_name):
-    """Oracle decode (NumPy restatement of _eager_reference_decode) on one
-    sequence of the same workload, repeated for ~cpu_seconds."""
-    import numpy as np  # noqa: F401
+def cpu_host_info():
+    """Threads for the CPU baseline and what the host reports: the box asks
+    for at most 16 worker threads per GPU (OMP_NUM_THREADS), so the baseline
+    uses min(os.cpu_count(), OMP_NUM_THREADS)."""
+    import torch
 
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
-    from helpers import oracle_decode, oracle_warm
-    from paged_tierkv_amd import workloads as W
+    ncpu = os.cpu_count() or 1
+    want = min(ncpu, int(os.environ.get("OMP_NUM_THREADS", ncpu) or ncpu))
+    torch.set_num_threads(max(1, want))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"os_cpu_count": ncpu, "torch_threads": torch.get_num_threads(), "cpu_model": model}
 
-    mk = W.config3 if args.workload == "c3" else W.config4
-    case = mk(seed=100, batch=1)
-    warm = oracle_warm(case, "absmax_i8")
-    nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim)
-    oracle_decode(case, warm, "absmax_i8", "masked")
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        oracle_decode(case, warm, "absmax_i8", "masked")
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= args.cpu_seconds:
-            break
-    per = el / reps
-    return {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"1 of {32 if args.workload == 'c3' else 4} sequences of {case_name}, {reps} reps "
-                      f"({per * 1e3:.1f} ms/sequence; NumPy, single thread)",
-            "us_per_layer_step_extrapolated": round(per * 1e6 * (32 if args.workload == 'c3' else 4), 1)}
+
+def cpu_baseline(args, layer, nbytes_fn):
+    """The reference's CPU PyTorch decode path on this host
+    (``oracle.torch_ref``): the restatement of _eager_reference_decode
+    (tierkv_triton.py:708-820) with its per-block ``.item()`` loop,
+    ``torch.cat``, ``repeat_interleave`` and fp32 softmax, looping over
+    sequences as the reference serves a batch (main.py:1182-1189); and the
+    vectorized torch-CPU variant beside it.  Inputs are layer 0's own tensors
+    copied back from the GPU.  Each variant runs on a sample of the batch
+    sized to about ``--cpu-seconds`` for 10 timed iterations after 2
+    warm-ups, and both are checked against the NumPy oracle on that sample."""
+    import numpy as np
+    import torch
+
+    from oracle import decode as odecode
+    from oracle import torch_ref
+
+    info = cpu_host_info()
+    a = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in layer["args"].items()}
+    case = layer["case"]
+    cold = args.cold
+    fmt = args.warm_format
+    pos = (a["hot_k_pool"], a["hot_v_pool"], a["warm_k_pool"], a["warm_v_pool"], a["k_scale"], a["k_zero"],
+           a["v_scale"], a["v_zero"], case.num_blocks, case.groups, case.scaling)
+
+    def run(fn, seqs):
+        return fn(a["query_states"][seqs], a["block_table"][seqs], a["block_states"][seqs], a["block_lengths"][seqs],
+                  *pos, warm_format=fmt, cold_mode=cold)
+
+    res = {}
+    for name, fn in (("looped", torch_ref.eager_decode_looped), ("vectorized", torch_ref.vectorized_decode)):
+        t0 = time.perf_counter()
+        run(fn, slice(0, 1))
+        t1 = time.perf_counter() - t0
+        nseq = max(1, min(case.batch, int(args.cpu_seconds / 20 / max(t1, 1e-6))))
+        seqs = slice(0, nseq)
+        out = run(fn, seqs)
+        reps, t0 = 0, time.perf_counter()
+        while reps < 10:
+            run(fn, seqs)
+            reps += 1
+        per = (time.perf_counter() - t0) / reps
+        exp = odecode.decode_attention(
+            a["query_states"][seqs, :, 0].numpy(), a["block_table"][seqs].numpy(), a["block_states"][seqs].numpy(),
+            a["block_lengths"][seqs].numpy(), case.num_blocks,
+            *(None if t is None else t.numpy() for t in pos[:8]), case.groups, case.scaling, warm_format=fmt,
+            cold_mode=cold)
+        err = np.abs(out[:, 0].float().numpy() - exp)
+        if not (err <= 2e-3 + 1e-2 * np.abs(exp)).all():
+            raise AssertionError(f"CPU baseline ({name}) disagrees with the oracle: max abs err {err.max():.3e}")
+        nbytes = nbytes_fn(nseq)
+        res[name] = {"GBps": round(nbytes / per / 1e9, 4), "sec_per_iter": round(per, 4), "seqs": nseq,
+                     "us_per_layer_step_extrapolated": round(per / nseq * case.batch * 1e6, 1),
+                     "max_abs_err_vs_oracle": float(err.max())}
+        log(f"[bench] CPU {name}: {nseq} of {case.batch} sequences in {per * 1e3:.1f} ms "
+            f"({res[name]['GBps']} GB/s algorithmic, {info['torch_threads']} threads)")
+    lp = res["looped"]
+    return {"value": lp["GBps"], "unit": "GB/s", "cores": info["torch_threads"], "kind": "port",
+            "sample": (f"{lp['seqs']} of {case.batch} sequences of layer 0 of {case.name}, 10 iterations after 2 "
+                       f"warm-ups: the reference's eager decode (tierkv_triton.py:708-820) restated in torch on "
+                       f"the CPU (per-block .item() loop, torch.cat, repeat_interleave, fp32 softmax, a loop over "
+                       f"sequences), checked against the NumPy oracle"),
+            "us_per_layer_step_extrapolated": lp["us_per_layer_step_extrapolated"],
+            "vectorized_torch_cpu": res["vectorized"], **info}
 
 
 def copy_calibration(device):
@@ -151,13 +225,13 @@ def copy_calibration(device):
                       "GBps_read_plus_write": 2 * n / t / 1e9}))
 
 
-def ceiling(device, c3_bytes=216944640, stream_grids=(1024, 2048, 4096)):
+def ceiling(device, c3_bytes=216944640, stream_grids=(1024, 2048, 4096), reps=50, release=True):
     """HBM read ceilings of this box (libtierkv_ceiling.so): a non-temporal
     streaming read of 1 GiB, and a non-temporal gather of C3's ideal bytes
     (rounded to whole 4 KB tiles: 256 workgroups x 207 tiles) in a shuffled
     tile order out of the same 1 GiB buffer -- the decode kernel's access
-    pattern without its arithmetic.  Each is timed with HIP events over 50
-    launches after 20 untimed ones."""
+    pattern without its arithmetic.  Each is timed with HIP events over
+    ``reps`` launches after ``reps // 2`` untimed ones."""
     import ctypes
 
     import torch
@@ -181,16 +255,16 @@ def ceiling(device, c3_bytes=216944640, stream_grids=(1024, 2048, 4096)):
     order = torch.randperm(n // 4096, generator=gen)[:n_wg * per_wg].to(torch.int32).to(device)
 
     def timed(call, nbytes):
-        for _ in range(20):
+        for _ in range(max(reps // 2, 1)):
             assert call() == 0
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        for _ in range(50):
+        for _ in range(reps):
             call()
         e1.record()
         e1.synchronize()
-        t = e0.elapsed_time(e1) / 1e3 / 50
+        t = e0.elapsed_time(e1) / 1e3 / reps
         return t, nbytes / t / 1e9
 
     res = {"mode": "ceiling"}
@@ -202,7 +276,8 @@ def ceiling(device, c3_bytes=216944640, stream_grids=(1024, 2048, 4096)):
                                                      sink.data_ptr(), stream), gbytes)
     res.update(gather_4k_tiles_bytes=gbytes, gather_4k_tiles_us=round(t * 1e6, 2), gather_4k_tiles_GBps=round(gbs, 1))
     del src, order
-    torch.cuda.empty_cache()
+    if release:
+        torch.cuda.empty_cache()
     return res
 
 
@@ -599,26 +674,9 @@ C5_METRIC = ("C5 end-to-end decode tokens/s + resident KV bytes, random-init Lla
 
 
 def c5_model(device):
-    """Random-init Llama-3-8B-shaped decoder:
-    32 layers, hidden 4096, 32 / 8 heads, head_dim 128, FFN 14336, vocab
-    128256, fp16 weights ~N(0, 0.02) (transformers' own init with
-    initializer_range 0.02), built directly on the GPU."""
-    import torch
-    from transformers import LlamaConfig, LlamaForCausalLM
+    from paged_tierkv_amd import workloads as W
 
-    cfg = LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=32, num_attention_heads=32,
-                      num_key_value_heads=8, head_dim=128, vocab_size=128256, max_position_embeddings=8192,
-                      rope_theta=500000.0, initializer_range=0.02, rms_norm_eps=1e-5, tie_word_embeddings=False)
-    cfg._attn_implementation = "sdpa"
-    torch.manual_seed(0)
-    prev = torch.get_default_dtype()
-    torch.set_default_dtype(torch.float16)
-    try:
-        with torch.device(device):
-            model = LlamaForCausalLM(cfg).eval()
-    finally:
-        torch.set_default_dtype(prev)
-    return model
+    return W.llama3_8b_random(device)
 
 
 def c5_generate(model, prompt, cache, steps, runtime=None):
@@ -826,9 +884,6 @@ def main():
         sys.exit(2)
     import torch
 
-    from paged_tierkv_amd import workloads as W
-    from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention, workspace_error_word
-
     device = torch.device("cuda:0")
     if args.mode == "copy":
         copy_calibration(device)
@@ -854,33 +909,75 @@ def main():
     if args.workload == "c2b":
         run_c2b(args, device)
         return
-    log(f"[bench] building {args.layers} layers of {args.workload} on {torch.cuda.get_device_name(0)}")
+    run_decode(args, device)
+
+
+def run_decode(args, device):
+    """C3 (default) / C4: one step = one decode-attention launch for one layer
+    over the whole batch; ``--layers`` layer buffers rotate.
+
+    Order: the box's HBM ceilings first, then W untimed warm-up steps and
+    exactly K timed steps.  After a few seconds idle the GPU's clocks go
+    through a transient of about 20 ms of sustained load (measured on the
+    box: C3 launches run 3-8 % slow for the first ~400 launches, whatever
+    the kernel that supplies the load); the ceiling measurement (about 0.1 s
+    of streaming and gathering HBM reads) runs immediately before the decode
+    steps, so K timed steps see the steady clocks a serving loop sees.  Every launch is a
+    ``PreparedDecode`` (validated and bound once: one C call per step, a few
+    microseconds of host time), and the K timed launches are enqueued while
+    the warm-up launches still run, so the timed region holds the K kernels
+    back to back -- a host synchronisation between warm-up and timing would
+    put the enqueue cost of the first timed call inside a short run's timed
+    region.  Both sides of the run are bracketed by a device synchronisation."""
+    import torch
+
+    from paged_tierkv_amd import workloads as W
+    from paged_tierkv_amd.tierkv_hip import PreparedDecode, workspace_error_word
+
+    scores = bool(args.scores)
+    fmt = args.warm_format
+    log(f"[bench] building {args.layers} layers of {args.workload} ({fmt}, cold {args.cold}, scores {scores}) on "
+        f"{torch.cuda.get_device_name(0)}")
     layers = build_layers(args, device)
     case = layers[0]["case"]
-    nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim)
-    splits = args.splits or None
+    nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim,
+                           warm_format=fmt, return_scores=scores)
 
-    def step(i):
-        tierkv_decode_attention(**layers[i % len(layers)]["args"], cold_mode="masked", splits=splits)
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    assert workspace_error_word(device) == 0, "kernel flagged an out-of-range slot"
+    plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=args.cold, splits=args.splits or None)
+             for L in layers]
+    # The first warm-up step of each layer runs before the ceiling
+    # measurement: a kernel's first launch in a process loads its code object
+    # (milliseconds of host time, the GPU idle meanwhile).
+    pre = min(args.warmup, len(plans))
+    for i in range(pre):
+        plans[i].launch()
+    # The box's own ceiling for this access pattern: the same bytes gathered
+    # as shuffled 4 KB tiles with the decode kernel's load policy, no
+    # arithmetic; and a streaming read.
+    ceil = ceiling(device, c3_bytes=nbytes, stream_grids=(4096,), reps=400, release=False)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(pre, args.warmup):
+        plans[i % len(plans)].launch()
+    h0 = time.perf_counter()
     e0.record()
     for i in range(args.steps):
-        step(i)
+        plans[(args.warmup + i) % len(plans)].launch()
     e1.record()
+    host = (time.perf_counter() - h0) / max(args.steps, 1)
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) / 1e3 / args.steps
+    assert workspace_error_word(device) == 0, "kernel flagged an out-of-range slot"
     gbs = nbytes / sec / 1e9
-    log(f"[bench] {sec * 1e6:.2f} us/layer-step, {gbs:.1f} GB/s algorithmic ({gbs / PEAK_HBM_GBS:.1%} of peak)")
+    log(f"[bench] measured ceilings: gather {ceil['gather_4k_tiles_GBps']} GB/s, stream read "
+        f"{ceil['stream_read_grid4096_GBps']} GB/s")
+    log(f"[bench] {sec * 1e6:.2f} us/layer-step, {gbs:.1f} GB/s algorithmic ({gbs / PEAK_HBM_GBS:.1%} of peak); "
+        f"host enqueue {host * 1e6:.1f} us per launch")
 
     # HBM bytes per launch of the decode kernel from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE summary of this workload (copy-calibrated).
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"tiered_decode_kernel_{case.name}_traffic.json")
+    tag = _decode_tag(case.name, fmt, args.cold, scores)
+    tpath = os.path.join(ROOT, "profiles", f"tiered_decode_kernel_{tag}_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -888,17 +985,17 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing the CPU baseline")
-        cpu = cpu_baseline(args, case.name)
-    # The box's own ceiling for this access pattern: the same bytes gathered
-    # as shuffled 4 KB tiles with the decode kernel's load policy, no
-    # arithmetic (bench.py --mode ceiling has the stream-read figures too).
-    ceil = ceiling(device, c3_bytes=nbytes, stream_grids=(4096,))
+
+        def sample_bytes(nseq):
+            return W.ideal_bytes(case.block_states[:nseq], case.num_blocks, case.num_heads, case.kv_heads,
+                                 case.head_dim, warm_format=fmt)
+
+        cpu = cpu_baseline(args, layers[0], sample_bytes)
     measured_ceiling = {"gather_4k_tiles_GBps": ceil["gather_4k_tiles_GBps"],
                         "stream_read_GBps": ceil["stream_read_grid4096_GBps"],
                         "frac_of_gather": round(gbs / ceil["gather_4k_tiles_GBps"], 4)}
-    log(f"[bench] measured ceilings: gather {ceil['gather_4k_tiles_GBps']} GB/s, stream read "
-        f"{ceil['stream_read_grid4096_GBps']} GB/s; decode at {measured_ceiling['frac_of_gather']:.1%} of the gather")
-
+    fmt_name = ("int8 absmax per (block, kv head)" if fmt == "absmax_i8"
+                else "reference uint8 per-token asymmetric (fp16 scale + zero)")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -912,20 +1009,33 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": case.name, "batch": case.batch, "num_heads": case.num_heads,
+        "config": {"workload": tag, "batch": case.batch, "num_heads": case.num_heads,
                    "kv_heads": case.kv_heads, "head_dim": case.head_dim, "block_size": case.block_size,
                    "blocks_per_seq": case.num_blocks, "tiers_per_seq": list(case.tier_counts()[0]),
-                   "warm_format": "int8 absmax per (block, kv head)", "cold": "masked",
+                   "warm_format": fmt_name, "cold": args.cold, "return_scores": scores,
                    "layers_rotated": args.layers},
         "us_per_layer_step": round(sec * 1e6, 3),
         "tokens_per_s_32_layers": round(case.batch / (32 * sec), 1),
         "ideal_bytes_per_step": nbytes,
+        "host_enqueue_us_per_launch": round(host * 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic},
         "measured_ceiling": measured_ceiling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def _decode_tag(name, fmt, cold, scores):
+    """Workload name of a decode bench line (and of its profile files)."""
+    tag = name
+    if fmt != "absmax_i8":
+        tag += "_ref_u8"
+    if cold != "masked":
+        tag += "_" + cold
+    if scores:
+        tag += "_scores"
+    return tag
 
 
 if __name__ == "__main__":

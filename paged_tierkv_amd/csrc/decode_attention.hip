@@ -44,7 +44,15 @@ constexpr int MAX_LIST = 512;      // resident blocks per workgroup (LDS list)
 constexpr int MAX_WAVES = 8;
 constexpr int PRE_CHUNKS = 4;      // table-row chunks loaded together by the list build
 constexpr int MERGE_UNROLL = 8;    // split partials loaded together by the merge
-constexpr int SCORE_UNROLL = 4;    // score elements per thread whose loads are in flight together
+constexpr int MAX_LDS_STAGE = 48 * 1024;   // bytes of per-block score statistics kept in LDS
+// Where a score launch stages each block's (max, sum) per head:
+//   STAGE_GLOBAL    workspace [B][H][num_blocks], written per tile (fallback);
+//   STAGE_LDS_BLOCK LDS [G][num_blocks] by logical block (unsplit launches);
+//   STAGE_LDS_LIST  LDS [G][stage_cap] by list position, copied to the
+//                   workspace once at the end of the workgroup (split launches).
+constexpr int STAGE_GLOBAL = 0;
+constexpr int STAGE_LDS_BLOCK = 1;
+constexpr int STAGE_LDS_LIST = 2;
 constexpr int MAX_SPLIT_UNITS = 1 << 16;   // units per launch when a unit is split
 constexpr float PBOOST = 64.f;     // P is scaled by 2^6 before its fp16 cast
 constexpr float LAZY_T = 8.f;      // log2 headroom of the running maximum
@@ -77,9 +85,11 @@ struct DecodeParams {
   float scaling;
   int32_t splits;
   uint32_t split_magic;   // ceil(2^32 / splits) when num_blocks * splits < 2^32, else 0
+  int32_t lds_stage;      // where score statistics are staged (STAGE_* below)
+  int32_t stage_cap;      // STAGE_LDS_LIST: entries per head in the LDS stage
   float* ws_acc;      // [units][splits][G][D]
   float* ws_ml;       // [units][splits][G][2]
-  float* ws_stage;    // [B][H][num_blocks][2]  (block reference max, block sum)
+  float* ws_stage;    // [B][H][num_blocks][2]  per-block (max, sum) (split score launches)
   uint32_t* ws_cnt;   // [MAX_SPLIT_UNITS] split arrival counters, zero between launches
   int32_t* ws_err;
   float* score_sums;  // [B][H][table_stride] or null
@@ -112,13 +122,25 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
 __device__ __forceinline__ float load_dev(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A staged (max, sum) pair as one 8-byte device-coherent access.
+__device__ __forceinline__ void store_dev2(float* p, float2 v) {
+  const uint64_t bits = (uint64_t(__float_as_uint(v.y)) << 32) | __float_as_uint(v.x);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_dev2(const float* p) {
+  const uint64_t bits = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float(uint32_t(bits)), __uint_as_float(uint32_t(bits >> 32)));
+}
 
 // --------------------------------------------------------------------------
 // Fast path
 // --------------------------------------------------------------------------
 
 // Tiles in registers.  Lane (n = lane & 15, g = lane >> 4) holds
-//   k: token n, dims g*D/4 .. +D/4;
+//   k: token n; HOT: dims 32i + 8g .. +7 of load i, WARM: dims 64i + 16g
+//      .. +15 of load i (each load instruction covers whole 64-byte row
+//      segments);
 //   v: tokens 4g + j (j = 0..3), dims n*D/16 .. +D/16 (row j at v[j*RW]);
 // HOT tiles as fp16 pairs, WARM tiles as 8-bit codes plus metadata
 // (absmax: s_k, s_v; reference format: fp16 pairs of the per-token k scale,
@@ -156,6 +178,14 @@ constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 buffer descriptor: raw 32-bit d
 #define TIERKV_TILE_CPOL 2
 #endif
 constexpr int TILE_CPOL = TIERKV_TILE_CPOL;
+// Tiles in flight per wave (register pipeline depth) in the HOT and WARM
+// loops.
+#ifndef TIERKV_NBH
+#define TIERKV_NBH 2
+#endif
+#ifndef TIERKV_NBW
+#define TIERKV_NBW 2
+#endif
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, RSRC_WORD3);
@@ -200,10 +230,12 @@ __device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int sl
   const int64_t tile0 = (int64_t(slot) * p.kv_heads + kvh) * FBS;
   const auto rk = tile_rsrc(reinterpret_cast<const uint8_t*>(p.warm_k) + tile0 * D, live ? TILE : 0u);
   const auto rv = tile_rsrc(reinterpret_cast<const uint8_t*>(p.warm_v) + tile0 * D, live ? TILE : 0u);
-  const int ko = n * D + g * (D / 4);
+  // Instruction i reads bytes [64i, 64i + 64) of every row (whole 64-byte
+  // segments, as for HOT K); lane g's 16 bytes are dims 64i + 16g .. +15.
+  const int ko = n * D + 16 * g;
 #pragma unroll
   for (int i = 0; i < D / 64; ++i) {
-    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 16 * i, 0, TILE_CPOL);
+    const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rk, ko + 64 * i, 0, TILE_CPOL);
     t.k[4 * i + 0] = x.x; t.k[4 * i + 1] = x.y; t.k[4 * i + 2] = x.z; t.k[4 * i + 3] = x.w;
   }
 #pragma unroll
@@ -255,38 +287,68 @@ struct WaveState {
   float corr;
 };
 
+template <int D>
+__device__ __forceinline__ void rescale_state(float m_new, WaveState<D>& ws) {
+  const float alpha = (ws.m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ws.m_run - m_new);
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s) ws.acc[s] *= alpha;
+  ws.l_part *= alpha;
+  ws.corr *= alpha;
+  ws.m_run = m_new;
+}
+
 // Lazy online-softmax update for the four logits x[] of this lane; returns
 // p[r] = 2^(x[r] - m_run).  The running maximum is re-based (and the state
 // rescaled) only when a logit exceeds it by more than LAZY_T.
+//
+// With SCORES the block's own statistics are staged per head at stage index
+// si (the tile's logical block, or its list position): its maximum
+// logit bm and bs = sum_t 2^(x_t - bm), both functions of the block's logits
+// alone (a fixed reduction over the 16 tokens), so they do not depend on the
+// order in which waves and splits met the blocks.  P is then formed as
+// 2^(x - bm) * 2^(bm - m_run).
 template <int D, bool SCORES>
 __device__ __forceinline__ void softmax_step(const DecodeParams& p, const float* x, float* pr, int lane,
-                                             bool head_ok, int b, int qh, int blk, WaveState<D>& ws) {
-  constexpr int DS = D / 16;
+                                             bool head_ok, int b, int qh, int si, float* s_stage,
+                                             WaveState<D>& ws) {
   const int g = lane >> 4;
   const float lm = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-  if (__any(head_ok && lm > ws.m_run + LAZY_T)) {
-    float tm = fmaxf(lm, shfl_xor_f(lm, 16));
-    tm = fmaxf(tm, shfl_xor_f(tm, 32));
-    const float m_new = fmaxf(ws.m_run, tm);
-    const float alpha = (ws.m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ws.m_run - m_new);
-#pragma unroll
-    for (int s = 0; s < DS; ++s) ws.acc[s] *= alpha;
-    ws.l_part *= alpha;
-    ws.corr *= alpha;
-    ws.m_run = m_new;
-  }
-#pragma unroll
-  for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(x[r] - ws.m_run);
-  const float psum = (pr[0] + pr[1]) + (pr[2] + pr[3]);
-  ws.l_part += psum;
   if constexpr (SCORES) {
-    float ls = psum + shfl_xor_f(psum, 16);
-    ls += shfl_xor_f(ls, 32);
-    if (g == 0 && head_ok) {
-      float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + blk) * 2;
-      store_dev(sp, ws.m_run);
-      store_dev(sp + 1, ls);
+    float bm = fmaxf(lm, xor16_f(lm));
+    bm = fmaxf(bm, xor32_f(bm));
+    if (__any(head_ok && bm > ws.m_run + LAZY_T)) {
+      rescale_state<D>(fmaxf(ws.m_run, bm), ws);
     }
+    const float bmr = (bm == -INFINITY) ? 0.f : bm;
+    float e[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) e[r] = __builtin_amdgcn_exp2f(x[r] - bmr);
+    const float es = (e[0] + e[1]) + (e[2] + e[3]);
+    float bs = es + xor16_f(es);
+    bs += xor32_f(bs);
+    if (g == 0 && head_ok) {
+      if (s_stage) {
+        // LDS stage [G][row] of (max, sum) at this tile's stage index (its
+        // logical block or its list position); lane n < G is head n.
+        const int row = (p.lds_stage == STAGE_LDS_LIST) ? p.stage_cap : p.num_blocks;
+        reinterpret_cast<float2*>(s_stage)[(lane & 15) * row + si] = make_float2(bm, bs);
+      } else {
+        store_dev2(p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + si) * 2, make_float2(bm, bs));
+      }
+    }
+    const float f = __builtin_amdgcn_exp2f(bmr - ws.m_run);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = e[r] * f;
+    ws.l_part += es * f;
+  } else {
+    if (__any(head_ok && lm > ws.m_run + LAZY_T)) {
+      float tm = fmaxf(lm, xor16_f(lm));
+      tm = fmaxf(tm, xor32_f(tm));
+      rescale_state<D>(fmaxf(ws.m_run, tm), ws);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = __builtin_amdgcn_exp2f(x[r] - ws.m_run);
+    ws.l_part += (pr[0] + pr[1]) + (pr[2] + pr[3]);
   }
 }
 
@@ -299,8 +361,9 @@ __device__ __forceinline__ void mask_tail(float* x, int g, int len) {
 }
 
 template <int D, bool SCORES>
-__device__ __forceinline__ void process_hot(const DecodeParams& p, const HotTile<D>& t, int blk, int len, int lane,
-                                            bool head_ok, int b, int qh, const uint32_t* qv, WaveState<D>& ws) {
+__device__ __forceinline__ void process_hot(const DecodeParams& p, const HotTile<D>& t, int si, int len, int lane,
+                                            bool head_ok, int b, int qh, const uint32_t* qv, float* s_stage,
+                                            WaveState<D>& ws) {
   constexpr int DS = D / 16;
   constexpr int RW = HotTile<D>::RW;
   // S^T = K Q^T
@@ -313,7 +376,7 @@ __device__ __forceinline__ void process_hot(const DecodeParams& p, const HotTile
 #pragma unroll
   for (int r = 0; r < 4; ++r) x[r] = sacc[r] * p.scale_log2;
   mask_tail(x, lane >> 4, len);
-  softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, blk, ws);
+  softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, si, s_stage, ws);
   // O^T += V^T P^T; the A operand of step s is {V[4g + j][n*DS + s]}_j.
   const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
 #pragma unroll
@@ -327,9 +390,9 @@ __device__ __forceinline__ void process_hot(const DecodeParams& p, const HotTile
 }
 
 template <int D, int WF, bool SCORES>
-__device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTile<D, WF>& t, int blk, int len,
+__device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTile<D, WF>& t, int si, int len,
                                              int lane, bool head_ok, int b, int qh, const uint32_t* qv, float qsum,
-                                             WaveState<D>& ws) {
+                                             float* s_stage, WaveState<D>& ws) {
   constexpr int DS = D / 16;
   constexpr int RW = WarmTile<D, WF>::RW;
   // S^T = (K + offset) Q^T with the codes as exact fp16 integers.
@@ -354,7 +417,7 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
     }
   }
   mask_tail(x, lane >> 4, len);
-  softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, blk, ws);
+  softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, si, s_stage, ws);
 
   // O^T += V^T P^T: transpose the four rows' codes so that vt[s] holds the
   // four tokens of dim n*DS + s.
@@ -439,6 +502,38 @@ __device__ __forceinline__ void cold_adjust(float& M, float& L, float& f, float 
   }
 }
 
+// Combine two (max, sum-relative-to-max) pairs of base-2 softmax statistics.
+// Symmetric in its operands bit for bit (max, and one product per operand
+// added commutatively), so a butterfly over lanes gives every lane the same
+// value and the result depends only on the pairs, not on who combines them.
+__device__ __forceinline__ void combine_ms(float& m, float& s, float m2, float s2) {
+  const float M = fmaxf(m, m2);
+  if (M == -INFINITY) return;
+  const float a = (m == -INFINITY) ? 0.f : s * __builtin_amdgcn_exp2f(m - M);
+  const float c = (m2 == -INFINITY) ? 0.f : s2 * __builtin_amdgcn_exp2f(m2 - M);
+  m = M;
+  s = a + c;
+}
+
+// Value of lane 16 * (lane / 16) + (lane + N) % 16 (DPP row rotate).
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf, false));
+}
+
+// Every lane receives the combination of the wave's 64 (max, sum) pairs, in
+// a fixed order: row rotations by 8, 4, 2, 1 (after each, lanes that are
+// paired hold bit-identical values because combine_ms is symmetric), then
+// the 16- and 32-lane exchanges.
+__device__ __forceinline__ void wave_combine_ms(float& m, float& s) {
+  combine_ms(m, s, row_ror<8>(m), row_ror<8>(s));
+  combine_ms(m, s, row_ror<4>(m), row_ror<4>(s));
+  combine_ms(m, s, row_ror<2>(m), row_ror<2>(s));
+  combine_ms(m, s, row_ror<1>(m), row_ror<1>(s));
+  combine_ms(m, s, xor16_f(m), xor16_f(s));
+  combine_ms(m, s, xor32_f(m), xor32_f(s));
+}
+
 // The arguments the list build needs first come ahead of the parameter block
 // so that they can be preloaded into scalar registers at wave launch.
 template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT, int NW, bool LONG>
@@ -448,7 +543,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     const int32_t* __restrict__ a_seq_nblocks, int32_t a_stride, int32_t a_num_blocks,
     int32_t a_kv_heads, int32_t a_splits, DecodeParams p) {
   constexpr int DS = D / 16;
-  extern __shared__ float s_dyn[];               // [NW][G][D] wave accumulators
+  extern __shared__ float s_dyn[];               // [NW][G][D] wave accumulators, then the LDS stage
   __shared__ int4 s_list[MAX_LIST];              // (block, slot, len, state)
   __shared__ int s_wcnt[2][PRE_CHUNKS * MAX_WAVES];   // per (chunk, wave): HOT / WARM counts
   __shared__ int s_wcold[MAX_WAVES];
@@ -456,8 +551,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   __shared__ int s_next[2];                      // next WARM / HOT list position to hand out
   __shared__ float s_m[MAX_WAVES][16];
   __shared__ float s_l[MAX_WAVES][16];
-  __shared__ float s_hm[16];                     // per head: resident (M, L) of the whole unit
-  __shared__ float s_hl[16];
+  __shared__ float s_tm[16];                     // score finalisation: per (head, part) max and sum
+  __shared__ float s_ts[16];
 
   const int G = p.groups;
   const int splits = a_splits;
@@ -473,6 +568,27 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // Blocks of this sequence: the per-sequence count is loaded together with
   // the first row chunk and applied afterwards.
   const int nb_ld = a_seq_nblocks ? a_seq_nblocks[b] : a_num_blocks;
+  // Per-block score statistics (max, sum) per head (STAGE_* modes above).
+  const int stage_mode = p.lds_stage;
+  float* s_stage = (SCORES && stage_mode != STAGE_GLOBAL) ? s_dyn + NW * G * D : nullptr;
+  const bool list_stage = SCORES && stage_mode == STAGE_LDS_LIST;
+  float* const gstage_unit = p.ws_stage + (int64_t(b) * p.num_heads + int64_t(kvh) * G) * p.num_blocks * 2;
+  // A block that no tile will visit gets an entry too, so the staged
+  // statistics describe every block below the row's count: (-inf, -len) for a
+  // COLD block whose tokens enter the softmax (zero-logit mode), (-inf, 0)
+  // for one that contributes nothing.  In the workspace (split launches) the
+  // split whose index is congruent to the block writes it.
+  auto stage_blank = [&](int st, int len) {
+    return make_float2(-INFINITY, (COLD_ZERO && st == COLD) ? -float(len) : 0.f);
+  };
+  auto stage_init = [&](int idx, int st, int len) {
+    if (stage_mode == STAGE_LDS_BLOCK) {
+      for (int h = 0; h < G; ++h) reinterpret_cast<float2*>(s_stage)[h * p.num_blocks + idx] = stage_blank(st, len);
+    } else if (stage_mode == STAGE_GLOBAL && idx % splits == split) {
+      for (int h = 0; h < G; ++h)
+        store_dev2(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2, stage_blank(st, len));
+    }
+  };
   if (tid == 0) {
     s_next[0] = 0;
     s_next[1] = 0;
@@ -486,9 +602,10 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   uint4 qraw[D / 32], qraw_h[D / 32];
   {
     const QT* qrow = reinterpret_cast<const QT*>(a_q) + (int64_t(b) * p.num_heads + qh) * D;
-    const uint4* qp = reinterpret_cast<const uint4*>(qrow + g * (D / 4));
+    // WARM K permutation: for load il of a WARM K tile, dims 64il + 16g .. +15.
 #pragma unroll
-    for (int i = 0; i < D / 32; ++i) qraw[i] = qp[i];
+    for (int i = 0; i < D / 32; ++i)
+      qraw[i] = *reinterpret_cast<const uint4*>(qrow + 64 * (i >> 1) + 16 * g + 8 * (i & 1));
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) qraw_h[i] = *reinterpret_cast<const uint4*>(qrow + 32 * i + 8 * g);
   }
@@ -565,6 +682,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         bad |= (in_row && tiered && !slot_ok && len[k] > 0) ? 1 : 0;
         bad |= (in_row && !tiered && st[k] != COLD) ? 2 : 0;
         if (COLD_ZERO) cold_part += (in_row && st[k] == COLD) ? len[k] : 0;
+        if (SCORES && in_row && cls[k] == 0) stage_init(c0 + k * nthreads + tid, st[k], len[k]);
         const int nh = __popcll(__ballot(cls[k] == 1));
         const int nwm = __popcll(__ballot(cls[k] == 2));
         if (lane == 0) {
@@ -587,14 +705,17 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         const int j = uniform(k * nw + w);
         const int hb = seen_hot + __builtin_amdgcn_readlane(ih - ch, j);
         const int wb = seen_warm + __builtin_amdgcn_readlane(iw - cw, j);
-        const int4 ent = make_int4(c0 + k * nthreads + tid, slot[k], len[k], st[k]);
+        // .w: the entry's stage index (its list position with list staging,
+        // else its logical block).
+        const int idx = c0 + k * nthreads + tid;
         const uint64_t mh = __ballot(cls[k] == 1);
         const uint64_t mw = __ballot(cls[k] == 2);
         int q;
         if (cls[k] == 1) {
-          if (mine(hb + __popcll(mh & below), q)) s_list[q] = ent;
+          if (mine(hb + __popcll(mh & below), q)) s_list[q] = make_int4(idx, slot[k], len[k], list_stage ? q : idx);
         } else if (cls[k] == 2) {
-          if (mine(wb + __popcll(mw & below), q)) s_list[MAX_LIST - 1 - q] = ent;
+          if (mine(wb + __popcll(mw & below), q))
+            s_list[MAX_LIST - 1 - q] = make_int4(idx, slot[k], len[k], list_stage ? p.stage_cap - 1 - q : idx);
         }
       }
       seen_hot += __builtin_amdgcn_readlane(ih, 63);
@@ -628,6 +749,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         } else {
           bad |= 2;
         }
+        if (SCORES && !hot && !warm) stage_init(idx, st, len);
       }
       const uint64_t mh = __ballot(hot);
       const uint64_t mw = __ballot(warm);
@@ -646,10 +768,12 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         seen_warm += cw;
       }
       const uint64_t below = (1ull << lane) - 1ull;
-      const int4 ent = make_int4(idx, slot, len, st);
+      // .w: the entry's stage index (its list position with list staging,
+      // else its logical block).
       int q;
-      if (hot && mine(hb + __popcll(mh & below), q)) s_list[q] = ent;
-      if (warm && mine(wb + __popcll(mw & below), q)) s_list[MAX_LIST - 1 - q] = ent;
+      if (hot && mine(hb + __popcll(mh & below), q)) s_list[q] = make_int4(idx, slot, len, list_stage ? q : idx);
+      if (warm && mine(wb + __popcll(mw & below), q))
+        s_list[MAX_LIST - 1 - q] = make_int4(idx, slot, len, list_stage ? p.stage_cap - 1 - q : idx);
       if (c0 + nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
     }
   }
@@ -666,7 +790,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   const int nwarm = uniform((seen_warm > split) ? (seen_warm - split + splits - 1) / splits : 0);
 
   // ---- query (fp16) and its per-head sum ------------------------------------
-  // qv: dims g*D/4 .. +D/4 (the WARM K permutation), qvh: dims 32i + 8g .. +7
+  // qv: dims 64(i/2) + 16g + 8(i%2) .. +7 in word group i (the WARM K
+  // permutation), qvh: dims 32i + 8g .. +7
   // (the HOT K permutation); the same fp16 values in two orders.
   uint32_t qv[D / 8], qvh[D / 8];
   float qsum = 0.f;
@@ -718,8 +843,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     if (lane == 0) v = atomicAdd(&s_next[c], 1);
     return uniform(v);
   };
-  constexpr int NBH = 2;
-  constexpr int NBW = 2;
+  constexpr int NBH = TIERKV_NBH;
+  constexpr int NBW = TIERKV_NBW;
   HotTile<D> th[NBH];
   int4 eh[NBH];
   bool lh[NBH];
@@ -769,7 +894,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
         nl = gi < nwarm;
         if (lw[k])
-          process_warm<D, WF, SCORES>(p, tw[k], uniform(ew[k].x), uniform(ew[k].z), lane, head_ok, b, qh, qv, qsum, st);
+          process_warm<D, WF, SCORES>(p, tw[k], uniform(ew[k].w), uniform(ew[k].z), lane, head_ok, b, qh, qv, qsum,
+                                      s_stage, st);
       }
     } while (lw[0]);   // buffer 0 holds the next tile; positions are handed out in order
   }
@@ -786,7 +912,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         hne = s_list[min(gi, nhot - 1)];
         hnl = gi < nhot;
         if (lh[k])
-          process_hot<D, SCORES>(p, th[k], uniform(eh[k].x), uniform(eh[k].z), lane, head_ok, b, qh, qvh, st);
+          process_hot<D, SCORES>(p, th[k], uniform(eh[k].w), uniform(eh[k].z), lane, head_ok, b, qh, qvh, s_stage,
+                                 st);
       }
     } while (lh[0]);
   }
@@ -840,51 +967,91 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   QT* out = reinterpret_cast<QT*>(p.out) + (int64_t(b) * p.num_heads + kvh * G) * D;
 
   // Per-block probability sums of this unit's heads (tierkv_triton.py:121-145)
-  // from each head's resident (M, L) in s_hm / s_hl.  The loads of
-  // SCORE_UNROLL elements per thread are in flight together.
+  // from the staged per-block (bm, bs) pairs.  Each head's maximum M and
+  // denominator L over its blocks are reduced in a fixed order: the head's
+  // row is cut into `parts` contiguous ranges (one wave each), every lane
+  // folds its blocks in ascending order, the wave combines its lanes in a
+  // fixed order (wave_combine_ms), and the parts are combined in ascending
+  // order.  So score_sums
+  // are the same bits on every launch over the same inputs, whatever order
+  // the tiles were processed in (the labels ranked from them are
+  // reproducible); the attention output keeps its own (M, L).
+  // score = bs * 2^(bm - M) / L, or len * 2^-M / L for a COLD block of the
+  // zero-logit mode.  A lane's entries of a part (up to 16) are loaded
+  // together and, when the wave's only part fits in one such round, kept in
+  // registers for the second pass.
   auto finalize_scores = [&]() {
     const int stride = int(p.table_stride);
-    const int total = G * stride;
-    const int last_blk = max(nb - 1, 0);
-    for (int c0 = 0; c0 < total; c0 += SCORE_UNROLL * nthreads) {
-      int stv[SCORE_UNROLL], lnv[SCORE_UNROLL], slv[SCORE_UNROLL];
-      float smv[SCORE_UNROLL], ssv[SCORE_UNROLL];
+    const int parts = (G <= nw) ? nw / G : 1;
+    const int ntask = G * parts;
+    const int chunk = (nb + parts - 1) / parts;
+    auto entry = [&](int h, int blk) -> float2 {
+      if (stage_mode == STAGE_LDS_BLOCK) return reinterpret_cast<const float2*>(s_stage)[h * p.num_blocks + blk];
+      return load_dev2(gstage_unit + (int64_t(h) * p.num_blocks + blk) * 2);
+    };
+    // U entries per lane per round; the caller picks the smallest U that
+    // covers a part in one round (rows up to 64 * U blocks per part).
+    auto run = [&](auto u_const) {
+      constexpr int U = decltype(u_const)::value;
+      const bool reuse = ntask <= nw && chunk <= 64 * U;
+      float2 kept[U];
+      for (int t = w; t < ntask; t += nw) {
+        const int h = t / parts;
+        const int lo = (t - h * parts) * chunk;
+        const int hi = min(nb, lo + chunk);
+        float m = -INFINITY, sum = 0.f;
+        for (int c0 = lo; c0 < hi; c0 += U * 64) {
 #pragma unroll
-      for (int k = 0; k < SCORE_UNROLL; ++k) {
-        // Clamped indices: every load is in bounds and none needs a branch.
-        const int i = min(c0 + k * nthreads + tid, total - 1);
-        const int h = i / stride;
-        const int blk = min(i - h * stride, last_blk);
-        const int64_t o = int64_t(b) * p.table_stride + blk;
-        stv[k] = p.states[o];
-        lnv[k] = p.lengths[o];
-        slv[k] = p.table[o];
-        const float* sp = p.ws_stage + ((int64_t(b) * p.num_heads + kvh * G + h) * p.num_blocks + blk) * 2;
-        smv[k] = load_dev(sp);
-        ssv[k] = load_dev(sp + 1);
+          for (int u = 0; u < U; ++u) kept[u] = entry(h, min(c0 + u * 64 + lane, hi - 1));
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            if (c0 + u * 64 + lane < hi) combine_ms(m, sum, kept[u].x, kept[u].y);
+        }
+        wave_combine_ms(m, sum);
+        if (lane == 0) {
+          s_tm[t] = m;
+          s_ts[t] = sum;
+        }
       }
-#pragma unroll
-      for (int k = 0; k < SCORE_UNROLL; ++k) {
-        const int i = c0 + k * nthreads + tid;
-        if (i >= total) continue;
-        const int h = i / stride;
-        const int blk = i - h * stride;
-        float M = s_hm[h], L = s_hl[h], f;
+      __syncthreads();
+      for (int t = w; t < ntask; t += nw) {
+        const int h = t / parts;
+        const int k0 = t - h * parts;
+        float M = -INFINITY, L = 0.f;
+        for (int k = 0; k < parts; ++k) combine_ms(M, L, s_tm[h * parts + k], s_ts[h * parts + k]);
+        float f;
         cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
-        float v = 0.f;
-        if (blk < nb && L > 0.f) {
-          const int st = stv[k];
-          const int len = min(max(lnv[k], 0), FBS);
-          if (st == COLD) {
-            v = COLD_ZERO ? float(len) * __builtin_amdgcn_exp2f(-M) / L : 0.f;
-          } else if ((st == HOT || st == WARM) && len > 0) {
-            const int64_t cap = (st == HOT) ? p.hot_slots : p.warm_slots;
-            if (slv[k] >= 0 && slv[k] < cap) v = ssv[k] * __builtin_amdgcn_exp2f(smv[k] - M) / L;
+        const float inv_l = (L > 0.f) ? 1.f / L : 0.f;
+        const float cold_p = COLD_ZERO ? __builtin_amdgcn_exp2f(-M) * inv_l : 0.f;
+        float* dst = p.score_sums + (int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride;
+        // Part k writes blocks [min(k * chunk, nb), min((k + 1) * chunk, nb));
+        // the last part also writes the zeros of [nb, stride).
+        const int lo = min(k0 * chunk, nb);
+        const int hi_nb = min(nb, (k0 + 1) * chunk);
+        const int hi = (k0 == parts - 1) ? stride : hi_nb;
+        for (int c0 = lo; c0 < hi; c0 += U * 64) {
+          if (!reuse) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) kept[u] = entry(h, min(c0 + u * 64 + lane, max(hi_nb - 1, 0)));
+          }
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int blk = c0 + u * 64 + lane;
+            if (blk >= hi) continue;
+            float v = 0.f;
+            if (blk < hi_nb) {
+              const float2 e = kept[u];
+              if (e.y < 0.f) v = -e.y * cold_p;
+              else if (e.x != -INFINITY) v = e.y * __builtin_amdgcn_exp2f(e.x - M) * inv_l;
+            }
+            dst[blk] = v;
           }
         }
-        p.score_sums[(int64_t(b) * p.num_heads + kvh * G + h) * p.table_stride + blk] = v;
       }
-    }
+    };
+    if (chunk <= 128) run(std::integral_constant<int, 2>{});
+    else if (chunk <= 256) run(std::integral_constant<int, 4>{});
+    else run(std::integral_constant<int, 16>{});
   };
 
   if (splits == 1) {
@@ -896,16 +1063,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
       out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
     }
-    if (SCORES) {
-      if (tid < G) {
-        float M, L, fw[NW];
-        wave_ml(tid, M, L, fw);
-        s_hm[tid] = M;
-        s_hl[tid] = L;
-      }
-      __syncthreads();
-      finalize_scores();
-    }
+    if (SCORES) finalize_scores();
     return;
   }
 
@@ -919,6 +1077,30 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     if (i - h * D == 0) {
       store_dev(p.ws_ml + pi * 2 + 0, M);
       store_dev(p.ws_ml + pi * 2 + 1, L);
+    }
+  }
+  if (list_stage) {
+    // The statistics this workgroup staged in LDS go to the workspace by
+    // logical block, and so do the blocks without a tile that it owns (index
+    // congruent to its split): one round of stores, covered by the wait
+    // before the arrival.
+    const int nlist = nhot + nwarm;
+    for (int i = tid; i < G * nlist; i += nthreads) {
+      const int h = i / nlist;
+      const int j = i - h * nlist;
+      const int4 e = (j < nhot) ? s_list[j] : s_list[MAX_LIST - 1 - (j - nhot)];
+      store_dev2(gstage_unit + (int64_t(h) * p.num_blocks + e.x) * 2,
+                 reinterpret_cast<const float2*>(s_stage)[h * p.stage_cap + e.w]);
+    }
+    for (int idx = split + tid * splits; idx < nb; idx += nthreads * splits) {
+      const int64_t o = int64_t(b) * p.table_stride + idx;
+      const int st = p.states[o];
+      const int len = min(max(p.lengths[o], 0), FBS);
+      const int slot = p.table[o];
+      const bool resident = (st == HOT || st == WARM) && len > 0 &&
+                            uint32_t(slot) < ((st == HOT) ? hot_cap : warm_cap);
+      if (!resident)
+        for (int h = 0; h < G; ++h) store_dev2(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2, stage_blank(st, len));
     }
   }
   // Every wave's device-coherent stores complete before the arrival is counted.
@@ -968,18 +1150,11 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         M = Mn;
       }
     }
-    if (SCORES && d == 0) {
-      s_hm[h] = M;
-      s_hl[h] = L;
-    }
     float f;
     cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
     out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
   }
-  if (SCORES) {
-    __syncthreads();
-    finalize_scores();
-  }
+  if (SCORES) finalize_scores();
 }
 
 // --------------------------------------------------------------------------
@@ -1153,7 +1328,10 @@ static Plan plan_launch(int batch, int kv_heads, int num_blocks, int groups, int
     splits = int(std::max<int64_t>(1, (target_waves + units * pl.nw - 1) / (units * pl.nw)));
     splits = std::min(splits, std::max(1, num_blocks / (4 * pl.nw)));
   }
-  splits = std::max(splits, (num_blocks + MAX_LIST - 1) / MAX_LIST);
+  // A split's list holds ceil(hot / splits) + ceil(warm / splits) entries,
+  // at most ceil(num_blocks / splits) + 1: MAX_LIST - 1 blocks per split keep
+  // the HOT (front) and WARM (back) halves of the list apart.
+  splits = std::max(splits, (num_blocks + MAX_LIST - 2) / (MAX_LIST - 1));
   splits = std::min(splits, std::max(1, num_blocks));
   pl.splits = std::max(1, splits);
   return pl;
@@ -1192,7 +1370,9 @@ static WsLayout ws_layout(int batch, int num_heads, int kv_heads, int num_blocks
 
 template <int D, int WF, bool SC, bool CZ, typename QT, int NW>
 static void launch_nw(const DecodeParams& p, bool long_rows, int grid, hipStream_t stream) {
-  const size_t shmem = size_t(NW) * p.groups * D * sizeof(float);
+  size_t shmem = size_t(NW) * p.groups * D * sizeof(float);
+  if (SC && p.lds_stage == STAGE_LDS_BLOCK) shmem += size_t(p.groups) * p.num_blocks * 2 * sizeof(float);
+  if (SC && p.lds_stage == STAGE_LDS_LIST) shmem += size_t(p.groups) * p.stage_cap * 2 * sizeof(float);
   const int32_t stride = int32_t(p.table_stride);
   if (long_rows)
     hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, true>), dim3(grid), dim3(NW * 64), shmem, stream,
@@ -1344,6 +1524,21 @@ extern "C" int32_t tierkv_decode_attention(
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, p.groups, splits_hint);
     p.splits = pl.splits;
     p.split_magic = 0;
+    // Unsplit score launches keep the per-block statistics in LDS (up to
+    // MAX_LDS_STAGE bytes per workgroup); split ones share them through the
+    // workspace, since the last workgroup of a unit finalises every block.
+    p.lds_stage = STAGE_GLOBAL;
+    p.stage_cap = 0;
+    if (scores) {
+      const int64_t pair = 2 * int64_t(sizeof(float));
+      const int cap = std::min<int>(MAX_LIST, (num_blocks + pl.splits - 1) / pl.splits + 1);
+      if (pl.splits == 1 && int64_t(p.groups) * num_blocks * pair <= MAX_LDS_STAGE) {
+        p.lds_stage = STAGE_LDS_BLOCK;
+      } else if (pl.splits > 1 && int64_t(p.groups) * cap * pair <= MAX_LDS_STAGE) {
+        p.lds_stage = STAGE_LDS_LIST;
+        p.stage_cap = cap;
+      }
+    }
     if (pl.splits > 1 && int64_t(num_blocks) * pl.splits < (int64_t(1) << 32))
       p.split_magic = uint32_t(((uint64_t(1) << 32) + uint64_t(pl.splits) - 1) / uint64_t(pl.splits));
     // Split launches go out in chunks of whole sequences, at most

@@ -43,6 +43,21 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
+// The value of lane (lane ^ 16) / (lane ^ 32) through gfx950's lane-swap
+// instructions (two VALU operations, no LDS crossbar round trip).
+// v_permlane16_swap(a, b) exchanges the odd 16-lane rows of a with the even
+// rows of b; with a = b = v, lanes of even rows find their partner's value in
+// the second result and lanes of odd rows in the first.  v_permlane32_swap
+// does the same with the two 32-lane halves.
+__device__ __forceinline__ float xor16_f(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float xor32_f(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor_f(v, m));

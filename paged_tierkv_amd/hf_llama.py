@@ -291,8 +291,12 @@ class DecodeGraphRunner:
     layer.  The host bookkeeping a Python forward would do (step counter,
     block counts, cache length) is done by the runner around each replay.
 
-    * The first step runs eagerly (it sizes every workspace); the next two
-      are captured and replayed.  Policy steps run eagerly.
+    * The runtime's decode workspace is reserved here, at its largest size
+      (``max_blocks`` with score sums), before anything is captured: captured
+      launches and eager policy steps use that one buffer, which is never
+      replaced.
+    * The first step runs eagerly; the next two are captured and replayed.
+      Policy steps run eagerly.
     * Two graphs alternate, so the logits a step returns stay valid while
       the next step is replayed.
     * ``step`` returns the graph's static logits tensor: read it before the
@@ -306,6 +310,7 @@ class DecodeGraphRunner:
         self.model = model
         self.rt = runtime
         runtime.fixed_launch_bound = True
+        runtime.reserve_decode_workspace(model.config.num_attention_heads)
         self.ids = torch.zeros((runtime.batch, 1), dtype=torch.long, device=runtime.device)
         self.pos = torch.zeros((1, 1), dtype=torch.long, device=runtime.device)
         self.graphs: list = []

@@ -201,7 +201,9 @@ def prefill_block_mass(query_states: torch.Tensor, key_states: torch.Tensor, blo
         raise ValueError("key states do not match the query geometry.")
     kv_heads = int(k.shape[1])
     need = int(lib.tierkv_prefill_block_mass_workspace_bytes(batch, kv_heads, tokens))
-    key = (q.device.type, q.device.index)
+    # One scratch buffer per (device, stream): launches on one stream are
+    # ordered; launches on different streams may overlap and never share it.
+    key = (q.device.index, _lib.stream_of(q.device))
     ws = _prefill_ws.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.empty(max(need, 256), dtype=torch.uint8, device=q.device)

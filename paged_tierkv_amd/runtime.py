@@ -31,7 +31,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib, kernels
-from .tierkv_hip import tierkv_decode_attention
+from .tierkv_hip import DecodeWorkspace, tierkv_decode_attention
 
 HOT_STATE, WARM_STATE, COLD_STATE = 0, 1, 2
 _MODES = {"hot_warm": 1, "hot_warm_cold": 2}
@@ -188,6 +188,13 @@ class BatchedTieredKVRuntime:
         self.current_query_length = 0
         self.policy_tick_this_forward = False
         self.fixed_launch_bound = False
+        # The decode kernel's scratch: owned by the runtime, sized once for the
+        # largest launch (max_blocks, with score sums) and never replaced, so
+        # captured decode steps always replay on live memory.  Every launch of
+        # the runtime is ordered on the caller's stream, so one serves all
+        # layers.
+        self.decode_workspace: DecodeWorkspace | None = None
+        self._workspace_heads = 0
         # HF hooks: rotate q / k inside the decode append (fp16 models).
         self.fused_rope = True
         from .tierkv_policy import TieredKVCache
@@ -321,6 +328,20 @@ class BatchedTieredKVRuntime:
 
     # -- decode -------------------------------------------------------------
 
+    def reserve_decode_workspace(self, num_heads: int) -> DecodeWorkspace:
+        """Allocate (once) the fixed decode workspace for ``num_heads`` query
+        heads; call it before capturing decode steps."""
+        num_heads = int(num_heads)
+        ws = self.decode_workspace
+        if ws is None or self._workspace_heads != num_heads:
+            if ws is not None and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("the decode workspace cannot be replaced during HIP graph capture.")
+            ws = DecodeWorkspace.for_shape(self.device, self.batch, num_heads, self.kv_heads, self.max_blocks,
+                                           self.head_dim, block_size=self.block_size, return_scores=True)
+            self.decode_workspace = ws
+            self._workspace_heads = num_heads
+        return ws
+
     def _advance_blocks(self, layer: int, tokens: int) -> int:
         """Mirror of the device append's block accounting (every sequence of
         the batch appends the same count): returns the new block count."""
@@ -403,7 +424,8 @@ class BatchedTieredKVRuntime:
         out, sums = tierkv_decode_attention(
             query_states, st.table, st.states, st.lengths, st.hot_k, st.hot_v, st.warm_k, st.warm_v,
             st.k_scale, st.k_zero, st.v_scale, st.v_zero, bound, num_key_value_groups, scaling,
-            return_scores=policy_step, cold_mode=self.cold_mode, seq_num_blocks=st.nblocks)
+            return_scores=policy_step, cold_mode=self.cold_mode, seq_num_blocks=st.nblocks,
+            workspace=self.reserve_decode_workspace(query_states.shape[1]))
         if policy_step:
             self.last_score_sums = sums   # the probability sums the tick ranked (kept for inspection)
             self.tick_layer(layer, sums, num_blocks)

@@ -25,7 +25,15 @@ Additive, keyword-only extensions:
 * ``splits``: split-K factor (default: chosen from the launch size).  The
   reference's ``TIERKV_SPLIT_DECODE`` switch is not needed: the kernel always
   splits when it pays, and the result equals the single pass up to fp32
-  re-association.
+  re-association;
+* ``workspace``: a ``DecodeWorkspace`` the caller owns (a fixed one is
+  required under HIP graph capture); by default each (device, stream) pair
+  has its own implicit workspace, so launches on different streams never
+  share scratch memory.
+
+``score_sums`` are reproducible: the same inputs give the same bits on every
+launch (each block's statistics are staged on their own and reduced in a
+fixed order), so tier labels ranked from them do not change from run to run.
 
 Set ``TIERKV_CHECK_ERRORS=1`` to make every call synchronise and raise if
 the kernel skipped a block whose slot or state was out of range.
@@ -33,34 +41,118 @@ the kernel skipped a block whose slot or state was out of range.
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _lib
 
-_workspaces: dict = {}
+class DecodeWorkspace:
+    """Device scratch of ``tierkv_decode_attention``: the error word, the
+    split-arrival counters, the split partials and the per-block score stage.
+
+    The kernels leave the counters at zero after every launch, so one
+    workspace serves launches of any shape, and captured graphs can replay
+    them -- as long as the launches that share it run one after another (on
+    one stream, or otherwise ordered).
+
+    ``growable=False`` fixes the buffer for the workspace's lifetime: a call
+    that needs more raises instead of reallocating.  Captured graphs hold the
+    buffer's address, so a workspace used under capture must be fixed and
+    sized before the capture (``DecodeWorkspace.for_shape``).  A growable
+    workspace replaces its buffer when a call needs more bytes; the error
+    flags set in the old buffer are carried into the new one on the device
+    (no host sync), and the old buffer is released on the stream that used
+    it.  The reference caches one placeholder tensor per device the same way
+    (tierkv_triton.py:24-40).
+    """
+
+    def __init__(self, device, nbytes: int = 0, *, growable: bool = True):
+        self.device = torch.device(device)
+        self.growable = bool(growable)
+        self.buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
+        _LIVE.add(self)
+
+    @staticmethod
+    def bytes_for(batch: int, num_heads: int, kv_heads: int, num_blocks: int, head_dim: int, *,
+                  block_size: int = 16, return_scores: bool = True, splits: int = 0) -> int:
+        need = _lib.lib().tierkv_decode_workspace_bytes(int(batch), int(num_heads), int(kv_heads), int(num_blocks),
+                                                        int(block_size), int(head_dim), int(bool(return_scores)),
+                                                        int(splits))
+        if need < 0:
+            raise ValueError("invalid decode geometry.")
+        return int(need)
+
+    @classmethod
+    def for_shape(cls, device, batch: int, num_heads: int, kv_heads: int, num_blocks: int, head_dim: int, *,
+                  block_size: int = 16, return_scores: bool = True, splits: int = 0) -> "DecodeWorkspace":
+        """A fixed workspace large enough for every launch of this geometry
+        with at most ``num_blocks`` blocks (with or without score sums)."""
+        need = cls.bytes_for(batch, num_heads, kv_heads, num_blocks, head_dim, block_size=block_size,
+                             return_scores=return_scores, splits=splits)
+        return cls(device, need, growable=False)
+
+    @property
+    def nbytes(self) -> int:
+        return int(self.buf.numel())
+
+    def data_ptr(self) -> int:
+        return self.buf.data_ptr()
+
+    def reserve(self, nbytes: int) -> None:
+        if nbytes <= self.nbytes:
+            return
+        if not self.growable:
+            raise RuntimeError(f"decode workspace holds {self.nbytes} bytes, the launch needs {int(nbytes)}: "
+                               "size the fixed workspace for the largest launch (DecodeWorkspace.for_shape).")
+        if self.device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("the decode workspace cannot grow during HIP graph capture: pass workspace= "
+                               "(a DecodeWorkspace sized before the capture), or run the launch once eagerly "
+                               "on this stream first.")
+        new = torch.zeros(int(nbytes), dtype=torch.uint8, device=self.device)
+        new[:4].view(torch.int32).bitwise_or_(self.buf[:4].view(torch.int32))
+        self.buf = new
+
+    def error_word(self, clear: bool = True) -> int:
+        """The kernels' error flags (synchronises); cleared unless ``clear`` is False."""
+        word = int(self.buf[:4].view(torch.int32).item())
+        if word and clear:
+            self.buf[:4].zero_()
+        return word
 
 
-def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Cached per-device scratch (the reference caches its score placeholder
-    the same way, tierkv_triton.py:24-40).  Zero-filled once: its first word
-    is the kernels' error flag."""
-    key = (device.type, device.index)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
+_LIVE: "weakref.WeakSet[DecodeWorkspace]" = weakref.WeakSet()
+# Implicit workspaces, one per (device, stream): launches on one stream are
+# ordered, so they may share one; launches on different streams may overlap
+# and never share.
+_implicit: dict = {}
+
+
+def stream_workspace(device=None) -> DecodeWorkspace:
+    """The implicit workspace of torch's current stream on ``device``."""
+    device = torch.device(device if device is not None else "cuda")
+    if device.index is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    key = (device.index, _lib.stream_of(device))
+    ws = _implicit.get(key)
+    if ws is None:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("no decode workspace exists for the capturing stream: pass workspace= (a "
+                               "DecodeWorkspace sized before the capture).")
+        ws = DecodeWorkspace(device)
+        _implicit[key] = ws
     return ws
 
 
 def workspace_error_word(device) -> int:
-    """Read (and clear) the kernels' error flag for ``device`` (synchronises)."""
+    """Read (and clear) the kernels' error flags of every decode workspace on
+    ``device`` (synchronises)."""
     device = torch.device(device)
-    ws = _workspaces.get((device.type, device.index))
-    if ws is None:
-        return 0
-    word = int(ws[:4].view(torch.int32).item())
-    if word:
-        ws[:4].zero_()
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    word = 0
+    for ws in list(_LIVE):
+        if ws.device.type == device.type and (ws.device.index or 0) == idx:
+            word |= ws.error_word()
     return word
 
 
@@ -98,8 +190,70 @@ def tierkv_decode_attention(
     cold_mode: str = "zero_logit",
     seq_num_blocks=None,
     splits: int | None = None,
+    workspace: DecodeWorkspace | None = None,
 ):
     """Decode attention over a tiered paged KV cache (see module docstring)."""
+    lib = _lib.lib()  # RuntimeError if the HIP library is not built
+    args, out, score_sums, ws, batched, _ = _bind(
+        query_states, block_table, block_states, block_lengths, hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool,
+        k_scale, k_zero, v_scale, v_zero, num_blocks, num_key_value_groups, scaling, return_scores,
+        cold_mode=cold_mode, seq_num_blocks=seq_num_blocks, splits=splits, workspace=workspace)
+    _launch(lib, args, query_states.device, ws)
+    if score_sums is not None and not batched:
+        score_sums = score_sums[0]
+    return out, score_sums
+
+
+class PreparedDecode:
+    """One ``tierkv_decode_attention`` launch validated and bound once, for
+    loops that re-issue the same launch (a serving loop's layer step, a
+    benchmark): ``launch()`` costs one C call on torch's current stream.
+
+    The bound tensors must stay where they are; their contents may change
+    between launches (write the next step's query into ``query`` in place).
+    Every launch overwrites ``out`` (and ``score_sums``).  The launch owns a
+    fixed workspace unless ``workspace`` (fixed) is given.  Arguments are
+    those of ``tierkv_decode_attention``."""
+
+    def __init__(self, *args, **kwargs):
+        self._lib = _lib.lib()
+        (self._args, self.out, scores, self.workspace, batched, self._keep) = _bind(*args, prepared=True, **kwargs)
+        self.query = self._keep[0]   # the bound (contiguous) query tensor
+        self.score_sums = scores if (scores is None or batched) else scores[0]
+        self.device = self.out.device
+
+    def launch(self):
+        _launch(self._lib, self._args, self.device, self.workspace)
+        return self.out, self.score_sums
+
+
+def _bind(
+    query_states: torch.Tensor,
+    block_table: torch.Tensor,
+    block_states: torch.Tensor,
+    block_lengths: torch.Tensor,
+    hot_k_pool: torch.Tensor,
+    hot_v_pool: torch.Tensor,
+    warm_k_pool: torch.Tensor,
+    warm_v_pool: torch.Tensor,
+    k_scale: torch.Tensor,
+    k_zero: torch.Tensor | None,
+    v_scale: torch.Tensor,
+    v_zero: torch.Tensor | None,
+    num_blocks: int,
+    num_key_value_groups: int,
+    scaling: float,
+    return_scores: bool = False,
+    *,
+    cold_mode: str = "zero_logit",
+    seq_num_blocks=None,
+    splits: int | None = None,
+    workspace: DecodeWorkspace | None = None,
+    prepared: bool = False,
+):
+    """Validate one decode launch and bind its C-ABI arguments (all but the
+    stream).  ``prepared`` binds a fixed workspace the launch owns unless one
+    is given, so the bound pointers stay valid for every later launch."""
     lib = _lib.lib()  # RuntimeError if the HIP library is not built
     if query_states.ndim != 4:
         raise ValueError("query_states must have shape [batch, num_heads, query_len, head_dim].")
@@ -173,8 +327,18 @@ def tierkv_decode_attention(
                                              head_dim, int(return_scores), splits_hint)
     if need < 0:
         raise ValueError("invalid decode geometry.")
-    ws = _workspace(device, need)
-    rc = lib.tierkv_decode_attention(
+    if workspace is not None:
+        ws = workspace
+    elif prepared:
+        ws = DecodeWorkspace(device, need, growable=False)
+    else:
+        ws = stream_workspace(device)
+    if ws.device != device:
+        raise ValueError("the decode workspace lives on another device.")
+    ws.reserve(need)
+    if prepared and ws.growable:
+        raise ValueError("a prepared decode needs a fixed workspace (DecodeWorkspace(..., growable=False)).")
+    args = (
         _lib.ptr(query), _lib.DTYPE_BF16 if query.dtype == torch.bfloat16 else _lib.DTYPE_F16,
         _lib.ptr(out), _lib.ptr(score_sums),
         _lib.ptr(block_table), _lib.ptr(block_states), _lib.ptr(block_lengths), table_stride,
@@ -186,12 +350,19 @@ def tierkv_decode_attention(
         fmt, _COLD_MODES[cold_mode],
         batch, num_heads, kv_heads, block_size, head_dim,
         float(scaling), splits_hint,
-        _lib.ptr(ws), int(ws.numel()), _lib.stream_of(device))
+        ws.data_ptr(), ws.nbytes)
+    # The tensors whose addresses are bound stay referenced with the arguments.
+    keep = (query, out, score_sums, snb, block_table, block_states, block_lengths, hot_k_pool, hot_v_pool,
+            warm_k_pool, warm_v_pool, k_scale, k_zero, v_scale, v_zero, ws)
+    return args, out, score_sums, ws, batched, keep
+
+
+def _launch(lib, args, device, ws) -> None:
+    rc = lib.tierkv_decode_attention(*args, _lib.stream_of(device))
     _lib.check(rc, "tierkv_decode_attention")
     if _lib.env_flag("TIERKV_CHECK_ERRORS"):
-        word = workspace_error_word(device)
+        word = ws.error_word()
         if word:
             raise RuntimeError(f"TierKV decode skipped blocks with out-of-range slot/state (flag {word}).")
-    if score_sums is not None and not batched:
-        score_sums = score_sums[0]
-    return out, score_sums
+
+

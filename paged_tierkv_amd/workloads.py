@@ -278,3 +278,26 @@ def score_ideal_bytes(batch, heads, tokens, block_size):
 C2B_HOT_BUDGET = 26     # block 0 and 255 plus 24 by score
 C2B_COLD_COUNT = 77
 C2B_WARM_BUDGET = 256 - C2B_HOT_BUDGET - C2B_COLD_COUNT
+
+
+def llama3_8b_random(device, num_layers: int = 32):
+    """Random-init Llama-3-8B-shaped decoder:
+    32 layers, hidden 4096, 32 / 8 heads, head_dim 128, FFN 14336, vocab
+    128256, fp16 weights ~N(0, 0.02) (transformers' own init with
+    initializer_range 0.02), built directly on ``device``."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(hidden_size=4096, intermediate_size=14336, num_hidden_layers=num_layers,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, vocab_size=128256,
+                      max_position_embeddings=8192, rope_theta=500000.0, initializer_range=0.02,
+                      rms_norm_eps=1e-5, tie_word_embeddings=False)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(device):
+            model = LlamaForCausalLM(cfg).eval()
+    finally:
+        torch.set_default_dtype(prev)
+    return model

@@ -51,7 +51,20 @@ def to_gpu_inputs(case, warm, device, query_dtype=torch.float16):
         num_blocks=case.num_blocks, num_key_value_groups=case.groups, scaling=case.scaling)
 
 
+def error_stats(actual, expected, atol=ATOL, rtol=RTOL) -> dict:
+    """max |a - e|, max |a - e| / |e| over |e| >= atol, and the largest
+    fraction of the tolerance atol + rtol |e| any element uses (< 1 passes)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    err = np.abs(a - e)
+    big = np.abs(e) >= atol
+    return {"max_abs": float(err.max()) if err.size else 0.0,
+            "max_rel": float((err[big] / np.abs(e[big])).max()) if big.any() else 0.0,
+            "tol_used": float((err / (atol + rtol * np.abs(e))).max()) if err.size else 0.0}
+
+
 def assert_close(actual, expected, atol=ATOL, rtol=RTOL, what="output"):
+    """Elementwise |a - e| <= atol + rtol |e|; returns error_stats."""
     a = np.asarray(actual, dtype=np.float64)
     e = np.asarray(expected, dtype=np.float64)
     assert a.shape == e.shape, f"{what}: shape {a.shape} != {e.shape}"
@@ -60,3 +73,9 @@ def assert_close(actual, expected, atol=ATOL, rtol=RTOL, what="output"):
         idx = np.argwhere(bad)[:5].tolist()
         raise AssertionError(f"{what}: {int(bad.sum())} of {a.size} outside atol={atol} rtol={rtol}; "
                              f"max abs err {np.abs(a - e).max():.3e}; first bad {idx}")
+    return error_stats(a, e, atol, rtol)
+
+
+def report(what: str, stats: dict) -> None:
+    print(f"[parity] {what}: max_abs={stats['max_abs']:.3e} max_rel={stats['max_rel']:.3e} "
+          f"tol_used={stats['tol_used']:.3f} (atol {ATOL}, rtol {RTOL})", flush=True)

@@ -1,0 +1,120 @@
+"""BASELINE configs[4] (C5) end to end on the GPU, at its full shape.
+
+Random-init Llama-3-8B (32 layers, hidden 4096, 32 / 8 heads, head_dim 128,
+FFN 14336, vocab 128256, fp16), batch 16, a 2048-token uniform-random prompt,
+256 greedy decode steps through the HF hooks and the batched tiered runtime
+(HOT 15 % / WARM 55 % / rest COLD, policy every 64 steps, absmax WARM,
+masked COLD), decode steps replayed as HIP graphs with eager policy steps.
+The reference's counterparts are its decode-throughput loop (main.py:831-981)
+and its memory telemetry (tierkv_policy.py:1193-1317, 1985-2032).
+
+Checks:
+* no allocator error bits on any layer;
+* the runtime's decode workspace (the buffer every captured launch writes
+  its split partials, arrival counters and score stage into) is the same
+  buffer from the first step to the last, across all four policy ticks, and
+  the implicit per-stream workspaces are never touched;
+* per layer and sequence, the tier counts after the last tick follow the
+  budgets (HOT = max(2, round(0.15 n)), WARM <= round(0.55 n), the rest COLD);
+* on two layers after the last tick, the decode kernel over the runtime's
+  own pools and tables matches the oracle for two sequences (2e-3 abs /
+  1e-2 rel of the fp32 reference);
+* resident and physical KV bytes are reported and below the dense cache.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+pytest.importorskip("transformers")
+
+from oracle import decode as odecode  # noqa: E402
+from paged_tierkv_amd import hf_llama, tierkv_hip, workloads as W  # noqa: E402
+from paged_tierkv_amd.runtime import BatchedTieredKVRuntime  # noqa: E402
+
+from helpers import assert_close, report  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+B, PROMPT, STEPS, INTERVAL = 16, 2048, 256, 64
+
+
+def test_c5_full_shape_graph_decode(device):
+    print("[c5] building random-init Llama-3-8B", flush=True)
+    model = W.llama3_8b_random(device)
+    cfg = model.config
+    hf_llama.install()
+    tierkv_hip._implicit.clear()
+    try:
+        rt = BatchedTieredKVRuntime(cfg.num_hidden_layers, B, cfg.num_key_value_heads, cfg.head_dim,
+                                    PROMPT + STEPS + 16, hot_fraction=0.15, warm_fraction=0.55,
+                                    policy_mode="hot_warm_cold", policy_interval=INTERVAL, warm_format="absmax_i8",
+                                    cold_mode="masked", device=device)
+        prompt = torch.randint(0, cfg.vocab_size, (B, PROMPT), generator=torch.Generator().manual_seed(1)).to(device)
+        with torch.no_grad():
+            out = model(input_ids=prompt, past_key_values=rt.cache, use_cache=True, logits_to_keep=1)
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        print("[c5] prefill done; decoding", flush=True)
+        runner = hf_llama.DecodeGraphRunner(model, rt)
+        ws = rt.decode_workspace
+        ptr = ws.data_ptr()
+        ticks = 0
+        for s in range(STEPS):
+            logits = runner.step(tok)
+            tok = logits[:, -1].argmax(-1, keepdim=True)
+            if rt.decode_step % INTERVAL == 0:
+                ticks += 1
+            assert rt.decode_workspace is ws and ws.data_ptr() == ptr, f"workspace replaced at step {s}"
+        torch.cuda.synchronize()
+        print(f"[c5] {STEPS} steps, {ticks} ticks, {runner.replays} replays", flush=True)
+        assert ticks == STEPS // INTERVAL and runner.replays > STEPS // 2
+        assert not tierkv_hip._implicit, "an implicit workspace was created"
+        assert torch.isfinite(logits).all()
+        rt.check_errors()
+
+        # Tier counts against the budgets of the last tick (it ran at the last step).
+        for li, st in enumerate(rt.layers):
+            states = st.states.cpu()
+            nblocks = st.nblocks.cpu()
+            for b in range(B):
+                n = int(nblocks[b])
+                hot_b, warm_b = rt.budgets(n)
+                row = states[b, :n]
+                hot, warm = int((row == 0).sum()), int((row == 1).sum())
+                assert hot == hot_b and warm <= warm_b, (li, b, n, hot, warm, hot_b, warm_b)
+                assert int((row == 2).sum()) == n - hot - warm
+        m = rt.memory_metrics()
+        print(f"[c5] resident KV {m['resident_kv_bytes'] / 2**20:.1f} MiB, physical pools "
+              f"{m['physical_pool_bytes'] / 2**20:.1f} MiB, dense {m['dense_equivalent_bytes'] / 2**20:.1f} MiB; "
+              f"tiers {m['hot_blocks']}/{m['warm_blocks']}/{m['cold_blocks']}", flush=True)
+        assert m["resident_kv_bytes"] < m["physical_pool_bytes"] < m["dense_equivalent_bytes"]
+
+        # The kernel over the runtime's own pools after the last tick, against the oracle.
+        gen = torch.Generator().manual_seed(5)
+        H, D = cfg.num_attention_heads, cfg.head_dim
+        seqs = [0, B - 1]
+        for li in (0, cfg.num_hidden_layers - 1):
+            st = rt.layers[li]
+            q = torch.randn((B, H, 1, D), generator=gen).to(torch.float16)
+            n = int(st.nblocks[0].item())
+            o, sc = tierkv_hip.tierkv_decode_attention(
+                q.to(device), st.table, st.states, st.lengths, st.hot_k, st.hot_v, st.warm_k, st.warm_v,
+                st.k_scale, None, st.v_scale, None, rt.max_blocks, H // cfg.num_key_value_heads, D ** -0.5,
+                return_scores=True, cold_mode="masked", seq_num_blocks=st.nblocks, workspace=rt.decode_workspace)
+            torch.cuda.synchronize()
+            host = {k: getattr(st, k).cpu().numpy() for k in ("table", "states", "lengths", "hot_k", "hot_v",
+                                                             "warm_k", "warm_v", "k_scale", "v_scale")}
+            exp_out, exp_sc = odecode.decode_attention(
+                q[seqs, :, 0].numpy(), host["table"][seqs], host["states"][seqs], host["lengths"][seqs], n,
+                host["hot_k"], host["hot_v"], host["warm_k"], host["warm_v"], host["k_scale"], None,
+                host["v_scale"], None, H // cfg.num_key_value_heads, D ** -0.5, warm_format="absmax_i8",
+                cold_mode="masked", return_scores=True)
+            report(f"c5 layer {li} output", assert_close(o[seqs, 0].float().cpu().numpy(), exp_out,
+                                                         what=f"c5 layer {li} output"))
+            report(f"c5 layer {li} score_sums", assert_close(sc[seqs].cpu().numpy(), exp_sc,
+                                                             what=f"c5 layer {li} scores"))
+            np.testing.assert_array_equal(sc[seqs, :, n:].cpu().numpy(), 0.0)
+    finally:
+        hf_llama.uninstall()

@@ -13,7 +13,7 @@ import torch
 from paged_tierkv_amd import workloads as W
 from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention, workspace_error_word
 
-from helpers import assert_close, oracle_decode, oracle_warm, to_gpu_inputs
+from helpers import assert_close, oracle_decode, oracle_warm, report, to_gpu_inputs
 
 pytestmark = pytest.mark.gpu
 
@@ -35,12 +35,12 @@ def _check(case, fmt, device, cold_mode=None, return_scores=False, seqs=None, qu
     res = oracle_decode(case, warm, fmt, cold_mode, return_scores, seqs=seqs)
     exp_out, exp_sc = (res if return_scores else (res, None))
     got = out[seqs, 0].float().cpu().numpy()
-    assert_close(got, exp_out, what=f"{case.name} output")
+    report(f"{case.name} {fmt} output ({len(seqs)} seqs)", assert_close(got, exp_out, what=f"{case.name} output"))
     if return_scores:
         sc = scores.cpu().numpy()
         if sc.ndim == 2:
             sc = sc[None]
-        assert_close(sc[seqs], exp_sc, what=f"{case.name} score_sums")
+        report(f"{case.name} {fmt} score_sums", assert_close(sc[seqs], exp_sc, what=f"{case.name} score_sums"))
     assert workspace_error_word(device) == 0
     return out, scores
 
@@ -61,16 +61,72 @@ def test_c1_bf16_query(device):
     _check(case, "absmax_i8", device, query_dtype=torch.bfloat16)
 
 
-def test_c3_llama3_subset(device):
-    _check(W.config3(), "absmax_i8", device, seqs=[0, 13, 31])
+def test_c3_llama3_full(device):
+    # Every one of the 32 sequences against the oracle.
+    _check(W.config3(), "absmax_i8", device)
 
 
-def test_c3_scores_subset(device):
-    _check(W.config3(batch=4), "absmax_i8", device, return_scores=True)
+def test_c3_scores_full(device):
+    _check(W.config3(), "absmax_i8", device, return_scores=True)
 
 
-def test_c4_long_context_subset(device):
-    _check(W.config4(), "absmax_i8", device, seqs=[0, 3])
+def test_c3_reference_format_zero_logit(device):
+    # The drop-in's default WARM format (uint8 per-token codes) and COLD
+    # semantics (zero logit) at C3's full size.
+    _check(W.config3(), "ref_u8", device, cold_mode="zero_logit", return_scores=True)
+
+
+def test_c4_long_context_full(device):
+    _check(W.config4(), "absmax_i8", device, return_scores=True)
+
+
+def test_scores_reproducible(device):
+    """Score sums (and the labels ranked from them) are the same bits on every
+    launch over the same inputs, whatever the split count or the order in
+    which waves met the tiles; the reference's score pass is a fixed
+    sequential loop (tierkv_triton.py:121-145)."""
+    from paged_tierkv_amd import kernels
+
+    case = W.config3()
+    warm = oracle_warm(case, "absmax_i8")
+    args = to_gpu_inputs(case, warm, device)
+    runs = []
+    for splits in (None, None, 2, 3, None):
+        _, sc = tierkv_decode_attention(**args, return_scores=True, cold_mode="masked", splits=splits)
+        scores = kernels.block_scores_from_sums(sc, args["block_lengths"], case.num_blocks)
+        labels = kernels.tier_labels(scores, args["block_states"], 26, 154, mode="hot_warm_cold")
+        torch.cuda.synchronize()
+        runs.append((sc.cpu(), labels.cpu()))
+    for sc, lab in runs[1:]:
+        assert torch.equal(sc.view(torch.int32), runs[0][0].view(torch.int32))
+        assert torch.equal(lab, runs[0][1])
+
+
+def test_two_streams_concurrent(device):
+    """Decodes of different shapes in flight on two streams at once: each
+    stream has its own implicit workspace (split partials, arrival counters,
+    score stage), so neither disturbs the other."""
+    a = W.make_tiered_case("stream_a", 4, 32, 8, 128, 300, 30, 170, seed=61)
+    b = W.make_tiered_case("stream_b", 3, 16, 4, 64, 200, 20, 120, seed=62)
+    wa, wb = oracle_warm(a, "absmax_i8"), oracle_warm(b, "ref_u8")
+    ia, ib = to_gpu_inputs(a, wa, device), to_gpu_inputs(b, wb, device)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(device), torch.cuda.Stream(device)
+    outs_a, outs_b = [], []
+    for _ in range(12):
+        with torch.cuda.stream(sa):
+            outs_a.append(tierkv_decode_attention(**ia, return_scores=True, cold_mode="masked", splits=4))
+        with torch.cuda.stream(sb):
+            outs_b.append(tierkv_decode_attention(**ib, return_scores=True, cold_mode="zero_logit", splits=3))
+    torch.cuda.synchronize()
+    ea, esa = oracle_decode(a, wa, "absmax_i8", "masked", True)
+    eb, esb = oracle_decode(b, wb, "ref_u8", "zero_logit", True)
+    for (oa, sca), (ob, scb) in zip(outs_a, outs_b):
+        assert_close(oa[:, 0].float().cpu().numpy(), ea, what="stream a output")
+        assert_close(sca.cpu().numpy(), esa, what="stream a scores")
+        assert_close(ob[:, 0].float().cpu().numpy(), eb, what="stream b output")
+        assert_close(scb.cpu().numpy(), esb, what="stream b scores")
+    assert workspace_error_word(device) == 0
 
 
 # -- shapes, formats and modes ------------------------------------------------
@@ -129,6 +185,16 @@ def test_long_row_list_build(device, groups):
                               recent_hot=4)
     _check(case, "absmax_i8", device, return_scores=True)
     _check(case, "ref_u8", device, cold_mode="zero_logit", return_scores=True)
+
+
+@pytest.mark.parametrize("fmt", ["absmax_i8", "ref_u8"])
+def test_split_list_capacity(device, fmt):
+    # 1 HOT + 1023 WARM blocks asked to run in 2 splits: split 0 would get
+    # ceil(1/2) + ceil(1023/2) = 513 list entries, one more than the LDS list
+    # holds; the plan raises the split count so that HOT (front) and WARM
+    # (back) entries never meet.
+    case = W.make_tiered_case("list_cap", 1, 4, 1, 64, 1024, 1, 1023, seed=71)
+    _check(case, fmt, device, cold_mode="zero_logit", return_scores=True, splits=2)
 
 
 def test_split_launch_in_sequence_chunks(device):
