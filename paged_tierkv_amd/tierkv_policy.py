@@ -1,34 +1,43 @@
 """Tier engine on MI355X -- drop-in for the reference module tierkv_policy.
 
-Same public names, constructor arguments, return values and exceptions as
-tierkv_policy.py: the codec pair (21-44), the dense ``TieredKVTensorPool``
-(53-698, alias ``PhysicalKVPool``), ``CompactTieredKVTensorPool`` (701-1365),
-``TierKVPolicyEngine`` (1372-1478), ``LayerRuntimeState`` (1481-1484), the
-HF ``TieredKVCache`` (1487-1531), ``TieredKVRuntime`` (1534-1912) and the
-module functions (1915-2044).  Host bookkeeping follows the reference rule
-for rule -- BlockManager calls, LIFO free-slot lists refilled
-``range(new - 1, old - 1, -1)``, slot and state transitions, error types and
-messages -- so slot ids, tables and pool bytes come out identical.
+Public names, constructor arguments, return values, environment variables and
+exceptions follow tierkv_policy.py: the codec pair (21-44), the dense
+``TieredKVTensorPool`` (53-698, alias ``PhysicalKVPool``),
+``CompactTieredKVTensorPool`` (701-1365), ``TierKVPolicyEngine``
+(1372-1478), ``LayerRuntimeState`` (1481-1484), the HF ``TieredKVCache``
+(1487-1531), ``TieredKVRuntime`` (1534-1912) and the module functions
+(1915-2044).  The behaviour the reference's callers and tests observe is kept
+exactly -- BlockManager calls, slot ids (LIFO free stacks refilled lowest slot
+first), table contents, pool bytes including stale tails, error types and
+messages -- and is checked against trajectories the reference itself recorded.
 
-What differs is how the device work is issued:
+How it is organised here:
 
-* every data movement runs in the HIP kernels of libtierkv_hip.so (token
-  copies with tail zeroing, reference-codec quantize and dequantize); the
-  module never falls back to PyTorch arithmetic, and a missing library raises
-  RuntimeError;
-* pool operations queue their copies and launch them in batches: a whole
-  prefill is one copy launch plus one quantize launch, a whole
-  ``sync_storage_states`` one demote and one promote launch, where the
-  reference issues about 20 launches per block.  Queued jobs never overlap on
-  a slot (a job that would read or write a slot a queued job writes, or write
-  a slot a queued job reads, first launches the queue), so batching preserves
-  the reference's sequential order;
-* the block tables keep a host copy; entry writes are queued and pushed with
-  one scatter launch when a table is next read (``get_layer_table``,
-  ``get_layer_lengths`` or the table attributes), instead of one launch per
-  entry; host-side reads (lengths, metrics) use the host copy, so
-  ``collect_memory_metrics`` does not synchronise;
-* the policy's ranking runs in the label kernel (one device-to-host copy per
+* Host half.  Each pool keeps a ledger of ``_Block`` records (tier, slot,
+  tokens) and table locations; the reference's per-block dictionaries and
+  storage sets are read-only views of it.  Slot storage of every tier is a
+  ``_SlotArena`` (LIFO stack for the compact tiers, index coverage for the
+  dense pool).  Tier changes are table-driven: ``_TRANSITION_RULES`` gives
+  each transition's no-op state and errors, each layout supplies
+  ``_present`` / ``_apply``, and ``_RETIER`` maps (assigned, held) state
+  pairs to the transition ``sync_storage_states`` needs.  Runtime settings
+  come from the ``_SETTINGS`` table of argument/environment precedence.
+* Device half.  Every data movement runs in the HIP kernels of
+  libtierkv_hip.so (token copies with tail zeroing, the reference codec's
+  quantize and dequantize); there is no PyTorch fallback, and a missing
+  library raises RuntimeError.  Pool operations queue their copies and launch
+  them in batches: a whole prefill is one copy launch plus one quantize
+  launch, a whole ``sync_storage_states`` one demote and one promote launch,
+  where the reference issues about 20 launches per block.  Queued jobs never
+  overlap on a slot (a job that would read or write a slot a queued job
+  writes, or write a slot a queued job reads, first launches the queue), so
+  batching keeps the sequential semantics.
+* Tables keep a host copy; entry writes are queued and pushed with one
+  scatter launch when a table is next read (``get_layer_table``,
+  ``get_layer_lengths`` or the table attributes).  Host-side reads (lengths,
+  metrics) use the host copy, so ``collect_memory_metrics`` does not
+  synchronise.
+* The policy's ranking runs in the label kernel (one device-to-host copy per
   enforce call instead of one per candidate, tierkv_policy.py:1424, 1462).
 
 Extension (keyword-only): ``warm_format="absmax_i8"`` stores WARM blocks as
@@ -504,57 +513,404 @@ class _QueuedStorage:
             return 0.0
         return tensor.numel() * tensor.element_size() / (1024 ** 2)
 
-    def _warm_token_meta_bytes(self) -> int:
-        return int(self.kv_heads) * 4 * 2
-
-
-def _zero_metrics() -> dict:
-    return {
-        "hot_blocks": 0, "warm_blocks": 0, "cold_blocks": 0,
-        "hot_tokens": 0, "warm_tokens": 0, "cold_tokens": 0, "active_tokens": 0,
-        "logical_hot_mb": 0.0, "logical_warm_mb": 0.0, "logical_warm_meta_mb": 0.0,
-        "logical_cold_evicted_mb": 0.0, "logical_dense_equivalent_mb": 0.0, "logical_resident_mb": 0.0,
-        "logical_compression_ratio": 0.0, "logical_compression_x": 0.0,
-    }
-
-
-def _logical_metrics(kv_heads, head_dim, hot_tokens, warm_tokens, cold_tokens, meta_bytes_per_token):
-    """Byte accounting of collect_memory_metrics (tierkv_policy.py:586-609,
-    1263-1276): fp16 K+V per HOT/COLD token, int8 K+V per WARM token plus
-    the per-token metadata."""
-    dense_tok = kv_heads * head_dim * 2 * 2
-    int8_tok = kv_heads * head_dim * 2
-    active = hot_tokens + warm_tokens + cold_tokens
-    hot_b = hot_tokens * dense_tok
-    warm_b = warm_tokens * int8_tok
-    meta_b = warm_tokens * meta_bytes_per_token
-    cold_b = cold_tokens * dense_tok
-    dense_b = active * dense_tok
-    resident_b = hot_b + warm_b + meta_b
-    mb = 1024 ** 2
-    return {
-        "active_tokens": active,
-        "logical_hot_mb": hot_b / mb,
-        "logical_warm_mb": warm_b / mb,
-        "logical_warm_meta_mb": meta_b / mb,
-        "logical_cold_evicted_mb": cold_b / mb,
-        "logical_dense_equivalent_mb": dense_b / mb,
-        "logical_resident_mb": resident_b / mb,
-        "_dense_b": dense_b,
-        "_resident_b": resident_b,
-    }
 
 
 # ---------------------------------------------------------------------------
-# Dense pool (tierkv_policy.py:53-698): one storage row per physical block in
-# every pool; tables hold the physical id.
+# Host half: what each pool knows about its blocks, where their bytes live,
+# and the rules that move a block between tiers.
 # ---------------------------------------------------------------------------
 
-class TieredKVTensorPool(_QueuedStorage):
-    _demote_pads_tail = True       # dense demote_to_warm zero-pads (350-356)
-    _stage_pads_tail = False       # dense write_warm_block copies [:length] only (292-312)
+@dataclass
+class _Block:
+    """One stored physical block: its tier, its slot in that tier's storage
+    (the compact layout; the dense layout addresses storage by physical id)
+    and the tokens it holds."""
+    state: int
+    slot: int = -1
+    length: int = 0
 
-    _T_TABLE, _T_STATE, _T_LEN = 0, 1, 2
+
+class _SlotArena:
+    """Storage rows of one tier, allocated in chunks up to ``limit``.
+
+    Two ways to hand out rows, one per pool layout:
+
+    * ``take`` / ``give`` -- a LIFO stack of free rows (compact tiers).  A
+      growth pushes the new rows highest first, so the next ``take`` returns
+      the lowest of them; a released row is the next one taken.  Slot ids
+      therefore follow tierkv_policy.py:849-915 exactly.
+    * ``cover`` -- rows are physical ids; the arena grows to the chunk
+      boundary above the requested id (dense pool, tierkv_policy.py:137-185).
+
+    ``on_grow(old, new)`` reallocates the tier's tensors."""
+
+    def __init__(self, limit: int, chunk: int, on_grow, exhausted: str):
+        self.limit = int(limit)
+        self.chunk = int(chunk)
+        self.on_grow = on_grow
+        self.exhausted = exhausted
+        self.capacity = 0
+        self.free: list[int] = []
+
+    def _extend_to(self, new: int) -> None:
+        old = self.capacity
+        self.on_grow(old, new)
+        self.capacity = new
+        return old
+
+    def take(self) -> int:
+        if not self.free:
+            if self.capacity >= self.limit:
+                raise RuntimeError(self.exhausted)
+            new = min(self.limit, self.capacity + max(1, self.chunk))
+            old = self._extend_to(new)
+            self.free.extend(range(new - 1, old - 1, -1))
+        return int(self.free.pop())
+
+    def give(self, slot: int) -> None:
+        if int(slot) >= 0:
+            self.free.append(int(slot))
+
+    def cover(self, index: int) -> None:
+        if index < self.capacity:
+            return
+        new = min(self.limit, _ceil_div(index + 1, self.chunk) * self.chunk)
+        if new > self.capacity:
+            self._extend_to(new)
+
+    def all_free(self) -> None:
+        self.free = list(range(self.capacity - 1, -1, -1))
+
+    def drop(self) -> None:
+        self.capacity = 0
+        self.free = []
+
+
+# Tier transitions of a stored block (tierkv_policy.py:329-402, 1042-1115):
+# the state in which the call does nothing, the error when the block is
+# COLD, the error when the source tier does not hold it.
+_TRANSITION_RULES = {
+    "demote_to_warm": (WARM_STATE, "is not eligible for WARM demotion from COLD storage",
+                       "is not present in HOT storage"),
+    "promote_to_hot": (HOT_STATE, "is not eligible for HOT promotion from COLD storage",
+                       "is not present in WARM storage"),
+    "demote_to_cold": (COLD_STATE, None, "is not present in HOT or WARM storage"),
+}
+
+# sync_storage_states (tierkv_policy.py:1849-1867): for the state the
+# BlockManager now holds and the state the pool holds, the pool call to make
+# or the error to raise; pairs not listed need no data movement.
+_RETIER = {
+    (HOT_STATE, WARM_STATE): "promote_to_hot",
+    (HOT_STATE, COLD_STATE): "cannot be promoted from COLD to HOT",
+    (WARM_STATE, HOT_STATE): "demote_to_warm",
+    (WARM_STATE, COLD_STATE): "cannot be promoted from COLD to WARM",
+    (COLD_STATE, HOT_STATE): "demote_to_cold",
+    (COLD_STATE, WARM_STATE): "demote_to_cold",
+    (COLD_STATE, None): "demote_to_cold",
+}
+
+
+class _PoolBase(_QueuedStorage):
+    """What the dense and compact pools share: geometry, the block ledger
+    (``_blocks``: stored blocks; ``_where``: table entry of each physical id),
+    the tier transitions and the metric arithmetic.  Layout-specific parts:
+    ``_present`` / ``_apply`` (transitions), the write paths, the tables."""
+
+    _table_fills: tuple = ()
+    _capacity_word = "tensor-pool"
+
+    def __init__(self, num_layers, block_size, max_seq_len, max_blocks_per_layer, pool_blocks, pool_chunk_blocks,
+                 warm_format):
+        for name, value in (("num_layers", num_layers), ("block_size", block_size), ("max_seq_len", max_seq_len)):
+            if value <= 0:
+                raise ValueError(f"{name} must be positive.")
+        self.num_layers = int(num_layers)
+        self.block_size = int(block_size)
+        self.max_seq_len = int(max_seq_len)
+        self.max_blocks_per_layer = int(max_blocks_per_layer or _ceil_div(max_seq_len, block_size))
+        self.pool_blocks = int(pool_blocks or self.num_layers * self.max_blocks_per_layer)
+        self.pool_chunk_blocks = int(pool_chunk_blocks)
+        self.warm_format = self._check_format(warm_format)
+        self.device = None
+        self.dtype = torch.float16
+        self.kv_heads = None
+        self.head_dim = None
+        self.full_table_sync_count = 0
+        self._tables: _Tables | None = None
+        self._blocks: dict[int, _Block] = {}
+        self._where: dict[int, tuple[int, int]] = {}
+        for name in _POOL_TENSORS:
+            setattr(self, name, None)
+        self._init_queue()
+
+    # -- the reference's per-block dictionaries and sets, as views ----------
+    @property
+    def physical_states(self) -> dict:
+        return {p: b.state for p, b in self._blocks.items()}
+
+    @property
+    def physical_locations(self) -> dict:
+        return dict(self._where)
+
+    def _in_tier(self, state: int) -> set:
+        return {p for p, b in self._blocks.items() if b.state == state}
+
+    @property
+    def hot_storage(self) -> set:
+        return self._in_tier(HOT_STATE)
+
+    @property
+    def warm_storage(self) -> set:
+        return self._in_tier(WARM_STATE)
+
+    @property
+    def cold_storage(self) -> set:
+        return self._in_tier(COLD_STATE)
+
+    def get_physical_state(self, physical_idx: int) -> int | None:
+        b = self._blocks.get(int(physical_idx))
+        return None if b is None else b.state
+
+    def _check_physical_idx(self, physical_idx: int) -> int:
+        physical_idx = int(physical_idx)
+        if not 0 <= physical_idx < self.pool_blocks:
+            raise RuntimeError(f"Physical block {physical_idx} is outside {self._capacity_word} capacity "
+                               f"{self.pool_blocks}.")
+        return physical_idx
+
+    def _check_entry(self, layer_idx: int, logical_idx: int) -> None:
+        if not 0 <= layer_idx < self.num_layers:
+            raise ValueError("layer_idx is out of range.")
+        if not 0 <= logical_idx < self.max_blocks_per_layer:
+            raise RuntimeError(
+                f"Logical block {logical_idx} exceeds max_blocks_per_layer={self.max_blocks_per_layer}.")
+
+    def _require_allocated(self) -> None:
+        if not self.is_allocated():
+            raise RuntimeError(f"{type(self).__name__} has not been allocated yet.")
+
+    def _adopt_geometry(self, key_states: torch.Tensor) -> bool:
+        """Take the device / kv_heads / head_dim of the first stored tensor;
+        returns whether this call allocated the tables."""
+        geometry = (key_states.device, int(key_states.shape[1]), int(key_states.shape[-1]))
+        if self._tables is not None:
+            if geometry != (self.device, self.kv_heads, self.head_dim):
+                raise ValueError("KV tensor geometry changed after tensor-pool allocation.")
+            return False
+        self.device, self.kv_heads, self.head_dim = geometry
+        self._tables = _Tables(self._table_fills, self.num_layers, self.max_blocks_per_layer, self.device)
+        return True
+
+    # -- tier transitions ---------------------------------------------------
+    def _transition(self, op: str, physical_idx) -> None:
+        p = self._check_physical_idx(physical_idx)
+        state = self.get_physical_state(p)
+        idle, cold_error, missing_error = _TRANSITION_RULES[op]
+        if state == idle:
+            return
+        if cold_error is not None and state == COLD_STATE:
+            raise KeyError(f"Physical block {p} {cold_error}.")
+        if not self._present(op, p, state):
+            raise KeyError(f"Physical block {p} {missing_error}.")
+        self._apply(op, p, state)
+
+    def demote_to_warm(self, physical_idx) -> None:
+        self._transition("demote_to_warm", physical_idx)
+
+    def promote_to_hot(self, physical_idx) -> None:
+        self._transition("promote_to_hot", physical_idx)
+
+    def demote_to_cold(self, physical_idx) -> None:
+        self._transition("demote_to_cold", physical_idx)
+
+    def retier(self, physical_idx: int, desired: int) -> None:
+        """Bring the pool's copy of a block to the tier the BlockManager
+        assigned it (one step of sync_storage_states)."""
+        step = _RETIER.get((int(desired), self.get_physical_state(physical_idx)))
+        if step is None:
+            return
+        if step in _TRANSITION_RULES:
+            self._transition(step, physical_idx)
+        else:
+            raise KeyError(f"Physical block {physical_idx} {step}.")
+
+    def store_hot_block(self, physical_idx, k_tensor, v_tensor) -> None:
+        self.write_hot_tokens(int(physical_idx), 0, k_tensor, v_tensor)
+
+    def write_hot_tokens(self, physical_idx: int, start: int, key_states: torch.Tensor,
+                         value_states: torch.Tensor) -> None:
+        p = self._check_physical_idx(physical_idx)
+        key_states, value_states = self._coerce_kv(key_states, value_states)
+        with self._batch():
+            self._write_hot_range(p, start, key_states, value_states, 0, key_states.shape[-2])
+
+    def write_warm_block(self, physical_idx, k_tensor, v_tensor) -> None:
+        p = self._check_physical_idx(physical_idx)
+        k_tensor, v_tensor = self._coerce_kv(k_tensor, v_tensor)
+        with self._batch():
+            self._write_warm_range(p, k_tensor, v_tensor, 0, k_tensor.shape[-2])
+
+    def _check_range(self, start: int, tokens: int) -> None:
+        if start < 0 or start + tokens > self.block_size:
+            raise ValueError("KV write exceeds the physical block capacity.")
+
+    # -- reads --------------------------------------------------------------
+    def _hot_rows(self, row: int, length: int):
+        self._launch_queue()
+        return (self.hot_k_pool[row: row + 1, :, :length, :].contiguous(),
+                self.hot_v_pool[row: row + 1, :, :length, :].contiguous())
+
+    def get_dequantized_block(self, physical_idx, state):
+        """fp16 K, V of one block as its table state says it is stored
+        (tierkv_policy.py:404-448, 1117-1162): a block asked for as HOT but
+        held WARM is promoted first; a COLD block reads as zeros."""
+        p = self._check_physical_idx(physical_idx)
+        if not self.is_allocated():
+            raise KeyError(f"Physical block {p} is not present in {self._storage_word} storage.")
+        length = self.get_block_length(p)
+        held = self.get_physical_state(p)
+        if state == COLD_STATE:
+            shape = (1, self.kv_heads, length, self.head_dim)
+            return (torch.zeros(shape, device=self.device, dtype=torch.float16),
+                    torch.zeros(shape, device=self.device, dtype=torch.float16))
+        if state not in (HOT_STATE, WARM_STATE):
+            raise ValueError(f"Unsupported block state: {state}")
+        if held == COLD_STATE:
+            raise KeyError(f"Physical block {p} is marked {'HOT' if state == HOT_STATE else 'WARM'} but only "
+                           "exists in COLD storage.")
+        if state == HOT_STATE:
+            if held == WARM_STATE:
+                self.promote_to_hot(p)
+            return self._hot_rows(self._row_of(p), length)
+        if held == HOT_STATE:
+            return self._hot_rows(self._row_of(p), length)
+        self._launch_queue()
+        return self._dequantize_slot(self._row_of(p), length)
+
+    def get_layer_table(self, layer_idx: int):
+        self._require_allocated()
+        self._before_decode()
+        return self._tables.view(self._t_table)[int(layer_idx)], self._tables.view(self._t_state)[int(layer_idx)]
+
+    def get_layer_lengths(self, layer_idx: int):
+        self._require_allocated()
+        return self._tables.view(self._t_len)[int(layer_idx)]
+
+    def _before_decode(self) -> None:
+        pass
+
+    def set_block_state(self, layer_idx: int, logical_idx: int, state: int) -> None:
+        self._require_allocated()
+        self._tables.set(self._t_state, layer_idx, logical_idx, int(state))
+
+    # -- telemetry ----------------------------------------------------------
+    def _tensor_bytes_mb(self, names) -> float:
+        return sum(self._tensor_mb(getattr(self, n)) for n in names)
+
+    def _physical_mb(self) -> tuple[float, float, float]:
+        return (self._tensor_bytes_mb(("hot_k_pool", "hot_v_pool")),
+                self._tensor_bytes_mb(("warm_k_pool", "warm_v_pool")),
+                self._tensor_bytes_mb(("k_scale", "k_zero", "v_scale", "v_zero")))
+
+    def _tier_counts(self, layer_states: dict):
+        """Blocks and tokens per tier over the layers' active blocks, from the
+        host copies of the tables; and the active-block figure the layout
+        reports."""
+        blocks = dict.fromkeys((HOT_STATE, WARM_STATE, COLD_STATE), 0)
+        tokens = dict.fromkeys((HOT_STATE, WARM_STATE, COLD_STATE), 0)
+        active = 0
+        for layer_idx in range(self.num_layers):
+            ls = layer_states.get(layer_idx)
+            n = int(ls.num_blocks) if ls is not None else 0
+            if n <= 0:
+                continue
+            rows = self._active_rows(layer_idx, n)
+            if rows is None:
+                continue
+            states, lengths = rows
+            for s in blocks:
+                mask = states == s
+                blocks[s] += int(mask.sum())
+                tokens[s] += int(lengths[mask].sum())
+            active += len(states)
+        return blocks, tokens, active
+
+    def collect_memory_metrics(self, layer_states: dict) -> dict:
+        """tierkv_policy.py:489-654 / 1193-1317 from the host copies of the
+        tables (no device synchronisation)."""
+        hot_mb, warm_mb, meta_mb = self._physical_mb()
+        out = dict.fromkeys(_TOKEN_KEYS, 0)
+        out.update(dict.fromkeys(_MB_KEYS, 0.0))
+        out.update(self._capacity_metrics(hot_mb, warm_mb, meta_mb))
+        if not self.is_allocated() or self.kv_heads is None or self.head_dim is None:
+            return out
+        blocks, tokens, active = self._tier_counts(layer_states)
+        per_dense = int(self.kv_heads) * int(self.head_dim) * 2 * 2
+        per_int8 = int(self.kv_heads) * int(self.head_dim) * 2
+        per_meta = int(self.kv_heads) * 4 * 2
+        total_tokens = sum(tokens.values())
+        mb = float(1024 ** 2)
+        hot_b = tokens[HOT_STATE] * per_dense
+        warm_b = tokens[WARM_STATE] * per_int8
+        meta_b = tokens[WARM_STATE] * per_meta
+        dense_b = total_tokens * per_dense
+        resident_b = hot_b + warm_b + meta_b
+        out.update({
+            "hot_blocks": blocks[HOT_STATE], "warm_blocks": blocks[WARM_STATE], "cold_blocks": blocks[COLD_STATE],
+            "hot_tokens": tokens[HOT_STATE], "warm_tokens": tokens[WARM_STATE], "cold_tokens": tokens[COLD_STATE],
+            "active_tokens": total_tokens,
+            "logical_hot_mb": hot_b / mb, "logical_warm_mb": warm_b / mb, "logical_warm_meta_mb": meta_b / mb,
+            "logical_cold_evicted_mb": tokens[COLD_STATE] * per_dense / mb,
+            "logical_dense_equivalent_mb": dense_b / mb, "logical_resident_mb": resident_b / mb,
+        })
+        out.update(self._usage_metrics(blocks, active, dense_b, resident_b, hot_mb + warm_mb + meta_mb))
+        return out
+
+    # -- lifecycle ------------------------------------------------------------
+    def _forget_blocks(self) -> None:
+        self._blocks.clear()
+        self._where.clear()
+        self.full_table_sync_count = 0
+
+    def clear(self) -> None:
+        """Forget every block; tensors and capacity stay (tierkv_policy.py:662-674, 1319-1334)."""
+        self._launch_queue()
+        if self.is_allocated():
+            self._tables.reset()
+        self._forget_blocks()
+        self._reset_rows()
+
+    def release(self) -> None:
+        """Drop every tensor and forget every block."""
+        self._launch_queue()
+        for name in _POOL_TENSORS:
+            setattr(self, name, None)
+        self._tables = None
+        self.device = self.kv_heads = self.head_dim = None
+        self._forget_blocks()
+        self._drop_rows()
+
+
+_POOL_TENSORS = ("hot_k_pool", "hot_v_pool", "warm_k_pool", "warm_v_pool", "k_scale", "k_zero", "v_scale", "v_zero")
+_TOKEN_KEYS = ("hot_blocks", "warm_blocks", "cold_blocks", "hot_tokens", "warm_tokens", "cold_tokens",
+               "active_tokens")
+_MB_KEYS = ("logical_hot_mb", "logical_warm_mb", "logical_warm_meta_mb", "logical_cold_evicted_mb",
+            "logical_dense_equivalent_mb", "logical_resident_mb", "logical_compression_ratio",
+            "logical_compression_x")
+
+
+# ---------------------------------------------------------------------------
+# Dense layout (tierkv_policy.py:53-698): a block's physical id is its row
+# in every tier's tensors; the table holds the physical id.
+# ---------------------------------------------------------------------------
+
+class TieredKVTensorPool(_PoolBase):
+    _demote_pads_tail = True       # demote_to_warm zero-pads the tail (350-356)
+    _stage_pads_tail = False       # write_warm_block copies [:length] only (292-312)
+    _table_fills = (-1, COLD_STATE, 0)
+    _t_table, _t_state, _t_len = 0, 1, 2
+    _storage_word = "tensor-pool"
 
     def __init__(
         self,
@@ -567,428 +923,202 @@ class TieredKVTensorPool(_QueuedStorage):
         *,
         warm_format: str = "ref_u8",
     ):
-        if num_layers <= 0:
-            raise ValueError("num_layers must be positive.")
-        if block_size <= 0:
-            raise ValueError("block_size must be positive.")
-        if max_seq_len <= 0:
-            raise ValueError("max_seq_len must be positive.")
-
-        self.num_layers = int(num_layers)
-        self.block_size = int(block_size)
-        self.max_seq_len = int(max_seq_len)
-        self.max_blocks_per_layer = int(max_blocks_per_layer or _ceil_div(max_seq_len, block_size))
-        self.pool_blocks = int(pool_blocks or self.num_layers * self.max_blocks_per_layer)
-        self.pool_chunk_blocks = int(pool_chunk_blocks)
+        super().__init__(num_layers, block_size, max_seq_len, max_blocks_per_layer, pool_blocks, pool_chunk_blocks,
+                         warm_format)
         if self.pool_chunk_blocks <= 0:
             raise ValueError("pool_chunk_blocks must be positive.")
-        self.warm_format = self._check_format(warm_format)
+        self._rows = _SlotArena(self.pool_blocks, self.pool_chunk_blocks, self._grow_rows, "")
+        self._lengths: _Vector | None = None        # tokens per physical id
 
-        self.device = None
-        self.dtype = torch.float16
-        self.kv_heads = None
-        self.head_dim = None
-        self.allocated_pool_blocks = 0
+    # Table views (queued entries are pushed first).
+    @property
+    def block_tables(self):
+        return None if self._tables is None else self._tables.view(self._t_table)
 
-        self.hot_k_pool = None
-        self.hot_v_pool = None
-        self.warm_k_pool = None
-        self.warm_v_pool = None
-        self.k_scale = None
-        self.k_zero = None
-        self.v_scale = None
-        self.v_zero = None
-        self._lengths: _Vector | None = None        # per physical block (block_lengths)
-        self._tables: _Tables | None = None         # block_tables, block_states, logical_block_lengths
-        self.full_table_sync_count = 0
+    @property
+    def block_states(self):
+        return None if self._tables is None else self._tables.view(self._t_state)
 
-        self.physical_states: dict[int, int] = {}
-        self.physical_locations: dict[int, tuple[int, int]] = {}
-        self.hot_storage = set()
-        self.warm_storage = set()
-        self.cold_storage = set()
-        self._init_queue()
+    @property
+    def logical_block_lengths(self):
+        return None if self._tables is None else self._tables.view(self._t_len)
 
-    # Device views of the tables (queued entries pushed first).
     @property
     def block_lengths(self):
         return None if self._lengths is None else self._lengths.tensor()
 
     @property
-    def block_tables(self):
-        return None if self._tables is None else self._tables.view(self._T_TABLE)
-
-    @property
-    def block_states(self):
-        return None if self._tables is None else self._tables.view(self._T_STATE)
-
-    @property
-    def logical_block_lengths(self):
-        return None if self._tables is None else self._tables.view(self._T_LEN)
+    def allocated_pool_blocks(self) -> int:
+        return self._rows.capacity
 
     def is_allocated(self) -> bool:
         return self.hot_k_pool is not None
 
-    def _target_capacity(self, physical_idx: int) -> int:
-        required = int(physical_idx) + 1
-        return min(self.pool_blocks, _ceil_div(required, self.pool_chunk_blocks) * self.pool_chunk_blocks)
-
-    def _check_physical_idx(self, physical_idx: int) -> int:
-        physical_idx = int(physical_idx)
-        if physical_idx < 0 or physical_idx >= self.pool_blocks:
-            raise RuntimeError(
-                f"Physical block {physical_idx} is outside tensor-pool capacity {self.pool_blocks}."
-            )
+    def _row_of(self, physical_idx: int) -> int:
         return physical_idx
 
-    def _grow_storage(self, required_physical_idx: int) -> None:
-        if required_physical_idx < self.allocated_pool_blocks:
-            return
-        new_capacity = self._target_capacity(required_physical_idx)
-        if new_capacity <= self.allocated_pool_blocks:
-            return
-        old = self.allocated_pool_blocks
+    def _grow_rows(self, old: int, new: int) -> None:
         self._launch_queue()
-        shape = (new_capacity, self.kv_heads, self.block_size, self.head_dim)
-        self.hot_k_pool = self._grow_copy(self.hot_k_pool, torch.zeros(shape, device=self.device,
-                                                                      dtype=torch.float16), old)
-        self.hot_v_pool = self._grow_copy(self.hot_v_pool, torch.zeros(shape, device=self.device,
-                                                                      dtype=torch.float16), old)
-        self.warm_k_pool = self._grow_copy(self.warm_k_pool, torch.zeros(shape, device=self.device,
-                                                                        dtype=self._warm_dtype()), old)
-        self.warm_v_pool = self._grow_copy(self.warm_v_pool, torch.zeros(shape, device=self.device,
-                                                                        dtype=self._warm_dtype()), old)
-        self.k_scale = self._grow_copy(self.k_scale, self._new_scale(new_capacity, 1), old)
-        self.k_zero = self._grow_copy(self.k_zero, self._new_zero_point(new_capacity), old)
-        self.v_scale = self._grow_copy(self.v_scale, self._new_scale(new_capacity, 1), old)
-        self.v_zero = self._grow_copy(self.v_zero, self._new_zero_point(new_capacity), old)
+        shape = (new, self.kv_heads, self.block_size, self.head_dim)
+        for name, dtype in (("hot_k_pool", torch.float16), ("hot_v_pool", torch.float16),
+                            ("warm_k_pool", self._warm_dtype()), ("warm_v_pool", self._warm_dtype())):
+            setattr(self, name, self._grow_copy(getattr(self, name), torch.zeros(shape, device=self.device,
+                                                                                 dtype=dtype), old))
+        for name, fresh in (("k_scale", self._new_scale(new, 1)), ("k_zero", self._new_zero_point(new)),
+                            ("v_scale", self._new_scale(new, 1)), ("v_zero", self._new_zero_point(new))):
+            setattr(self, name, self._grow_copy(getattr(self, name), fresh, old))
         if self._lengths is None:
-            self._lengths = _Vector(new_capacity, self.device)
+            self._lengths = _Vector(new, self.device)
         else:
-            self._lengths.grow(new_capacity)
-        self.allocated_pool_blocks = new_capacity
+            self._lengths.grow(new)
 
-    def _ensure_allocated(self, key_states: torch.Tensor, required_physical_idx: int) -> None:
+    def _reserve(self, key_states: torch.Tensor, physical_idx: int) -> None:
+        """Tables on the first store, rows up to the chunk above physical_idx."""
         if key_states.ndim != 4:
             raise ValueError("KV tensors must have shape [1, kv_heads, tokens, head_dim].")
         if key_states.shape[0] != 1:
             raise ValueError("TieredKVTensorPool currently supports batch size 1 only.")
-        device = key_states.device
-        kv_heads = int(key_states.shape[1])
-        head_dim = int(key_states.shape[-1])
-        if self.is_allocated():
-            if device != self.device or kv_heads != self.kv_heads or head_dim != self.head_dim:
-                raise ValueError("KV tensor geometry changed after tensor-pool allocation.")
-            self._grow_storage(required_physical_idx)
-            return
-        self.device = device
-        self.kv_heads = kv_heads
-        self.head_dim = head_dim
-        self._tables = _Tables((-1, COLD_STATE, 0), self.num_layers, self.max_blocks_per_layer, device)
-        self._grow_storage(required_physical_idx)
-
-    def get_physical_state(self, physical_idx: int) -> int | None:
-        return self.physical_states.get(int(physical_idx))
+        self._adopt_geometry(key_states)
+        self._rows.cover(physical_idx)
 
     def get_block_length(self, physical_idx: int) -> int:
-        self._check_physical_idx(physical_idx)
-        if self._lengths is None or int(physical_idx) >= self.allocated_pool_blocks:
+        p = self._check_physical_idx(physical_idx)
+        if self._lengths is None or p >= self._rows.capacity:
             return 0
-        return int(self._lengths.host[int(physical_idx)])
+        return int(self._lengths.host[p])
 
-    def _note_length(self, physical_idx: int, length: int) -> None:
-        self._lengths.set(physical_idx, length)
-        if physical_idx in self.physical_locations and self._tables is not None:
-            layer_idx, logical_idx = self.physical_locations[physical_idx]
-            self._tables.set(self._T_LEN, layer_idx, logical_idx, length)
+    def _record(self, physical_idx: int, state: int, length: int | None = None) -> None:
+        """A block's new tier (and token count), mirrored into its table row."""
+        if length is not None:
+            self._lengths.set(physical_idx, length)
+            where = self._where.get(physical_idx)
+            if where is not None and self._tables is not None:
+                self._tables.set(self._t_len, where[0], where[1], length)
+        self._blocks[physical_idx] = _Block(state)
 
     def _write_hot_range(self, physical_idx, start, src_k, src_v, tok0, tokens) -> None:
-        physical_idx = self._check_physical_idx(physical_idx)
-        self._ensure_allocated(src_k, physical_idx)
+        self._reserve(src_k, physical_idx)
         start, tokens = int(start), int(tokens)
-        if start < 0 or start + tokens > self.block_size:
-            raise ValueError("KV write exceeds the physical block capacity.")
+        self._check_range(start, tokens)
         self._queue_write(src_k, src_v, tok0, tokens, physical_idx, start)
-        self._note_length(physical_idx, start + tokens)
-        self.physical_states[physical_idx] = HOT_STATE
-        self.hot_storage.add(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.discard(physical_idx)
-
-    def write_hot_tokens(self, physical_idx: int, start: int, key_states: torch.Tensor,
-                         value_states: torch.Tensor) -> None:
-        """tierkv_policy.py:238-267."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        key_states, value_states = self._coerce_kv(key_states, value_states)
-        self._write_hot_range(physical_idx, start, key_states, value_states, 0, key_states.shape[-2])
-
-    def set_block_entry(self, layer_idx: int, logical_idx: int, physical_idx: int, state: int) -> None:
-        """tierkv_policy.py:269-285."""
-        if not self.is_allocated():
-            raise RuntimeError("TieredKVTensorPool has not been allocated yet.")
-        layer_idx = int(layer_idx)
-        logical_idx = int(logical_idx)
-        physical_idx = self._check_physical_idx(physical_idx)
-        if layer_idx < 0 or layer_idx >= self.num_layers:
-            raise ValueError("layer_idx is out of range.")
-        if logical_idx < 0 or logical_idx >= self.max_blocks_per_layer:
-            raise RuntimeError(
-                f"Logical block {logical_idx} exceeds max_blocks_per_layer={self.max_blocks_per_layer}."
-            )
-        if physical_idx >= self._lengths.host.size:
-            raise IndexError(f"index {physical_idx} is out of bounds for dimension 0 with size "
-                             f"{self._lengths.host.size}")
-        self._tables.set(self._T_TABLE, layer_idx, logical_idx, physical_idx)
-        self._tables.set(self._T_STATE, layer_idx, logical_idx, int(state))
-        self._tables.set(self._T_LEN, layer_idx, logical_idx, int(self._lengths.host[physical_idx]))
-        self.physical_locations[physical_idx] = (layer_idx, logical_idx)
-
-    def set_block_state(self, layer_idx: int, logical_idx: int, state: int) -> None:
-        if not self.is_allocated():
-            raise RuntimeError("TieredKVTensorPool has not been allocated yet.")
-        self._tables.set(self._T_STATE, layer_idx, logical_idx, int(state))
+        self._record(physical_idx, HOT_STATE, start + tokens)
 
     def _write_warm_range(self, physical_idx, src_k, src_v, tok0, length) -> None:
-        physical_idx = self._check_physical_idx(physical_idx)
-        self._ensure_allocated(src_k, physical_idx)
+        self._reserve(src_k, physical_idx)
         self._queue_stage(src_k, src_v, tok0, length, physical_idx)
-        self._note_length(physical_idx, int(length))
-        self.physical_states[physical_idx] = WARM_STATE
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.add(physical_idx)
-        self.cold_storage.discard(physical_idx)
-
-    def write_warm_block(self, physical_idx, k_tensor, v_tensor) -> None:
-        """tierkv_policy.py:292-312 (tokens past the block's length untouched)."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        k_tensor, v_tensor = self._coerce_kv(k_tensor, v_tensor)
-        self._write_warm_range(physical_idx, k_tensor, v_tensor, 0, k_tensor.shape[-2])
+        self._record(physical_idx, WARM_STATE, int(length))
 
     def register_cold_block(self, physical_idx, length: int) -> None:
-        """tierkv_policy.py:314-324."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        if self._lengths is not None:
-            self._note_length(physical_idx, int(length))
-        self.physical_states[physical_idx] = COLD_STATE
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.add(physical_idx)
+        p = self._check_physical_idx(physical_idx)
+        self._record(p, COLD_STATE, int(length) if self._lengths is not None else None)
 
-    def store_hot_block(self, physical_idx, k_tensor, v_tensor) -> None:
-        self.write_hot_tokens(int(physical_idx), 0, k_tensor, v_tensor)
+    def _present(self, op: str, p: int, state) -> bool:
+        if op == "promote_to_hot":
+            return state == WARM_STATE
+        return self.is_allocated() and self.get_block_length(p) > 0
 
-    def demote_to_warm(self, physical_idx) -> None:
-        """tierkv_policy.py:329-361: quantize in place, tail zero-padded."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        if self.get_physical_state(physical_idx) == WARM_STATE:
-            return
-        if self.get_physical_state(physical_idx) == COLD_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not eligible for WARM demotion from COLD storage.")
-        if not self.is_allocated() or self.get_block_length(physical_idx) == 0:
-            raise KeyError(f"Physical block {physical_idx} is not present in HOT storage.")
-        self._queue_demote(physical_idx, physical_idx, self.get_block_length(physical_idx))
-        self.physical_states[physical_idx] = WARM_STATE
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.add(physical_idx)
-        self.cold_storage.discard(physical_idx)
+    def _apply(self, op: str, p: int, state) -> None:
+        if op == "demote_to_warm":
+            self._queue_demote(p, p, self.get_block_length(p))
+            self._record(p, WARM_STATE)
+        elif op == "promote_to_hot":
+            self._queue_promote(p, p, self.get_block_length(p))
+            self._record(p, HOT_STATE)
+        else:
+            self._record(p, COLD_STATE)
 
-    def demote_to_cold(self, physical_idx) -> None:
-        """tierkv_policy.py:363-373 (metadata only)."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        if self.get_physical_state(physical_idx) == COLD_STATE:
-            return
-        if not self.is_allocated() or self.get_block_length(physical_idx) == 0:
-            raise KeyError(f"Physical block {physical_idx} is not present in HOT or WARM storage.")
-        self.physical_states[physical_idx] = COLD_STATE
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.add(physical_idx)
+    def _write_entry(self, layer_idx: int, logical_idx: int, physical_idx: int, state: int) -> None:
+        self._tables.set(self._t_table, layer_idx, logical_idx, physical_idx)
+        self._tables.set(self._t_state, layer_idx, logical_idx, int(state))
+        self._tables.set(self._t_len, layer_idx, logical_idx, int(self._lengths.host[physical_idx]))
+        self._where[physical_idx] = (layer_idx, logical_idx)
 
-    def promote_to_hot(self, physical_idx) -> None:
-        """tierkv_policy.py:375-402: dequantize [:length] in place."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        state = self.get_physical_state(physical_idx)
-        if state == HOT_STATE:
-            return
-        if state == COLD_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not eligible for HOT promotion from COLD storage.")
-        if state != WARM_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not present in WARM storage.")
-        self._queue_promote(physical_idx, physical_idx, self.get_block_length(physical_idx))
-        self.physical_states[physical_idx] = HOT_STATE
-        self.hot_storage.add(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.discard(physical_idx)
+    def _check_row(self, physical_idx: int) -> None:
+        # the reference indexes its per-physical-id lengths tensor here
+        n = self._lengths.host.size
+        if not 0 <= physical_idx < n:
+            raise IndexError(f"index {physical_idx} is out of bounds for dimension 0 with size {n}")
 
-    def get_dequantized_block(self, physical_idx, state):
-        """tierkv_policy.py:404-448."""
+    def set_block_entry(self, layer_idx: int, logical_idx: int, physical_idx: int, state: int) -> None:
+        self._require_allocated()
+        layer_idx, logical_idx = int(layer_idx), int(logical_idx)
         physical_idx = self._check_physical_idx(physical_idx)
-        if not self.is_allocated():
-            raise KeyError(f"Physical block {physical_idx} is not present in tensor-pool storage.")
-        length = self.get_block_length(physical_idx)
-        if state == HOT_STATE:
-            if self.get_physical_state(physical_idx) == WARM_STATE:
-                self.promote_to_hot(physical_idx)
-            if self.get_physical_state(physical_idx) == COLD_STATE:
-                raise KeyError(f"Physical block {physical_idx} is marked HOT but only exists in COLD storage.")
-            self._launch_queue()
-            return (self.hot_k_pool[physical_idx: physical_idx + 1, :, :length, :].contiguous(),
-                    self.hot_v_pool[physical_idx: physical_idx + 1, :, :length, :].contiguous())
-        if state == WARM_STATE:
-            if self.get_physical_state(physical_idx) == COLD_STATE:
-                raise KeyError(f"Physical block {physical_idx} is marked WARM but only exists in COLD storage.")
-            self._launch_queue()
-            if self.get_physical_state(physical_idx) == HOT_STATE:
-                return (self.hot_k_pool[physical_idx: physical_idx + 1, :, :length, :].contiguous(),
-                        self.hot_v_pool[physical_idx: physical_idx + 1, :, :length, :].contiguous())
-            return self._dequantize_slot(physical_idx, length)
-        if state == COLD_STATE:
-            shape = (1, self.kv_heads, length, self.head_dim)
-            return (torch.zeros(shape, device=self.device, dtype=torch.float16),
-                    torch.zeros(shape, device=self.device, dtype=torch.float16))
-        raise ValueError(f"Unsupported block state: {state}")
+        self._check_entry(layer_idx, logical_idx)
+        self._check_row(physical_idx)
+        self._write_entry(layer_idx, logical_idx, physical_idx, state)
 
     def sync_gpu_block_tables(self, layer_idx: int, physical_indices, states) -> None:
-        """tierkv_policy.py:450-477."""
+        """Rewrite one layer's table rows from the BlockManager's lists (tierkv_policy.py:450-477)."""
         if not self.is_allocated():
             return
         self.full_table_sync_count += 1
         layer_idx = int(layer_idx)
-        if layer_idx < 0 or layer_idx >= self.num_layers:
+        if not 0 <= layer_idx < self.num_layers:
             raise ValueError("layer_idx is out of range.")
         if len(physical_indices) > self.max_blocks_per_layer:
-            raise RuntimeError(
-                f"Layer {layer_idx} has {len(physical_indices)} blocks, exceeding max_blocks_per_layer="
-                f"{self.max_blocks_per_layer}."
-            )
+            raise RuntimeError(f"Layer {layer_idx} has {len(physical_indices)} blocks, exceeding "
+                               f"max_blocks_per_layer={self.max_blocks_per_layer}.")
         if len(physical_indices) != len(states):
             raise ValueError("Block table and state table lengths must match.")
-        for p in physical_indices:
-            if not (0 <= int(p) < self._lengths.host.size):
-                raise IndexError("index out of range in self")
-        self._tables.fill_row(self._T_TABLE, layer_idx, -1)
-        self._tables.fill_row(self._T_STATE, layer_idx, COLD_STATE)
-        self._tables.fill_row(self._T_LEN, layer_idx, 0)
-        for logical_idx, (physical_idx, state) in enumerate(zip(physical_indices, states)):
-            self._tables.set(self._T_TABLE, layer_idx, logical_idx, int(physical_idx))
-            self._tables.set(self._T_STATE, layer_idx, logical_idx, int(state))
-            self._tables.set(self._T_LEN, layer_idx, logical_idx, int(self._lengths.host[int(physical_idx)]))
-            self.physical_locations[int(physical_idx)] = (layer_idx, int(logical_idx))
+        if any(not 0 <= int(p) < self._lengths.host.size for p in physical_indices):
+            raise IndexError("index out of range in self")
+        for k, fill in enumerate(self._table_fills):
+            self._tables.fill_row(k, layer_idx, fill)
+        for logical_idx, (p, s) in enumerate(zip(physical_indices, states)):
+            self._write_entry(layer_idx, logical_idx, int(p), s)
 
-    def get_layer_table(self, layer_idx: int):
-        if not self.is_allocated():
-            raise RuntimeError("TieredKVTensorPool has not been allocated yet.")
-        return self.block_tables[int(layer_idx)], self.block_states[int(layer_idx)]
+    def _active_rows(self, layer_idx: int, n: int):
+        table = self._tables.row(self._t_table, layer_idx)[:n]
+        keep = table >= 0
+        if not keep.any():
+            return None
+        lengths = np.maximum(self._lengths.host[table[keep]], 0).astype(np.int64)
+        return self._tables.row(self._t_state, layer_idx)[:n][keep], lengths
 
-    def get_layer_lengths(self, layer_idx: int):
-        if not self.is_allocated():
-            raise RuntimeError("TieredKVTensorPool has not been allocated yet.")
-        return self.logical_block_lengths[int(layer_idx)]
-
-    def collect_memory_metrics(self, layer_states: dict) -> dict:
-        """tierkv_policy.py:489-654, from the host copies of the tables (no
-        device synchronisation)."""
-        metrics = _zero_metrics()
-        metrics.update({
+    def _capacity_metrics(self, hot_mb, warm_mb, meta_mb) -> dict:
+        cap = int(self._rows.capacity)
+        return {
             "physical_hot_pool_mb": 0.0, "physical_warm_pool_mb": 0.0, "physical_warm_meta_mb": 0.0,
             "physical_total_kv_mb": 0.0, "physical_compression_x": 0.0,
-            "hot_slots_used": 0, "hot_slots_capacity": int(self.allocated_pool_blocks),
-            "warm_slots_used": 0, "warm_slots_capacity": int(self.allocated_pool_blocks),
-            "active_pool_blocks": 0, "allocated_pool_blocks": int(self.allocated_pool_blocks),
-            "pool_blocks": int(self.pool_blocks), "pool_utilization": 0.0,
-            "capacity_utilization": float(self.allocated_pool_blocks) / max(float(self.pool_blocks), 1.0),
-        })
-        if not self.is_allocated() or self.kv_heads is None or self.head_dim is None:
-            return metrics
-        counts = {HOT_STATE: [0, 0], WARM_STATE: [0, 0], COLD_STATE: [0, 0]}
-        active_pool_blocks = 0
-        for layer_idx in range(self.num_layers):
-            layer_state = layer_states.get(layer_idx)
-            num_blocks = int(layer_state.num_blocks) if layer_state is not None else 0
-            if num_blocks <= 0:
-                continue
-            table = self._tables.row(self._T_TABLE, layer_idx)[:num_blocks]
-            states = self._tables.row(self._T_STATE, layer_idx)[:num_blocks]
-            valid = table >= 0
-            if not valid.any():
-                continue
-            lengths = np.maximum(self._lengths.host[table[valid]], 0).astype(np.int64)
-            for s in (HOT_STATE, WARM_STATE, COLD_STATE):
-                mask = states[valid] == s
-                counts[s][0] += int(mask.sum())
-                counts[s][1] += int(lengths[mask].sum())
-            active_pool_blocks += int(valid.sum())
-        lm = _logical_metrics(int(self.kv_heads), int(self.head_dim), counts[HOT_STATE][1],
-                              counts[WARM_STATE][1], counts[COLD_STATE][1], self._warm_token_meta_bytes())
-        hot_mb = self._tensor_mb(self.hot_k_pool) + self._tensor_mb(self.hot_v_pool)
-        warm_mb = self._tensor_mb(self.warm_k_pool) + self._tensor_mb(self.warm_v_pool)
-        meta_mb = sum(self._tensor_mb(t) for t in (self.k_scale, self.k_zero, self.v_scale, self.v_zero))
-        total_mb = hot_mb + warm_mb + meta_mb
-        dense_mb = lm["logical_dense_equivalent_mb"]
-        metrics.update({
-            "hot_blocks": counts[HOT_STATE][0], "warm_blocks": counts[WARM_STATE][0],
-            "cold_blocks": counts[COLD_STATE][0], "hot_tokens": counts[HOT_STATE][1],
-            "warm_tokens": counts[WARM_STATE][1], "cold_tokens": counts[COLD_STATE][1],
-            "active_tokens": lm["active_tokens"],
-            "logical_hot_mb": lm["logical_hot_mb"], "logical_warm_mb": lm["logical_warm_mb"],
-            "logical_warm_meta_mb": lm["logical_warm_meta_mb"],
-            "logical_cold_evicted_mb": lm["logical_cold_evicted_mb"],
-            "logical_dense_equivalent_mb": dense_mb, "logical_resident_mb": lm["logical_resident_mb"],
-            "logical_compression_ratio": lm["_resident_b"] / lm["_dense_b"] if lm["_dense_b"] > 0 else 0.0,
-            "logical_compression_x": lm["_dense_b"] / lm["_resident_b"] if lm["_resident_b"] > 0 else 0.0,
-            "active_pool_blocks": active_pool_blocks,
-            "pool_utilization": active_pool_blocks / max(float(self.allocated_pool_blocks), 1.0),
-            "physical_hot_pool_mb": hot_mb, "physical_warm_pool_mb": warm_mb,
-            "physical_warm_meta_mb": meta_mb, "physical_total_kv_mb": total_mb,
+            "hot_slots_used": 0, "hot_slots_capacity": cap, "warm_slots_used": 0, "warm_slots_capacity": cap,
+            "active_pool_blocks": 0, "allocated_pool_blocks": cap, "pool_blocks": int(self.pool_blocks),
+            "pool_utilization": 0.0, "capacity_utilization": float(cap) / max(float(self.pool_blocks), 1.0),
+        }
+
+    def _usage_metrics(self, blocks, active, dense_b, resident_b, total_mb) -> dict:
+        hot_mb, warm_mb, meta_mb = self._physical_mb()
+        dense_mb = dense_b / float(1024 ** 2)
+        return {
+            "logical_compression_ratio": resident_b / dense_b if dense_b > 0 else 0.0,
+            "logical_compression_x": dense_b / resident_b if resident_b > 0 else 0.0,
+            "active_pool_blocks": active,
+            "pool_utilization": active / max(float(self._rows.capacity), 1.0),
+            "physical_hot_pool_mb": hot_mb, "physical_warm_pool_mb": warm_mb, "physical_warm_meta_mb": meta_mb,
+            "physical_total_kv_mb": total_mb,
             "physical_compression_x": dense_mb / max(total_mb, 1e-12) if dense_mb > 0 else 0.0,
-            "hot_slots_used": counts[HOT_STATE][0], "warm_slots_used": counts[WARM_STATE][0],
-        })
-        return metrics
+            "hot_slots_used": blocks[HOT_STATE], "warm_slots_used": blocks[WARM_STATE],
+        }
 
-    def clear(self) -> None:
-        """tierkv_policy.py:662-674 (pool contents are left as they are)."""
-        self._launch_queue()
-        if self.is_allocated():
+    def _reset_rows(self) -> None:
+        if self._lengths is not None and self.is_allocated():
             self._lengths.zero()
-            self._tables.reset()
-        self.physical_states.clear()
-        self.physical_locations.clear()
-        self.hot_storage.clear()
-        self.warm_storage.clear()
-        self.cold_storage.clear()
-        self.full_table_sync_count = 0
 
-    def release(self) -> None:
-        self._launch_queue()
-        self.hot_k_pool = None
-        self.hot_v_pool = None
-        self.warm_k_pool = None
-        self.warm_v_pool = None
-        self.k_scale = None
-        self.k_zero = None
-        self.v_scale = None
-        self.v_zero = None
+    def _drop_rows(self) -> None:
         self._lengths = None
-        self._tables = None
-        self.device = None
-        self.kv_heads = None
-        self.head_dim = None
-        self.allocated_pool_blocks = 0
-        self.physical_states.clear()
-        self.physical_locations.clear()
-        self.hot_storage.clear()
-        self.warm_storage.clear()
-        self.cold_storage.clear()
-        self.full_table_sync_count = 0
+        self._rows.drop()
 
 
 # ---------------------------------------------------------------------------
-# Compact pool (tierkv_policy.py:701-1365): separate HOT and WARM slot pools,
-# tables hold the state-specific slot (-1 for COLD).
+# Compact layout (tierkv_policy.py:701-1365): HOT and WARM keep their own slot
+# storage; the table holds the tier-specific slot (-1 for COLD) beside the
+# physical id.
 # ---------------------------------------------------------------------------
 
-class CompactTieredKVTensorPool(_QueuedStorage):
-    _T_PHYS, _T_SLOT, _T_STATE, _T_LEN = 0, 1, 2, 3
+class CompactTieredKVTensorPool(_PoolBase):
+    _table_fills = (-1, -1, COLD_STATE, 0)
+    _t_phys, _t_table, _t_state, _t_len = 0, 1, 2, 3
+    _capacity_word = "tensor-pool metadata"
+    _storage_word = "compact tensor-pool"
 
     def __init__(
         self,
@@ -1005,499 +1135,243 @@ class CompactTieredKVTensorPool(_QueuedStorage):
         *,
         warm_format: str = "ref_u8",
     ):
-        if num_layers <= 0:
-            raise ValueError("num_layers must be positive.")
-        if block_size <= 0:
-            raise ValueError("block_size must be positive.")
-        if max_seq_len <= 0:
-            raise ValueError("max_seq_len must be positive.")
-
-        self.num_layers = int(num_layers)
-        self.block_size = int(block_size)
-        self.max_seq_len = int(max_seq_len)
-        self.max_blocks_per_layer = int(max_blocks_per_layer or _ceil_div(max_seq_len, block_size))
-        self.pool_blocks = int(pool_blocks or self.num_layers * self.max_blocks_per_layer)
-        self.pool_chunk_blocks = int(pool_chunk_blocks)
-        self.max_hot_slots = int(max_hot_slots if max_hot_slots is not None else self.pool_blocks)
-        self.max_warm_slots = int(max_warm_slots if max_warm_slots is not None else self.pool_blocks)
+        super().__init__(num_layers, block_size, max_seq_len, max_blocks_per_layer, pool_blocks, pool_chunk_blocks,
+                         warm_format)
+        self.max_hot_slots = int(self.pool_blocks if max_hot_slots is None else max_hot_slots)
+        self.max_warm_slots = int(self.pool_blocks if max_warm_slots is None else max_warm_slots)
         self.hot_chunk_slots = int(hot_chunk_slots or self.pool_chunk_blocks)
         self.warm_chunk_slots = int(warm_chunk_slots or self.pool_chunk_blocks)
-        if self.max_hot_slots < 0 or self.max_warm_slots < 0:
+        if min(self.max_hot_slots, self.max_warm_slots) < 0:
             raise ValueError("max_hot_slots and max_warm_slots must be non-negative.")
-        self.warm_format = self._check_format(warm_format)
+        self._hot = _SlotArena(self.max_hot_slots, self.hot_chunk_slots, self._grow_hot,
+                               "No HOT slots available in compact TierKV pool.")
+        self._warm = _SlotArena(self.max_warm_slots, self.warm_chunk_slots, self._grow_warm,
+                                "No WARM slots available in compact TierKV pool.")
 
-        self.device = None
-        self.dtype = torch.float16
-        self.kv_heads = None
-        self.head_dim = None
-        self.allocated_pool_blocks = 0
-        self.allocated_hot_slots = 0
-        self.allocated_warm_slots = 0
-
-        self.hot_k_pool = None
-        self.hot_v_pool = None
-        self.warm_k_pool = None
-        self.warm_v_pool = None
-        self.k_scale = None
-        self.k_zero = None
-        self.v_scale = None
-        self.v_zero = None
-        self._tables: _Tables | None = None
-        self.full_table_sync_count = 0
-
-        self.physical_states: dict[int, int] = {}
-        self.physical_locations: dict[int, tuple[int, int]] = {}
-        self.physical_lengths: dict[int, int] = {}
-        self.physical_slots: dict[int, int] = {}
-        self.hot_free_slots: list[int] = []
-        self.warm_free_slots: list[int] = []
-        self.hot_storage = set()
-        self.warm_storage = set()
-        self.cold_storage = set()
-        self._init_queue()
+    # Views of the slot arenas and the ledger in the reference's names.
+    @property
+    def hot_free_slots(self) -> list:
+        return self._hot.free
 
     @property
+    def warm_free_slots(self) -> list:
+        return self._warm.free
+
+    @property
+    def allocated_hot_slots(self) -> int:
+        return self._hot.capacity
+
+    @property
+    def allocated_warm_slots(self) -> int:
+        return self._warm.capacity
+
+    @property
+    def allocated_pool_blocks(self) -> int:
+        return max(self._hot.capacity, self._warm.capacity)
+
+    @property
+    def physical_slots(self) -> dict:
+        return {p: b.slot for p, b in self._blocks.items()}
+
+    @property
+    def physical_lengths(self) -> dict:
+        return {p: b.length for p, b in self._blocks.items()}
+
+    # Table views (queued entries are pushed first).
+    @property
     def physical_block_tables(self):
-        return None if self._tables is None else self._tables.view(self._T_PHYS)
+        return None if self._tables is None else self._tables.view(self._t_phys)
 
     @property
     def block_slot_indices(self):
-        return None if self._tables is None else self._tables.view(self._T_SLOT)
+        return None if self._tables is None else self._tables.view(self._t_table)
 
-    @property
-    def block_tables(self):
-        return self.block_slot_indices
+    block_tables = block_slot_indices
 
     @property
     def block_states(self):
-        return None if self._tables is None else self._tables.view(self._T_STATE)
+        return None if self._tables is None else self._tables.view(self._t_state)
 
     @property
     def block_lengths(self):
-        return None if self._tables is None else self._tables.view(self._T_LEN)
+        return None if self._tables is None else self._tables.view(self._t_len)
 
     def is_allocated(self) -> bool:
         return self._tables is not None
 
-    def _check_physical_idx(self, physical_idx: int) -> int:
-        physical_idx = int(physical_idx)
-        if physical_idx < 0 or physical_idx >= self.pool_blocks:
-            raise RuntimeError(
-                f"Physical block {physical_idx} is outside tensor-pool metadata capacity {self.pool_blocks}."
-            )
-        return physical_idx
+    def get_block_length(self, physical_idx: int) -> int:
+        b = self._blocks.get(int(physical_idx))
+        return 0 if b is None else b.length
 
-    def _ensure_metadata(self, key_states: torch.Tensor) -> None:
-        if key_states.ndim != 4 or key_states.shape[0] != 1:
-            raise ValueError("KV tensors must have shape [1, kv_heads, tokens, head_dim].")
-        device = key_states.device
-        kv_heads = int(key_states.shape[1])
-        head_dim = int(key_states.shape[-1])
-        if self.is_allocated():
-            if device != self.device or kv_heads != self.kv_heads or head_dim != self.head_dim:
-                raise ValueError("KV tensor geometry changed after tensor-pool allocation.")
-            return
-        self.device = device
-        self.kv_heads = kv_heads
-        self.head_dim = head_dim
-        self._tables = _Tables((-1, -1, COLD_STATE, 0), self.num_layers, self.max_blocks_per_layer, device)
+    def _row_of(self, physical_idx: int) -> int:
+        return self._blocks[physical_idx].slot
 
-    def _new_kv_pool(self, capacity: int, dtype):
-        return torch.zeros((capacity, self.kv_heads, self.block_size, self.head_dim), device=self.device,
-                           dtype=dtype)
+    def _kv_rows(self, n: int, dtype):
+        return torch.zeros((n, self.kv_heads, self.block_size, self.head_dim), device=self.device, dtype=dtype)
 
-    def _ensure_decode_placeholders(self) -> None:
-        """One-slot pools so the decode kernel gets valid pointers before the
-        first HOT / WARM block exists (tierkv_policy.py:814-826)."""
-        if not self.is_allocated():
-            return
-        if self.hot_k_pool is None:
-            self.hot_k_pool = self._new_kv_pool(1, torch.float16)
-            self.hot_v_pool = self._new_kv_pool(1, torch.float16)
-        if self.warm_k_pool is None:
-            self.warm_k_pool = self._new_kv_pool(1, self._warm_dtype())
-            self.warm_v_pool = self._new_kv_pool(1, self._warm_dtype())
-            self.k_scale = self._new_scale(1, 1)
-            self.k_zero = self._new_zero_point(1)
-            self.v_scale = self._new_scale(1, 1)
-            self.v_zero = self._new_zero_point(1)
-
-    def _grow_hot_slots(self) -> None:
-        """tierkv_policy.py:849-869."""
-        if self.allocated_hot_slots >= self.max_hot_slots:
-            raise RuntimeError("No HOT slots available in compact TierKV pool.")
+    def _grow_hot(self, old: int, new: int) -> None:
         self._launch_queue()
-        old = self.allocated_hot_slots
-        new = min(self.max_hot_slots, old + max(1, self.hot_chunk_slots))
-        self.hot_k_pool = self._grow_copy(self.hot_k_pool, self._new_kv_pool(new, torch.float16), old)
-        self.hot_v_pool = self._grow_copy(self.hot_v_pool, self._new_kv_pool(new, torch.float16), old)
-        self.hot_free_slots.extend(range(new - 1, old - 1, -1))
-        self.allocated_hot_slots = new
-        self.allocated_pool_blocks = max(self.allocated_hot_slots, self.allocated_warm_slots)
+        self.hot_k_pool = self._grow_copy(self.hot_k_pool, self._kv_rows(new, torch.float16), old)
+        self.hot_v_pool = self._grow_copy(self.hot_v_pool, self._kv_rows(new, torch.float16), old)
 
-    def _grow_warm_slots(self) -> None:
-        """tierkv_policy.py:871-895."""
-        if self.allocated_warm_slots >= self.max_warm_slots:
-            raise RuntimeError("No WARM slots available in compact TierKV pool.")
+    def _grow_warm(self, old: int, new: int) -> None:
         self._launch_queue()
-        old = self.allocated_warm_slots
-        new = min(self.max_warm_slots, old + max(1, self.warm_chunk_slots))
-        self.warm_k_pool = self._grow_copy(self.warm_k_pool, self._new_kv_pool(new, self._warm_dtype()), old)
-        self.warm_v_pool = self._grow_copy(self.warm_v_pool, self._new_kv_pool(new, self._warm_dtype()), old)
+        self.warm_k_pool = self._grow_copy(self.warm_k_pool, self._kv_rows(new, self._warm_dtype()), old)
+        self.warm_v_pool = self._grow_copy(self.warm_v_pool, self._kv_rows(new, self._warm_dtype()), old)
         self.k_scale = self._grow_copy(self.k_scale, self._new_scale(new, 1), old)
         self.k_zero = self._grow_copy(self.k_zero, self._new_zero_point(new), old)
         self.v_scale = self._grow_copy(self.v_scale, self._new_scale(new, 1), old)
         self.v_zero = self._grow_copy(self.v_zero, self._new_zero_point(new), old)
-        self.warm_free_slots.extend(range(new - 1, old - 1, -1))
-        self.allocated_warm_slots = new
-        self.allocated_pool_blocks = max(self.allocated_hot_slots, self.allocated_warm_slots)
 
-    def _alloc_hot_slot(self) -> int:
-        if not self.hot_free_slots:
-            self._grow_hot_slots()
-        return int(self.hot_free_slots.pop())
+    def _before_decode(self) -> None:
+        """One-row tensors for a tier that has never stored a block, so the
+        decode kernel always receives valid pointers (tierkv_policy.py:814-826);
+        the tier's first growth replaces them."""
+        if self.hot_k_pool is None:
+            self.hot_k_pool, self.hot_v_pool = self._kv_rows(1, torch.float16), self._kv_rows(1, torch.float16)
+        if self.warm_k_pool is None:
+            self.warm_k_pool, self.warm_v_pool = (self._kv_rows(1, self._warm_dtype()),
+                                                  self._kv_rows(1, self._warm_dtype()))
+            self.k_scale, self.v_scale = self._new_scale(1, 1), self._new_scale(1, 1)
+            self.k_zero, self.v_zero = self._new_zero_point(1), self._new_zero_point(1)
 
-    def _alloc_warm_slot(self) -> int:
-        if not self.warm_free_slots:
-            self._grow_warm_slots()
-        return int(self.warm_free_slots.pop())
+    def _arena(self, state: int) -> _SlotArena | None:
+        return self._hot if state == HOT_STATE else self._warm if state == WARM_STATE else None
 
-    def _free_hot_slot(self, slot_idx: int) -> None:
-        slot_idx = int(slot_idx)
-        if slot_idx >= 0:
-            self.hot_free_slots.append(slot_idx)
+    def _release_slot(self, physical_idx: int) -> None:
+        """Give the block's current slot back to its tier's stack."""
+        b = self._blocks.get(physical_idx)
+        if b is not None and self._arena(b.state) is not None:
+            self._arena(b.state).give(b.slot)
 
-    def _free_warm_slot(self, slot_idx: int) -> None:
-        slot_idx = int(slot_idx)
-        if slot_idx >= 0:
-            self.warm_free_slots.append(slot_idx)
-
-    def _set_metadata(self, physical_idx: int, state: int, slot_idx: int, length: int) -> None:
-        """tierkv_policy.py:917-926."""
-        self.physical_states[int(physical_idx)] = int(state)
-        self.physical_slots[int(physical_idx)] = int(slot_idx)
-        self.physical_lengths[int(physical_idx)] = int(length)
-        location = self.physical_locations.get(int(physical_idx))
-        if location is not None and self.is_allocated():
-            layer_idx, logical_idx = location
-            self._tables.set(self._T_STATE, layer_idx, logical_idx, int(state))
-            self._tables.set(self._T_SLOT, layer_idx, logical_idx, int(slot_idx))
-            self._tables.set(self._T_LEN, layer_idx, logical_idx, int(length))
-
-    def get_physical_state(self, physical_idx: int) -> int | None:
-        return self.physical_states.get(int(physical_idx))
-
-    def get_block_length(self, physical_idx: int) -> int:
-        return int(self.physical_lengths.get(int(physical_idx), 0))
+    def _record(self, physical_idx: int, state: int, slot: int, length: int) -> None:
+        """A block's new tier, slot and token count, mirrored into its table row
+        (tierkv_policy.py:917-926)."""
+        self._blocks[physical_idx] = _Block(int(state), int(slot), int(length))
+        where = self._where.get(physical_idx)
+        if where is not None and self._tables is not None:
+            for column, value in ((self._t_state, state), (self._t_table, slot), (self._t_len, length)):
+                self._tables.set(column, where[0], where[1], int(value))
 
     def _write_hot_range(self, physical_idx, start, src_k, src_v, tok0, tokens) -> None:
-        """write_hot_tokens (934-967) for tokens [tok0, tok0 + tokens) of a whole source."""
-        self._ensure_metadata(src_k)
+        if src_k.ndim != 4 or src_k.shape[0] != 1:
+            raise ValueError("KV tensors must have shape [1, kv_heads, tokens, head_dim].")
+        self._adopt_geometry(src_k)
         start, tokens = int(start), int(tokens)
-        if start < 0 or start + tokens > self.block_size:
-            raise ValueError("KV write exceeds the physical block capacity.")
-        current_state = self.get_physical_state(physical_idx)
-        if current_state == COLD_STATE:
+        self._check_range(start, tokens)
+        held = self.get_physical_state(physical_idx)
+        if held == COLD_STATE:
             raise KeyError(f"Physical block {physical_idx} is COLD and cannot be promoted.")
-        if current_state == WARM_STATE:
+        if held == WARM_STATE:
             self.promote_to_hot(physical_idx)
-        slot_idx = self.physical_slots.get(physical_idx)
-        if slot_idx is None or current_state is None:
-            slot_idx = self._alloc_hot_slot()
-        self._queue_write(src_k, src_v, tok0, tokens, slot_idx, start)
-        self.hot_storage.add(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.discard(physical_idx)
-        self._set_metadata(physical_idx, HOT_STATE, slot_idx, start + tokens)
-
-    def write_hot_tokens(self, physical_idx: int, start: int, key_states: torch.Tensor,
-                         value_states: torch.Tensor) -> None:
-        physical_idx = self._check_physical_idx(physical_idx)
-        key_states, value_states = self._coerce_kv(key_states, value_states)
-        with self._batch():
-            self._write_hot_range(physical_idx, start, key_states, value_states, 0, key_states.shape[-2])
+        slot = self._hot.take() if held is None else self._blocks[physical_idx].slot
+        self._queue_write(src_k, src_v, tok0, tokens, slot, start)
+        self._record(physical_idx, HOT_STATE, slot, start + tokens)
 
     def _write_warm_range(self, physical_idx, src_k, src_v, tok0, length) -> None:
-        """write_warm_block (969-1002) for tokens [tok0, tok0 + length) of a whole source."""
-        self._ensure_metadata(src_k)
-        current_state = self.get_physical_state(physical_idx)
-        if current_state == HOT_STATE:
-            self._free_hot_slot(self.physical_slots.get(physical_idx, -1))
-        elif current_state == WARM_STATE:
-            self._free_warm_slot(self.physical_slots.get(physical_idx, -1))
-        elif current_state == COLD_STATE:
+        if src_k.ndim != 4 or src_k.shape[0] != 1:
+            raise ValueError("KV tensors must have shape [1, kv_heads, tokens, head_dim].")
+        self._adopt_geometry(src_k)
+        if self.get_physical_state(physical_idx) == COLD_STATE:
             raise KeyError(f"Physical block {physical_idx} is COLD and cannot be promoted.")
-        slot_idx = self._alloc_warm_slot()
-        self._queue_stage(src_k, src_v, tok0, length, slot_idx)
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.add(physical_idx)
-        self.cold_storage.discard(physical_idx)
-        self._set_metadata(physical_idx, WARM_STATE, slot_idx, int(length))
-
-    def write_warm_block(self, physical_idx, k_tensor, v_tensor) -> None:
-        physical_idx = self._check_physical_idx(physical_idx)
-        k_tensor, v_tensor = self._coerce_kv(k_tensor, v_tensor)
-        with self._batch():
-            self._write_warm_range(physical_idx, k_tensor, v_tensor, 0, k_tensor.shape[-2])
+        self._release_slot(physical_idx)
+        slot = self._warm.take()
+        self._queue_stage(src_k, src_v, tok0, length, slot)
+        self._record(physical_idx, WARM_STATE, slot, int(length))
 
     def register_cold_block(self, physical_idx, length: int) -> None:
-        """tierkv_policy.py:1004-1014."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        state = self.get_physical_state(physical_idx)
-        if state == HOT_STATE:
-            self._free_hot_slot(self.physical_slots.get(physical_idx, -1))
-        elif state == WARM_STATE:
-            self._free_warm_slot(self.physical_slots.get(physical_idx, -1))
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.add(physical_idx)
-        self._set_metadata(physical_idx, COLD_STATE, -1, int(length))
+        p = self._check_physical_idx(physical_idx)
+        self._release_slot(p)
+        self._record(p, COLD_STATE, -1, int(length))
 
-    def store_hot_block(self, physical_idx, k_tensor, v_tensor) -> None:
-        self.write_hot_tokens(int(physical_idx), 0, k_tensor, v_tensor)
+    def _present(self, op: str, p: int, state) -> bool:
+        return state in {"demote_to_warm": (HOT_STATE,), "promote_to_hot": (WARM_STATE,),
+                         "demote_to_cold": (HOT_STATE, WARM_STATE)}[op]
+
+    def _apply(self, op: str, p: int, state) -> None:
+        b = self._blocks[p]
+        if op == "demote_to_cold":
+            self._release_slot(p)
+            self._record(p, COLD_STATE, -1, b.length)
+            return
+        # The destination slot is taken before the source slot is released.
+        if op == "demote_to_warm":
+            dst = self._warm.take()
+            self._queue_demote(b.slot, dst, b.length)
+            self._hot.give(b.slot)
+            self._record(p, WARM_STATE, dst, b.length)
+        else:
+            dst = self._hot.take()
+            self._queue_promote(b.slot, dst, b.length)
+            self._warm.give(b.slot)
+            self._record(p, HOT_STATE, dst, b.length)
 
     def set_block_entry(self, layer_idx: int, logical_idx: int, physical_idx: int, state: int) -> None:
-        """tierkv_policy.py:1019-1035."""
-        if not self.is_allocated():
-            raise RuntimeError("CompactTieredKVTensorPool has not been allocated yet.")
-        layer_idx = int(layer_idx)
-        logical_idx = int(logical_idx)
+        self._require_allocated()
+        layer_idx, logical_idx = int(layer_idx), int(logical_idx)
         physical_idx = self._check_physical_idx(physical_idx)
-        if layer_idx < 0 or layer_idx >= self.num_layers:
-            raise ValueError("layer_idx is out of range.")
-        if logical_idx < 0 or logical_idx >= self.max_blocks_per_layer:
-            raise RuntimeError(
-                f"Logical block {logical_idx} exceeds max_blocks_per_layer={self.max_blocks_per_layer}."
-            )
-        self.physical_locations[physical_idx] = (layer_idx, logical_idx)
-        self._tables.set(self._T_PHYS, layer_idx, logical_idx, physical_idx)
-        self._tables.set(self._T_STATE, layer_idx, logical_idx, int(state))
-        self._tables.set(self._T_SLOT, layer_idx, logical_idx, int(self.physical_slots.get(physical_idx, -1)))
-        self._tables.set(self._T_LEN, layer_idx, logical_idx, int(self.physical_lengths.get(physical_idx, 0)))
-
-    def set_block_state(self, layer_idx: int, logical_idx: int, state: int) -> None:
-        if not self.is_allocated():
-            raise RuntimeError("CompactTieredKVTensorPool has not been allocated yet.")
-        self._tables.set(self._T_STATE, layer_idx, logical_idx, int(state))
-
-    def demote_to_warm(self, physical_idx) -> None:
-        """tierkv_policy.py:1042-1068."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        state = self.get_physical_state(physical_idx)
-        if state == WARM_STATE:
-            return
-        if state == COLD_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not eligible for WARM demotion from COLD storage.")
-        if state != HOT_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not present in HOT storage.")
-        length = self.get_block_length(physical_idx)
-        hot_slot = self.physical_slots[physical_idx]
-        warm_slot = self._alloc_warm_slot()
-        self._queue_demote(hot_slot, warm_slot, length)
-        self._free_hot_slot(hot_slot)
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.add(physical_idx)
-        self.cold_storage.discard(physical_idx)
-        self._set_metadata(physical_idx, WARM_STATE, warm_slot, length)
-
-    def demote_to_cold(self, physical_idx) -> None:
-        """tierkv_policy.py:1070-1085."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        state = self.get_physical_state(physical_idx)
-        if state == COLD_STATE:
-            return
-        if state == HOT_STATE:
-            self._free_hot_slot(self.physical_slots.get(physical_idx, -1))
-        elif state == WARM_STATE:
-            self._free_warm_slot(self.physical_slots.get(physical_idx, -1))
-        elif state is None:
-            raise KeyError(f"Physical block {physical_idx} is not present in HOT or WARM storage.")
-        length = self.get_block_length(physical_idx)
-        self.hot_storage.discard(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.add(physical_idx)
-        self._set_metadata(physical_idx, COLD_STATE, -1, length)
-
-    def promote_to_hot(self, physical_idx) -> None:
-        """tierkv_policy.py:1087-1115."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        state = self.get_physical_state(physical_idx)
-        if state == HOT_STATE:
-            return
-        if state == COLD_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not eligible for HOT promotion from COLD storage.")
-        if state != WARM_STATE:
-            raise KeyError(f"Physical block {physical_idx} is not present in WARM storage.")
-        length = self.get_block_length(physical_idx)
-        warm_slot = self.physical_slots[physical_idx]
-        hot_slot = self._alloc_hot_slot()
-        self._queue_promote(warm_slot, hot_slot, length)
-        self._free_warm_slot(warm_slot)
-        self.hot_storage.add(physical_idx)
-        self.warm_storage.discard(physical_idx)
-        self.cold_storage.discard(physical_idx)
-        self._set_metadata(physical_idx, HOT_STATE, hot_slot, length)
-
-    def get_dequantized_block(self, physical_idx, state):
-        """tierkv_policy.py:1117-1162."""
-        physical_idx = self._check_physical_idx(physical_idx)
-        if not self.is_allocated():
-            raise KeyError(f"Physical block {physical_idx} is not present in compact tensor-pool storage.")
-        length = self.get_block_length(physical_idx)
-        actual_state = self.get_physical_state(physical_idx)
-        if state == HOT_STATE:
-            if actual_state == WARM_STATE:
-                self.promote_to_hot(physical_idx)
-                actual_state = HOT_STATE
-            if actual_state == COLD_STATE:
-                raise KeyError(f"Physical block {physical_idx} is marked HOT but only exists in COLD storage.")
-            self._launch_queue()
-            slot_idx = self.physical_slots[physical_idx]
-            return (self.hot_k_pool[slot_idx: slot_idx + 1, :, :length, :].contiguous(),
-                    self.hot_v_pool[slot_idx: slot_idx + 1, :, :length, :].contiguous())
-        if state == WARM_STATE:
-            if actual_state == COLD_STATE:
-                raise KeyError(f"Physical block {physical_idx} is marked WARM but only exists in COLD storage.")
-            self._launch_queue()
-            slot_idx = self.physical_slots[physical_idx]
-            if actual_state == HOT_STATE:
-                return (self.hot_k_pool[slot_idx: slot_idx + 1, :, :length, :].contiguous(),
-                        self.hot_v_pool[slot_idx: slot_idx + 1, :, :length, :].contiguous())
-            return self._dequantize_slot(slot_idx, length)
-        if state == COLD_STATE:
-            shape = (1, self.kv_heads, length, self.head_dim)
-            return (torch.zeros(shape, device=self.device, dtype=torch.float16),
-                    torch.zeros(shape, device=self.device, dtype=torch.float16))
-        raise ValueError(f"Unsupported block state: {state}")
+        self._check_entry(layer_idx, logical_idx)
+        self._where[physical_idx] = (layer_idx, logical_idx)
+        b = self._blocks.get(physical_idx)
+        for column, value in ((self._t_phys, physical_idx), (self._t_state, state),
+                              (self._t_table, -1 if b is None else b.slot), (self._t_len, 0 if b is None else b.length)):
+            self._tables.set(column, layer_idx, logical_idx, int(value))
 
     def sync_gpu_block_tables(self, layer_idx: int, physical_indices, states) -> None:
-        """tierkv_policy.py:1164-1174."""
+        """Rewrite one layer's table rows from the BlockManager's lists (tierkv_policy.py:1164-1174)."""
         if not self.is_allocated():
             return
         self.full_table_sync_count += 1
         layer_idx = int(layer_idx)
-        for k, fill in ((self._T_PHYS, -1), (self._T_SLOT, -1), (self._T_STATE, COLD_STATE), (self._T_LEN, 0)):
+        for k, fill in enumerate(self._table_fills):
             self._tables.fill_row(k, layer_idx, fill)
-        for logical_idx, (physical_idx, state) in enumerate(zip(physical_indices, states)):
-            self.set_block_entry(layer_idx, logical_idx, int(physical_idx), int(state))
+        for logical_idx, (p, s) in enumerate(zip(physical_indices, states)):
+            self.set_block_entry(layer_idx, logical_idx, int(p), int(s))
 
-    def get_layer_table(self, layer_idx: int):
-        if not self.is_allocated():
-            raise RuntimeError("CompactTieredKVTensorPool has not been allocated yet.")
-        self._ensure_decode_placeholders()
-        return self.block_slot_indices[int(layer_idx)], self.block_states[int(layer_idx)]
+    def _active_rows(self, layer_idx: int, n: int):
+        return (self._tables.row(self._t_state, layer_idx)[:n],
+                self._tables.row(self._t_len, layer_idx)[:n].astype(np.int64))
 
-    def get_layer_lengths(self, layer_idx: int):
-        if not self.is_allocated():
-            raise RuntimeError("CompactTieredKVTensorPool has not been allocated yet.")
-        return self.block_lengths[int(layer_idx)]
-
-    def collect_memory_metrics(self, layer_states: dict) -> dict:
-        """tierkv_policy.py:1193-1317, from the host copies of the tables."""
-        hot_mb = self._tensor_mb(self.hot_k_pool) + self._tensor_mb(self.hot_v_pool)
-        warm_mb = self._tensor_mb(self.warm_k_pool) + self._tensor_mb(self.warm_v_pool)
-        meta_mb = sum(self._tensor_mb(t) for t in (self.k_scale, self.k_zero, self.v_scale, self.v_zero))
-        metrics = _zero_metrics()
-        metrics.update({
+    def _capacity_metrics(self, hot_mb, warm_mb, meta_mb) -> dict:
+        return {
             "active_pool_blocks": 0, "allocated_pool_blocks": int(self.allocated_pool_blocks),
             "pool_blocks": int(self.pool_blocks), "pool_utilization": 0.0, "capacity_utilization": 0.0,
             "physical_hot_pool_mb": hot_mb, "physical_warm_pool_mb": warm_mb, "physical_warm_meta_mb": meta_mb,
             "physical_total_kv_mb": hot_mb + warm_mb + meta_mb, "physical_compression_x": 0.0,
-            "hot_slots_used": len(self.hot_storage), "hot_slots_capacity": int(self.allocated_hot_slots),
-            "warm_slots_used": len(self.warm_storage), "warm_slots_capacity": int(self.allocated_warm_slots),
-        })
-        if not self.is_allocated() or self.kv_heads is None or self.head_dim is None:
-            return metrics
-        counts = {HOT_STATE: [0, 0], WARM_STATE: [0, 0], COLD_STATE: [0, 0]}
-        for layer_idx in range(self.num_layers):
-            layer_state = layer_states.get(layer_idx)
-            num_blocks = int(layer_state.num_blocks) if layer_state is not None else 0
-            if num_blocks <= 0:
-                continue
-            states = self._tables.row(self._T_STATE, layer_idx)[:num_blocks]
-            lengths = self._tables.row(self._T_LEN, layer_idx)[:num_blocks].astype(np.int64)
-            for s in (HOT_STATE, WARM_STATE, COLD_STATE):
-                mask = states == s
-                counts[s][0] += int(mask.sum())
-                counts[s][1] += int(lengths[mask].sum())
-        lm = _logical_metrics(int(self.kv_heads), int(self.head_dim), counts[HOT_STATE][1],
-                              counts[WARM_STATE][1], counts[COLD_STATE][1], self._warm_token_meta_bytes())
-        dense_mb = lm["logical_dense_equivalent_mb"]
-        resident_mb = lm["logical_resident_mb"]
-        resident_blocks = counts[HOT_STATE][0] + counts[WARM_STATE][0]
-        allocated = self.allocated_hot_slots + self.allocated_warm_slots
-        total_mb = hot_mb + warm_mb + meta_mb
-        metrics.update({
-            "hot_blocks": counts[HOT_STATE][0], "warm_blocks": counts[WARM_STATE][0],
-            "cold_blocks": counts[COLD_STATE][0], "hot_tokens": counts[HOT_STATE][1],
-            "warm_tokens": counts[WARM_STATE][1], "cold_tokens": counts[COLD_STATE][1],
-            "active_tokens": lm["active_tokens"],
-            "logical_hot_mb": lm["logical_hot_mb"], "logical_warm_mb": lm["logical_warm_mb"],
-            "logical_warm_meta_mb": lm["logical_warm_meta_mb"],
-            "logical_cold_evicted_mb": lm["logical_cold_evicted_mb"],
-            "logical_dense_equivalent_mb": dense_mb, "logical_resident_mb": resident_mb,
+            "hot_slots_used": len(self.hot_storage), "hot_slots_capacity": int(self._hot.capacity),
+            "warm_slots_used": len(self.warm_storage), "warm_slots_capacity": int(self._warm.capacity),
+        }
+
+    def _usage_metrics(self, blocks, active, dense_b, resident_b, total_mb) -> dict:
+        mb = float(1024 ** 2)
+        dense_mb, resident_mb = dense_b / mb, resident_b / mb
+        resident_blocks = blocks[HOT_STATE] + blocks[WARM_STATE]
+        allocated = self._hot.capacity + self._warm.capacity
+        limit = self.max_hot_slots + self.max_warm_slots
+        return {
             "logical_compression_ratio": resident_mb / dense_mb if dense_mb > 0 else 0.0,
             "logical_compression_x": dense_mb / resident_mb if resident_mb > 0 else 0.0,
-            "active_pool_blocks": resident_blocks,
-            "allocated_pool_blocks": int(allocated),
-            "pool_blocks": int(self.max_hot_slots + self.max_warm_slots),
+            "active_pool_blocks": resident_blocks, "allocated_pool_blocks": int(allocated), "pool_blocks": int(limit),
             "pool_utilization": resident_blocks / max(float(allocated), 1.0),
-            "capacity_utilization": allocated / max(float(self.max_hot_slots + self.max_warm_slots), 1.0),
+            "capacity_utilization": allocated / max(float(limit), 1.0),
             "physical_compression_x": dense_mb / total_mb if total_mb > 0 else 0.0,
-        })
-        return metrics
+        }
 
-    def clear(self) -> None:
-        """tierkv_policy.py:1319-1334 (pool contents are left as they are)."""
-        self._launch_queue()
-        if self.is_allocated():
-            self._tables.reset()
-        self.physical_states.clear()
-        self.physical_locations.clear()
-        self.physical_lengths.clear()
-        self.physical_slots.clear()
-        self.hot_storage.clear()
-        self.warm_storage.clear()
-        self.cold_storage.clear()
-        self.hot_free_slots = list(range(self.allocated_hot_slots - 1, -1, -1))
-        self.warm_free_slots = list(range(self.allocated_warm_slots - 1, -1, -1))
-        self.full_table_sync_count = 0
+    def _reset_rows(self) -> None:
+        self._hot.all_free()
+        self._warm.all_free()
 
-    def release(self) -> None:
-        self._launch_queue()
-        self.hot_k_pool = None
-        self.hot_v_pool = None
-        self.warm_k_pool = None
-        self.warm_v_pool = None
-        self.k_scale = None
-        self.k_zero = None
-        self.v_scale = None
-        self.v_zero = None
-        self._tables = None
-        self.device = None
-        self.kv_heads = None
-        self.head_dim = None
-        self.allocated_pool_blocks = 0
-        self.allocated_hot_slots = 0
-        self.allocated_warm_slots = 0
-        self.physical_states.clear()
-        self.physical_locations.clear()
-        self.physical_lengths.clear()
-        self.physical_slots.clear()
-        self.hot_free_slots.clear()
-        self.warm_free_slots.clear()
-        self.hot_storage.clear()
-        self.warm_storage.clear()
-        self.cold_storage.clear()
-        self.full_table_sync_count = 0
+    def _drop_rows(self) -> None:
+        self._hot.drop()
+        self._warm.drop()
 
 
 # The reference keeps the old public name for its tests (tierkv_policy.py:1368-1369).
 PhysicalKVPool = TieredKVTensorPool
 
-
 # ---------------------------------------------------------------------------
-# Policy engine (tierkv_policy.py:1372-1478).
+# Policy engine (tierkv_policy.py:1372-1478): scores in, BlockManager states
+# out; the ranking runs in the label kernel.
 # ---------------------------------------------------------------------------
 
 def _score_device(block_scores: torch.Tensor) -> torch.device:
@@ -1553,58 +1427,40 @@ class TierKVPolicyEngine:
         _lib.check(rc, "tierkv_block_mass_from_probs")
         return out[0].to(attn_weights.dtype)
 
-    def _checked_states(self, seq_id, block_scores):
-        physical_indices = self.block_manager.get_physical_indices(seq_id)
-        current_states = self.block_manager.get_states(seq_id)
-        return physical_indices, current_states
-
-    def _apply(self, seq_id, current_states, desired) -> None:
-        for block_idx, (cur, want) in enumerate(zip(current_states, desired)):
-            if cur != want:
-                self.block_manager.update_block_state(seq_id, block_idx, int(want))
+    def _relabel(self, seq_id, block_scores, hot_budget, warm_budget, mode, demoted_state=WARM_STATE) -> None:
+        """Rank the sequence's blocks and write the states that change into
+        the BlockManager (tierkv_policy.py:1391-1477).  Sequences of at most
+        two blocks are all HOT (the first and last blocks are reserved)."""
+        current = self.block_manager.get_states(seq_id)
+        n = len(self.block_manager.get_physical_indices(seq_id))
+        if n == 0:
+            return
+        checks = ((mode == "hot_warm" and demoted_state not in (WARM_STATE, COLD_STATE),
+                   "demoted_state must be WARM_STATE or COLD_STATE."),
+                  (block_scores.ndim != 1, "block_scores must be a 1D tensor."),
+                  (block_scores.ndim == 1 and len(block_scores) != n,
+                   "block_scores length must match the allocated block count."),
+                  (len(current) != n, "Block state table is inconsistent with physical index table."))
+        for failed, message in checks:
+            if failed:
+                raise ValueError(message)
+        wanted = ([HOT_STATE] * n if n <= 2
+                  else _labels(block_scores, current, hot_budget, warm_budget, mode, demoted_state))
+        for logical_idx, (have, want) in enumerate(zip(current, wanted)):
+            if have != want:
+                self.block_manager.update_block_state(seq_id, logical_idx, int(want))
 
     def enforce_budget(self, seq_id: int, block_scores: torch.Tensor, hot_budget: int,
                        demoted_state: int = WARM_STATE):
-        """tierkv_policy.py:1391-1432."""
-        physical_indices, current_states = self._checked_states(seq_id, block_scores)
-        num_blocks = len(physical_indices)
-        if num_blocks == 0:
-            return
-        if demoted_state not in (WARM_STATE, COLD_STATE):
-            raise ValueError("demoted_state must be WARM_STATE or COLD_STATE.")
-        if block_scores.ndim != 1:
-            raise ValueError("block_scores must be a 1D tensor.")
-        if len(block_scores) != num_blocks:
-            raise ValueError("block_scores length must match the allocated block count.")
-        if len(current_states) != num_blocks:
-            raise ValueError("Block state table is inconsistent with physical index table.")
-        if num_blocks <= 2:
-            self._apply(seq_id, current_states, [HOT_STATE] * num_blocks)
-            return
-        desired = _labels(block_scores, current_states, hot_budget, 0, "hot_warm", demoted_state)
-        self._apply(seq_id, current_states, desired)
+        self._relabel(seq_id, block_scores, hot_budget, 0, "hot_warm", demoted_state)
 
     def enforce_tiered_budget(self, seq_id: int, block_scores: torch.Tensor, hot_budget: int, warm_budget: int):
-        """tierkv_policy.py:1434-1477."""
-        physical_indices, current_states = self._checked_states(seq_id, block_scores)
-        num_blocks = len(physical_indices)
-        if num_blocks == 0:
-            return
-        if block_scores.ndim != 1:
-            raise ValueError("block_scores must be a 1D tensor.")
-        if len(block_scores) != num_blocks:
-            raise ValueError("block_scores length must match the allocated block count.")
-        if len(current_states) != num_blocks:
-            raise ValueError("Block state table is inconsistent with physical index table.")
-        if num_blocks <= 2:
-            self._apply(seq_id, current_states, [HOT_STATE] * num_blocks)
-            return
-        desired = _labels(block_scores, current_states, hot_budget, warm_budget, "hot_warm_cold")
-        self._apply(seq_id, current_states, desired)
+        self._relabel(seq_id, block_scores, hot_budget, warm_budget, "hot_warm_cold")
 
 
 @dataclass
 class LayerRuntimeState:
+    """A layer's block count and the block still taking appended tokens."""
     open_physical_idx: int | None = None
     open_token_count: int = 0
     num_blocks: int = 0
@@ -1612,23 +1468,22 @@ class LayerRuntimeState:
 
 class TieredKVCache(HFCache):
     """The HF cache object of a tiered runtime (tierkv_policy.py:1487-1531):
-    it only tracks the committed sequence length; the KV lives in the runtime."""
+    it counts the committed tokens; the KV itself lives in the runtime.  The
+    beam and crop hooks are no-ops."""
 
     is_compileable = False
 
     def __init__(self, runtime):
         self.runtime = runtime
         self.is_tierkv_cache = True
-        self.pending_query_length = 0
-        self.committed_seq_len = 0
+        self.reset()
 
     def begin_forward(self, query_length: int) -> None:
         self.pending_query_length = int(query_length)
         self.runtime.begin_forward(query_length)
 
     def finish_forward(self) -> None:
-        self.committed_seq_len += self.pending_query_length
-        self.pending_query_length = 0
+        self.committed_seq_len, self.pending_query_length = self.committed_seq_len + self.pending_query_length, 0
         self.runtime.finish_forward()
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
@@ -1664,6 +1519,85 @@ class TieredKVCache(HFCache):
 # Runtime (tierkv_policy.py:1534-1912).
 # ---------------------------------------------------------------------------
 
+def _flag(value) -> bool:
+    return str(value).lower() in ("1", "true", "yes", "on")
+
+
+# Runtime settings and where they come from (tierkv_policy.py:1551-1575):
+# (name, environment variable, the environment overrides the argument?,
+#  parse, accepted values or a predicate, error message).  Settings the
+# environment does not override read it only when the argument is missing.
+_SETTINGS = (
+    ("attention_backend", "TIERKV_ATTENTION_BACKEND", False, str, ("eager", "triton"),
+     'attention_backend must be "eager" or "triton".'),
+    ("policy_interval", "TIERKV_POLICY_INTERVAL", False, int, lambda v: v > 0, "policy_interval must be positive."),
+    ("pool_chunk_blocks", "TIERKV_POOL_CHUNK_BLOCKS", True, int, lambda v: v > 0,
+     "pool_chunk_blocks must be positive."),
+    ("policy_on_new_block", "TIERKV_POLICY_ON_NEW_BLOCK", True, _flag, None, None),
+    ("score_accumulation_mode", "TIERKV_SCORE_ACCUMULATION_MODE", True, str, ("policy_ticks", "every_step"),
+     'score_accumulation_mode must be "policy_ticks" or "every_step".'),
+    ("policy_mode", "TIERKV_POLICY_MODE", True, str, ("hot_only", "hot_warm", "hot_warm_cold"),
+     'policy_mode must be "hot_only", "hot_warm", or "hot_warm_cold".'),
+    ("warm_budget", "TIERKV_WARM_BUDGET", True, int, lambda v: v >= 0, "warm_budget must be non-negative."),
+    ("pool_layout", "TIERKV_POOL_LAYOUT", True, str, ("compact", "dense"), 'pool_layout must be "compact" or "dense".'),
+)
+# Fallbacks when neither the argument nor the environment gives a value.
+_FALLBACK = {"attention_backend": "triton", "policy_interval": 16, "pool_layout": "compact"}
+
+
+def _resolve_settings(given: dict) -> dict:
+    out = {}
+    for name, var, env_first, parse, accepted, message in _SETTINGS:
+        arg = given[name]
+        missing = arg is None or (name in ("attention_backend", "pool_layout") and not arg)
+        if env_first and var in os.environ:
+            raw = os.environ[var]
+        elif not missing:
+            raw = arg
+        else:
+            raw = os.environ.get(var, _FALLBACK.get(name))
+        value = parse(raw)
+        ok = True if accepted is None else (accepted(value) if callable(accepted) else value in accepted)
+        if not ok:
+            raise ValueError(message)
+        out[name] = value
+    return out
+
+
+class _StageTimer:
+    """HIP-event timing of named host stages (TIERKV_PROFILE=1): each
+    ``end`` waits for the stage's GPU work, as the reference profiler does."""
+
+    def __init__(self, enabled: bool):
+        self.enabled = enabled
+        self.totals: dict[str, float] = {}
+        self.counts: dict[str, int] = {}
+
+    def start(self):
+        if not (self.enabled and torch.cuda.is_available()):
+            return None
+        mark = torch.cuda.Event(enable_timing=True)
+        mark.record()
+        return mark
+
+    def end(self, name: str, mark) -> None:
+        if mark is None:
+            return
+        done = torch.cuda.Event(enable_timing=True)
+        done.record()
+        done.synchronize()
+        self.totals[name] = self.totals.get(name, 0.0) + float(mark.elapsed_time(done))
+        self.counts[name] = self.counts.get(name, 0) + 1
+
+    def summary(self) -> dict:
+        return {name: (total, self.counts.get(name, 0), total / max(self.counts.get(name, 0), 1))
+                for name, total in self.totals.items()}
+
+    def clear(self) -> None:
+        self.totals.clear()
+        self.counts.clear()
+
+
 class TieredKVRuntime:
     def __init__(
         self,
@@ -1684,37 +1618,18 @@ class TieredKVRuntime:
         warm_format: str = "ref_u8",
         prefill_scoring: str = "proxy",
     ):
-        attention_backend = attention_backend or os.environ.get("TIERKV_ATTENTION_BACKEND", "triton")
         if prefill_scoring not in ("proxy", "attention"):
             raise ValueError('prefill_scoring must be "proxy" or "attention".')
+        settings = _resolve_settings(dict(
+            attention_backend=attention_backend, policy_interval=policy_interval, pool_chunk_blocks=pool_chunk_blocks,
+            policy_on_new_block=policy_on_new_block, score_accumulation_mode=score_accumulation_mode,
+            policy_mode=policy_mode, warm_budget=warm_budget, pool_layout=pool_layout))
+        for name, value in settings.items():
+            setattr(self, name, value)
         # Prefill block scores when the model's attention returns no
         # probabilities: "proxy" = the reference's sink + recency scores,
         # "attention" = the prefill block-score kernel (extension).
         self.prefill_scoring = prefill_scoring
-        if attention_backend not in ("eager", "triton"):
-            raise ValueError('attention_backend must be "eager" or "triton".')
-        if policy_interval is None:
-            policy_interval = int(os.environ.get("TIERKV_POLICY_INTERVAL", "16"))
-        if policy_interval <= 0:
-            raise ValueError("policy_interval must be positive.")
-        pool_chunk_blocks = int(os.environ.get("TIERKV_POOL_CHUNK_BLOCKS", pool_chunk_blocks))
-        if pool_chunk_blocks <= 0:
-            raise ValueError("pool_chunk_blocks must be positive.")
-        policy_on_new_block = os.environ.get("TIERKV_POLICY_ON_NEW_BLOCK", str(policy_on_new_block)).lower()
-        policy_on_new_block = policy_on_new_block in ("1", "true", "yes", "on")
-        score_accumulation_mode = os.environ.get("TIERKV_SCORE_ACCUMULATION_MODE", score_accumulation_mode)
-        if score_accumulation_mode not in ("policy_ticks", "every_step"):
-            raise ValueError('score_accumulation_mode must be "policy_ticks" or "every_step".')
-        policy_mode = os.environ.get("TIERKV_POLICY_MODE", policy_mode)
-        if policy_mode not in ("hot_only", "hot_warm", "hot_warm_cold"):
-            raise ValueError('policy_mode must be "hot_only", "hot_warm", or "hot_warm_cold".')
-        warm_budget = int(os.environ.get("TIERKV_WARM_BUDGET", warm_budget))
-        if warm_budget < 0:
-            raise ValueError("warm_budget must be non-negative.")
-        pool_layout = os.environ.get("TIERKV_POOL_LAYOUT", pool_layout or "compact")
-        if pool_layout not in ("compact", "dense"):
-            raise ValueError('pool_layout must be "compact" or "dense".')
-
         self.block_manager = block_manager
         self.num_layers = int(num_layers)
         self.block_size = int(block_size)
@@ -1722,70 +1637,55 @@ class TieredKVRuntime:
         self.max_seq_len = int(max_seq_len)
         self.max_blocks_per_layer = _ceil_div(self.max_seq_len, self.block_size)
         self.pool_blocks = self.num_layers * self.max_blocks_per_layer
-        self.attention_backend = attention_backend
-        self.policy_interval = int(policy_interval)
-        self.pool_chunk_blocks = int(pool_chunk_blocks)
-        self.policy_on_new_block = bool(policy_on_new_block)
-        self.score_accumulation_mode = score_accumulation_mode
-        self.policy_mode = policy_mode
-        self.warm_budget = int(warm_budget)
-        self.pool_layout = pool_layout
         self.demoted_state = WARM_STATE
         self.cold_block_policy = "zero"
-        self.tiered_layer_indices = set(range(num_layers))
-        if self.pool_layout == "compact":
-            hot_slots_per_layer, warm_slots_per_layer = self._compact_slot_capacities()
-            self.kv_pool = CompactTieredKVTensorPool(
-                num_layers=self.num_layers,
-                block_size=self.block_size,
-                max_seq_len=self.max_seq_len,
-                max_blocks_per_layer=self.max_blocks_per_layer,
-                pool_blocks=self.pool_blocks,
-                pool_chunk_blocks=self.pool_chunk_blocks,
-                max_hot_slots=self.num_layers * hot_slots_per_layer,
-                max_warm_slots=self.num_layers * warm_slots_per_layer,
-                hot_chunk_slots=max(1, hot_slots_per_layer),
-                warm_chunk_slots=max(1, warm_slots_per_layer),
-                warm_format=warm_format,
-            )
-        else:
-            self.kv_pool = TieredKVTensorPool(
-                num_layers=self.num_layers,
-                block_size=self.block_size,
-                max_seq_len=self.max_seq_len,
-                max_blocks_per_layer=self.max_blocks_per_layer,
-                pool_blocks=self.pool_blocks,
-                pool_chunk_blocks=self.pool_chunk_blocks,
-                warm_format=warm_format,
-            )
-        self.policy_engine = TierKVPolicyEngine(block_size=block_size, block_manager=block_manager)
-        self.layer_states = {layer_idx: LayerRuntimeState() for layer_idx in range(num_layers)}
+        self.tiered_layer_indices = set(range(self.num_layers))
+        self.kv_pool = self._build_pool(warm_format)
+        self.policy_engine = TierKVPolicyEngine(block_size=self.block_size, block_manager=block_manager)
+        self._timer = _StageTimer(os.environ.get("TIERKV_PROFILE", "0") == "1")
+        self.profile_enabled = self._timer.enabled
+        self.profile_totals_ms = self._timer.totals
+        self.profile_counts = self._timer.counts
         self.cache = TieredKVCache(self)
-        self.current_query_length = 0
-        self.decode_step = 0
-        self.policy_tick_this_forward = False
-        self.profile_enabled = os.environ.get("TIERKV_PROFILE", "0") == "1"
-        self.profile_totals_ms: dict[str, float] = {}
-        self.profile_counts: dict[str, int] = {}
+        self._restart()
+
+    def _build_pool(self, warm_format: str):
+        geometry = dict(num_layers=self.num_layers, block_size=self.block_size, max_seq_len=self.max_seq_len,
+                        max_blocks_per_layer=self.max_blocks_per_layer, pool_blocks=self.pool_blocks,
+                        pool_chunk_blocks=self.pool_chunk_blocks, warm_format=warm_format)
+        if self.pool_layout == "dense":
+            return TieredKVTensorPool(**geometry)
+        hot, warm = self._compact_slot_capacities()
+        return CompactTieredKVTensorPool(**geometry, max_hot_slots=self.num_layers * hot,
+                                         max_warm_slots=self.num_layers * warm, hot_chunk_slots=max(1, hot),
+                                         warm_chunk_slots=max(1, warm))
 
     def _compact_slot_capacities(self) -> tuple[int, int]:
-        """tierkv_policy.py:1628-1637."""
+        """Slots per layer of each compact tier (tierkv_policy.py:1628-1637):
+        HOT holds the budget plus the blocks appended between two policy
+        ticks and two spare; WARM the WARM budget plus two (or every block
+        when nothing is evicted)."""
         if self.policy_mode == "hot_only":
             return self.max_blocks_per_layer, 0
-        hot_slack = _ceil_div(self.policy_interval, self.block_size) + 2
-        hot_slots = min(self.max_blocks_per_layer, max(2, self.hot_budget) + hot_slack)
-        if self.policy_mode == "hot_warm_cold":
-            warm_slots = min(self.max_blocks_per_layer, self.warm_budget + 2)
-        else:
-            warm_slots = self.max_blocks_per_layer
-        return max(1, hot_slots), max(0, warm_slots)
+        cap = self.max_blocks_per_layer
+        hot = min(cap, max(2, self.hot_budget) + _ceil_div(self.policy_interval, self.block_size) + 2)
+        warm = min(cap, self.warm_budget + 2) if self.policy_mode == "hot_warm_cold" else cap
+        return max(1, hot), max(0, warm)
 
-    def begin_forward(self, query_length: int) -> None:
-        self.current_query_length = int(query_length)
+    def _restart(self) -> None:
+        self.layer_states = {layer_idx: LayerRuntimeState() for layer_idx in range(self.num_layers)}
+        self.decode_step = 0
+        self.current_query_length = 0
         self.policy_tick_this_forward = False
-        if self.current_query_length == 1:
-            self.decode_step += 1
-            self.policy_tick_this_forward = (self.decode_step % self.policy_interval) == 0
+
+    # -- forward bracket -------------------------------------------------------
+    def begin_forward(self, query_length: int) -> None:
+        """A one-token forward is a decode step; every policy_interval-th
+        decode step is a policy tick (tierkv_policy.py:1639-1644)."""
+        self.current_query_length = int(query_length)
+        decode = self.current_query_length == 1
+        self.decode_step += int(decode)
+        self.policy_tick_this_forward = decode and self.decode_step % self.policy_interval == 0
 
     def finish_forward(self) -> None:
         self.current_query_length = 0
@@ -1794,224 +1694,195 @@ class TieredKVRuntime:
     def reset(self, release_storage: bool = False) -> None:
         for seq_id in range(self.num_layers):
             self.block_manager.free_sequence(seq_id)
-        if release_storage:
-            self.kv_pool.release()
-        else:
-            self.kv_pool.clear()
-        self.layer_states = {layer_idx: LayerRuntimeState() for layer_idx in range(self.num_layers)}
-        self.decode_step = 0
-        self.current_query_length = 0
-        self.policy_tick_this_forward = False
-        self.profile_totals_ms.clear()
-        self.profile_counts.clear()
+        (self.kv_pool.release if release_storage else self.kv_pool.clear)()
+        self._restart()
+        self._timer.clear()
         self.cache.reset()
 
+    # -- profiling ------------------------------------------------------------
     def profile_start(self):
-        if not self.profile_enabled or not torch.cuda.is_available():
-            return None
-        event = torch.cuda.Event(enable_timing=True)
-        event.record()
-        return event
+        return self._timer.start()
 
     def profile_end(self, name: str, start_event) -> None:
-        if start_event is None:
-            return
-        end_event = torch.cuda.Event(enable_timing=True)
-        end_event.record()
-        end_event.synchronize()
-        elapsed = float(start_event.elapsed_time(end_event))
-        self.profile_totals_ms[name] = self.profile_totals_ms.get(name, 0.0) + elapsed
-        self.profile_counts[name] = self.profile_counts.get(name, 0) + 1
+        self._timer.end(name, start_event)
 
     def profile_summary(self) -> dict[str, tuple[float, int, float]]:
-        summary = {}
-        for name, total_ms in self.profile_totals_ms.items():
-            count = self.profile_counts.get(name, 0)
-            summary[name] = (total_ms, count, total_ms / max(count, 1))
-        return summary
+        return self._timer.summary()
 
     def collect_memory_metrics(self) -> dict:
         return self.kv_pool.collect_memory_metrics(self.layer_states)
 
-    def append_tokens(self, layer_idx: int, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
-        return self.append_to_layer(layer_idx, key_states, value_states)
-
+    # -- storing K/V ------------------------------------------------------------
     def _desired_prefill_states(self, num_blocks: int, block_scores: torch.Tensor) -> list[int]:
-        """tierkv_policy.py:1695-1720, ranked by the label kernel."""
-        if self.policy_mode == "hot_only" or num_blocks <= 2:
-            return [HOT_STATE] * int(num_blocks)
-        if block_scores.ndim != 1 or len(block_scores) != int(num_blocks):
+        """Initial tiers of a prompt's blocks (tierkv_policy.py:1695-1720),
+        ranked by the label kernel."""
+        n = int(num_blocks)
+        if self.policy_mode == "hot_only" or n <= 2:
+            return [HOT_STATE] * n
+        if block_scores.ndim != 1 or len(block_scores) != n:
             raise ValueError("block_scores must be a 1D tensor matching prefill block count.")
-        if self.policy_mode == "hot_warm_cold":
-            return _labels(block_scores, [HOT_STATE] * int(num_blocks), self.hot_budget, self.warm_budget,
-                           "hot_warm_cold")
-        return _labels(block_scores, [HOT_STATE] * int(num_blocks), self.hot_budget, 0, "hot_warm",
-                       self.demoted_state)
+        tiered = self.policy_mode == "hot_warm_cold"
+        return _labels(block_scores, [HOT_STATE] * n, self.hot_budget, self.warm_budget if tiered else 0,
+                       self.policy_mode, self.demoted_state)
+
+    def _store_prompt_block(self, physical_idx: int, tier: int, src_k, src_v, start: int, length: int) -> None:
+        pool = self.kv_pool
+        if tier == HOT_STATE:
+            pool._write_hot_range(physical_idx, 0, src_k, src_v, start, length)
+        elif tier == WARM_STATE:
+            pool._write_warm_range(physical_idx, src_k, src_v, start, length)
+        elif tier == COLD_STATE:
+            # A pool that holds nothing yet learns its geometry from the
+            # block's tensors before recording it as evicted.
+            if pool.is_allocated():
+                pool.register_cold_block(physical_idx, length)
+            else:
+                pool._write_hot_range(physical_idx, 0, src_k, src_v, start, length)
+                pool.demote_to_cold(physical_idx)
+        else:
+            raise ValueError(f"Unsupported desired state: {tier}")
 
     def append_prefill_with_policy(self, seq_id: int, key_states: torch.Tensor, value_states: torch.Tensor,
                                    block_scores: torch.Tensor) -> None:
-        """tierkv_policy.py:1722-1766: every block goes straight to its tier
-        (HOT copied, WARM quantized, COLD metadata only); one copy launch and
-        one quantize launch for the whole prompt."""
+        """Store a prompt with each block going straight to its tier
+        (tierkv_policy.py:1722-1766): HOT copied, WARM quantized, COLD
+        metadata only; one copy launch and one quantize launch for the whole
+        prompt.  Decode tokens then start a new block."""
         if key_states.shape[-2] != value_states.shape[-2]:
             raise ValueError("Key and value states must have the same sequence length.")
-        layer_state = self.layer_states[seq_id]
-        if layer_state.num_blocks != 0 or layer_state.open_physical_idx is not None:
+        cursor = self.layer_states[seq_id]
+        if cursor.num_blocks != 0 or cursor.open_physical_idx is not None:
             raise RuntimeError("append_prefill_with_policy expects an empty layer cache.")
-        total_tokens = int(key_states.shape[-2])
-        num_blocks = _ceil_div(total_tokens, self.block_size)
-        if num_blocks > self.max_blocks_per_layer:
+        total = int(key_states.shape[-2])
+        n = _ceil_div(total, self.block_size)
+        if n > self.max_blocks_per_layer:
             raise RuntimeError(f"Layer {seq_id} exceeded max_blocks_per_layer={self.max_blocks_per_layer}.")
-        desired_states = self._desired_prefill_states(num_blocks, block_scores)
+        tiers = self._desired_prefill_states(n, block_scores)
         pool = self.kv_pool
         src_k, src_v = pool._source(key_states, value_states)
         with pool._batch():
-            for logical_idx, desired_state in enumerate(desired_states):
+            for logical_idx, tier in enumerate(tiers):
                 physical_idx = self.block_manager.allocate_block(seq_id)
-                if desired_state != HOT_STATE:
-                    self.block_manager.update_block_state(seq_id, logical_idx, desired_state)
+                if tier != HOT_STATE:
+                    self.block_manager.update_block_state(seq_id, logical_idx, tier)
                 start = logical_idx * self.block_size
-                length = min(start + self.block_size, total_tokens) - start
-                physical_idx = pool._check_physical_idx(physical_idx)
-                if desired_state == HOT_STATE:
-                    pool._write_hot_range(physical_idx, 0, src_k, src_v, start, length)
-                elif desired_state == WARM_STATE:
-                    pool._write_warm_range(physical_idx, src_k, src_v, start, length)
-                elif desired_state == COLD_STATE:
-                    if not pool.is_allocated():
-                        pool._write_hot_range(physical_idx, 0, src_k, src_v, start, length)
-                        pool.demote_to_cold(physical_idx)
-                    else:
-                        pool.register_cold_block(physical_idx, length)
-                else:
-                    raise ValueError(f"Unsupported desired state: {desired_state}")
-                pool.set_block_entry(seq_id, logical_idx, physical_idx, desired_state)
-        layer_state.num_blocks = num_blocks
-        layer_state.open_physical_idx = None
-        layer_state.open_token_count = 0
+                self._store_prompt_block(pool._check_physical_idx(physical_idx), tier, src_k, src_v, start,
+                                         min(self.block_size, total - start))
+                pool.set_block_entry(seq_id, logical_idx, physical_idx, tier)
+        cursor.num_blocks, cursor.open_physical_idx, cursor.open_token_count = n, None, 0
+
+    def _placements(self, seq_id: int, cursor: LayerRuntimeState, tokens: int):
+        """Where ``tokens`` appended tokens go: yields (physical block, its new
+        logical index or None, position in the block, token count), opening
+        a block from the BlockManager whenever none is open."""
+        while tokens > 0:
+            new_logical = None
+            if cursor.open_physical_idx is None:
+                cursor.open_physical_idx = self.block_manager.allocate_block(seq_id)
+                cursor.open_token_count = 0
+                new_logical = cursor.num_blocks
+                if new_logical >= self.max_blocks_per_layer:
+                    raise RuntimeError(f"Layer {seq_id} exceeded max_blocks_per_layer={self.max_blocks_per_layer}.")
+                self.kv_pool._check_physical_idx(cursor.open_physical_idx)
+            take = min(self.block_size - cursor.open_token_count, tokens)
+            yield cursor.open_physical_idx, new_logical, cursor.open_token_count, take
+            tokens -= take
+            cursor.open_token_count += take
+            if cursor.open_token_count == self.block_size:
+                cursor.open_physical_idx, cursor.open_token_count = None, 0
 
     def append_to_layer(self, seq_id: int, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
-        """tierkv_policy.py:1768-1816: fill the open block, then new HOT blocks."""
+        """Append tokens to a layer (tierkv_policy.py:1768-1816): the open
+        block first, then new HOT blocks; a WARM open block is promoted
+        before it takes tokens.  Returns whether a block was allocated."""
         if key_states.shape[-2] != value_states.shape[-2]:
             raise ValueError("Key and value states must have the same sequence length.")
-        layer_state = self.layer_states[seq_id]
-        offset = 0
-        total_tokens = int(key_states.shape[-2])
-        allocated_new_block = False
+        cursor = self.layer_states[seq_id]
         pool = self.kv_pool
         src_k, src_v = pool._source(key_states, value_states)
+        opened = False
+        consumed = 0
         with pool._batch():
-            while offset < total_tokens:
-                new_logical_idx = None
-                if layer_state.open_physical_idx is None:
-                    layer_state.open_physical_idx = self.block_manager.allocate_block(seq_id)
-                    layer_state.open_token_count = 0
-                    allocated_new_block = True
-                    new_logical_idx = layer_state.num_blocks
-                    if new_logical_idx >= self.max_blocks_per_layer:
-                        raise RuntimeError(
-                            f"Layer {seq_id} exceeded max_blocks_per_layer={self.max_blocks_per_layer}."
-                        )
-                    pool._check_physical_idx(layer_state.open_physical_idx)
-                physical_idx = layer_state.open_physical_idx
+            for physical_idx, new_logical, position, take in self._placements(seq_id, cursor,
+                                                                              int(key_states.shape[-2])):
+                opened = opened or new_logical is not None
                 if pool.get_physical_state(physical_idx) == WARM_STATE:
                     pool.promote_to_hot(physical_idx)
-                take = min(self.block_size - layer_state.open_token_count, total_tokens - offset)
-                pool._write_hot_range(physical_idx, layer_state.open_token_count, src_k, src_v, offset, take)
-                if new_logical_idx is not None:
-                    pool.set_block_entry(seq_id, new_logical_idx, physical_idx, HOT_STATE)
-                    layer_state.num_blocks += 1
-                layer_state.open_token_count += take
-                offset += take
-                if layer_state.open_token_count == self.block_size:
-                    layer_state.open_physical_idx = None
-                    layer_state.open_token_count = 0
-        return allocated_new_block
+                pool._write_hot_range(physical_idx, position, src_k, src_v, consumed, take)
+                consumed += take
+                if new_logical is not None:
+                    pool.set_block_entry(seq_id, new_logical, physical_idx, HOT_STATE)
+                    cursor.num_blocks += 1
+        return opened
 
+    def append_tokens(self, layer_idx: int, key_states: torch.Tensor, value_states: torch.Tensor) -> bool:
+        return self.append_to_layer(layer_idx, key_states, value_states)
+
+    # -- reading K/V and tables -------------------------------------------------
     def reconstruct_layer(self, seq_id: int, allow_decode_reconstruct: bool = False):
-        """tierkv_policy.py:1818-1841."""
+        """Dense fp16 K/V of a layer in logical order (tierkv_policy.py:1818-1841)."""
         if self.attention_backend == "triton" and self.current_query_length == 1 and not allow_decode_reconstruct:
             raise RuntimeError("Decode reconstruction is disabled for the Triton TierKV hot path.")
-        physical_indices = self.block_manager.get_physical_indices(seq_id)
+        ids = self.block_manager.get_physical_indices(seq_id)
         states = self.block_manager.get_states(seq_id)
-        if not physical_indices:
-            return None, None, physical_indices, states
-        key_blocks, value_blocks = [], []
-        for physical_idx, state in zip(physical_indices, states):
-            key_block, value_block = self.kv_pool.get_dequantized_block(physical_idx, state)
-            key_blocks.append(key_block)
-            value_blocks.append(value_block)
-        key_states = torch.cat(key_blocks, dim=-2).contiguous()
-        value_states = torch.cat(value_blocks, dim=-2).contiguous()
-        return key_states, value_states, physical_indices, states
+        if not ids:
+            return None, None, ids, states
+        parts = [self.kv_pool.get_dequantized_block(p, s) for p, s in zip(ids, states)]
+        key = torch.cat([k for k, _ in parts], dim=-2).contiguous()
+        value = torch.cat([v for _, v in parts], dim=-2).contiguous()
+        return key, value, ids, states
 
     def sync_gpu_block_tables(self, seq_id: int) -> None:
-        physical_indices = self.block_manager.get_physical_indices(seq_id)
-        states = self.block_manager.get_states(seq_id)
-        self.kv_pool.sync_gpu_block_tables(seq_id, physical_indices, states)
-        self.layer_states[seq_id].num_blocks = len(physical_indices)
+        ids = self.block_manager.get_physical_indices(seq_id)
+        self.kv_pool.sync_gpu_block_tables(seq_id, ids, self.block_manager.get_states(seq_id))
+        self.layer_states[seq_id].num_blocks = len(ids)
 
     def sync_storage_states(self, seq_id: int) -> None:
-        """tierkv_policy.py:1849-1867: every migration of the layer in one
-        batch (one demote launch, one promote launch, one table push)."""
-        physical_indices = self.block_manager.get_physical_indices(seq_id)
-        states = self.block_manager.get_states(seq_id)
+        """Move every block of a layer to the tier the BlockManager now gives
+        it (tierkv_policy.py:1849-1867), all in one batch: one demote launch,
+        one promote launch, one table push."""
         pool = self.kv_pool
+        pairs = zip(self.block_manager.get_physical_indices(seq_id), self.block_manager.get_states(seq_id))
         with pool._batch():
-            for logical_idx, (physical_idx, state) in enumerate(zip(physical_indices, states)):
-                current_state = pool.get_physical_state(physical_idx)
-                if state == HOT_STATE:
-                    if current_state == WARM_STATE:
-                        pool.promote_to_hot(physical_idx)
-                    elif current_state == COLD_STATE:
-                        raise KeyError(f"Physical block {physical_idx} cannot be promoted from COLD to HOT.")
-                elif state == COLD_STATE and current_state != COLD_STATE:
-                    pool.demote_to_cold(physical_idx)
-                elif state == WARM_STATE:
-                    if current_state == HOT_STATE:
-                        pool.demote_to_warm(physical_idx)
-                    elif current_state == COLD_STATE:
-                        raise KeyError(f"Physical block {physical_idx} cannot be promoted from COLD to WARM.")
+            for logical_idx, (physical_idx, state) in enumerate(pairs):
+                pool.retier(physical_idx, state)
                 pool.set_block_state(seq_id, logical_idx, state)
 
     def get_layer_table(self, seq_id: int):
-        block_table, block_states = self.kv_pool.get_layer_table(seq_id)
-        num_blocks = self.layer_states[seq_id].num_blocks
-        return block_table, block_states, self.kv_pool.get_layer_lengths(seq_id), num_blocks
+        table, states = self.kv_pool.get_layer_table(seq_id)
+        return table, states, self.kv_pool.get_layer_lengths(seq_id), self.layer_states[seq_id].num_blocks
+
+    # -- policy ---------------------------------------------------------------
+    def _tiered(self, seq_id: int) -> bool:
+        return seq_id in self.tiered_layer_indices and self.policy_mode != "hot_only"
 
     def should_run_decode_policy(self, seq_id: int, allocated_new_block: bool) -> bool:
-        return (
-            seq_id in self.tiered_layer_indices
-            and self.policy_mode != "hot_only"
-            and self.current_query_length == 1
-            and (self.policy_tick_this_forward or (self.policy_on_new_block and allocated_new_block))
-        )
+        due = self.policy_tick_this_forward or (self.policy_on_new_block and allocated_new_block)
+        return self._tiered(seq_id) and self.current_query_length == 1 and bool(due)
 
     def should_collect_decode_scores(self, seq_id: int, run_policy: bool) -> bool:
-        if seq_id not in self.tiered_layer_indices or self.policy_mode == "hot_only":
-            return False
-        return bool(run_policy or self.score_accumulation_mode == "every_step")
+        return self._tiered(seq_id) and bool(run_policy or self.score_accumulation_mode == "every_step")
 
     def enforce_policy(self, seq_id: int, block_scores: torch.Tensor) -> None:
-        if self.policy_mode == "hot_only":
-            return
         if self.policy_mode == "hot_warm_cold":
             self.policy_engine.enforce_tiered_budget(seq_id, block_scores, self.hot_budget, self.warm_budget)
-            return
-        self.policy_engine.enforce_budget(seq_id, block_scores, self.hot_budget, demoted_state=self.demoted_state)
+        elif self.policy_mode == "hot_warm":
+            self.policy_engine.enforce_budget(seq_id, block_scores, self.hot_budget, demoted_state=self.demoted_state)
 
     def block_scores_from_probability_sums(self, seq_id: int, score_sums: torch.Tensor) -> torch.Tensor:
-        """tierkv_policy.py:1905-1912 in the block-score kernel."""
-        num_blocks = self.layer_states[seq_id].num_blocks
-        if num_blocks == 0:
+        """Per-block probability mass averaged over heads and divided by the
+        block's token count (tierkv_policy.py:1905-1912), in the block-score
+        kernel."""
+        n = self.layer_states[seq_id].num_blocks
+        if n == 0:
             return torch.empty(0, device=score_sums.device, dtype=torch.float32)
         _lib.require_gpu_tensor(score_sums, "score_sums")
         lengths = self.kv_pool.get_layer_lengths(seq_id)
         sums = score_sums.to(torch.float32).contiguous()
-        heads, stride = int(sums.shape[0]), int(sums.shape[1])
-        out = torch.empty(num_blocks, dtype=torch.float32, device=sums.device)
-        rc = _lib.lib().tierkv_block_scores_from_sums(_lib.ptr(sums), stride, _lib.ptr(lengths), int(lengths.numel()),
-                                                     _lib.ptr(out), 1, heads, num_blocks, _lib.stream_of(sums.device))
+        out = torch.empty(n, dtype=torch.float32, device=sums.device)
+        rc = _lib.lib().tierkv_block_scores_from_sums(_lib.ptr(sums), int(sums.shape[1]), _lib.ptr(lengths),
+                                                     int(lengths.numel()), _lib.ptr(out), 1, int(sums.shape[0]), n,
+                                                     _lib.stream_of(sums.device))
         _lib.check(rc, "tierkv_block_scores_from_sums")
         return out
 
@@ -2019,36 +1890,6 @@ class TieredKVRuntime:
 # ---------------------------------------------------------------------------
 # Module-level runtime handle (tierkv_policy.py:1915-2044).
 # ---------------------------------------------------------------------------
-
-def initialize_global_tierkv(
-    block_manager,
-    num_layers,
-    block_size=16,
-    hot_budget=3,
-    max_seq_len=2048,
-    attention_backend: str | None = None,
-    policy_interval: int | None = None,
-    pool_chunk_blocks: int = 128,
-    policy_on_new_block: bool = False,
-    score_accumulation_mode: str = "policy_ticks",
-    policy_mode: str = "hot_warm",
-    warm_budget: int = 32,
-    pool_layout: str | None = None,
-    *,
-    warm_format: str = "ref_u8",
-) -> TieredKVCache:
-    global _GLOBAL_TIERKV_RUNTIME
-    if _GLOBAL_TIERKV_RUNTIME is not None:
-        _GLOBAL_TIERKV_RUNTIME.reset(release_storage=True)
-    _GLOBAL_TIERKV_RUNTIME = create_tierkv_runtime(
-        block_manager=block_manager, num_layers=num_layers, block_size=block_size, hot_budget=hot_budget,
-        max_seq_len=max_seq_len, attention_backend=attention_backend, policy_interval=policy_interval,
-        pool_chunk_blocks=pool_chunk_blocks, policy_on_new_block=policy_on_new_block,
-        score_accumulation_mode=score_accumulation_mode, policy_mode=policy_mode, warm_budget=warm_budget,
-        pool_layout=pool_layout, warm_format=warm_format,
-    )
-    return _GLOBAL_TIERKV_RUNTIME.cache
-
 
 def create_tierkv_runtime(
     block_manager,
@@ -2067,38 +1908,60 @@ def create_tierkv_runtime(
     *,
     warm_format: str = "ref_u8",
 ) -> TieredKVRuntime:
-    return TieredKVRuntime(
-        block_manager=block_manager, num_layers=num_layers, block_size=block_size, hot_budget=hot_budget,
-        max_seq_len=max_seq_len, attention_backend=attention_backend, policy_interval=policy_interval,
-        pool_chunk_blocks=pool_chunk_blocks, policy_on_new_block=policy_on_new_block,
-        score_accumulation_mode=score_accumulation_mode, policy_mode=policy_mode, warm_budget=warm_budget,
-        pool_layout=pool_layout, warm_format=warm_format,
-    )
+    options = dict(locals())
+    return TieredKVRuntime(**options)
 
 
-_SUMMED_KEYS = (
-    "hot_blocks", "warm_blocks", "cold_blocks", "hot_tokens", "warm_tokens", "cold_tokens", "active_tokens",
-    "logical_hot_mb", "logical_warm_mb", "logical_warm_meta_mb", "logical_cold_evicted_mb",
-    "logical_dense_equivalent_mb", "logical_resident_mb", "physical_hot_pool_mb", "physical_warm_pool_mb",
-    "physical_warm_meta_mb", "physical_total_kv_mb", "active_pool_blocks", "allocated_pool_blocks",
-    "pool_blocks", "hot_slots_used", "hot_slots_capacity", "warm_slots_used", "warm_slots_capacity",
-)
+def initialize_global_tierkv(
+    block_manager,
+    num_layers,
+    block_size=16,
+    hot_budget=3,
+    max_seq_len=2048,
+    attention_backend: str | None = None,
+    policy_interval: int | None = None,
+    pool_chunk_blocks: int = 128,
+    policy_on_new_block: bool = False,
+    score_accumulation_mode: str = "policy_ticks",
+    policy_mode: str = "hot_warm",
+    warm_budget: int = 32,
+    pool_layout: str | None = None,
+    *,
+    warm_format: str = "ref_u8",
+) -> TieredKVCache:
+    """Replace the process-wide runtime (releasing the previous one's storage)
+    and return its HF cache."""
+    global _GLOBAL_TIERKV_RUNTIME
+    options = dict(locals())
+    reset_global_tierkv()
+    _GLOBAL_TIERKV_RUNTIME = create_tierkv_runtime(**options)
+    return _GLOBAL_TIERKV_RUNTIME.cache
+
+
+# Metrics that add up over runtimes; the ratios are recomputed from the sums
+# (tierkv_policy.py:1985-2032).
+_SUMMED_KEYS = _TOKEN_KEYS + _MB_KEYS[:6] + (
+    "physical_hot_pool_mb", "physical_warm_pool_mb", "physical_warm_meta_mb", "physical_total_kv_mb",
+    "active_pool_blocks", "allocated_pool_blocks", "pool_blocks", "hot_slots_used", "hot_slots_capacity",
+    "warm_slots_used", "warm_slots_capacity")
+
+
+def _ratio(num: float, den: float) -> float:
+    return num / den if den > 0 else 0.0
 
 
 def aggregate_memory_metrics(metrics_list) -> dict:
-    """tierkv_policy.py:1985-2032: sums plus recomputed ratios."""
-    metrics_list = [metrics for metrics in metrics_list if metrics]
-    if not metrics_list:
+    present = [m for m in metrics_list if m]
+    if not present:
         return TieredKVTensorPool().collect_memory_metrics({})
-    out = {key: sum(metrics.get(key, 0) for metrics in metrics_list) for key in _SUMMED_KEYS}
-    resident = float(out.get("logical_resident_mb", 0.0))
-    dense = float(out.get("logical_dense_equivalent_mb", 0.0))
-    out["logical_compression_ratio"] = resident / dense if dense > 0 else 0.0
-    out["logical_compression_x"] = dense / resident if resident > 0 else 0.0
+    out = {key: sum(m.get(key, 0) for m in present) for key in _SUMMED_KEYS}
+    resident = float(out["logical_resident_mb"])
+    dense = float(out["logical_dense_equivalent_mb"])
+    out["logical_compression_ratio"] = _ratio(resident, dense)
+    out["logical_compression_x"] = _ratio(dense, resident)
     out["pool_utilization"] = out["active_pool_blocks"] / max(float(out["allocated_pool_blocks"]), 1.0)
     out["capacity_utilization"] = out["allocated_pool_blocks"] / max(float(out["pool_blocks"]), 1.0)
-    physical_total = float(out.get("physical_total_kv_mb", 0.0))
-    out["physical_compression_x"] = dense / physical_total if physical_total > 0 else 0.0
+    out["physical_compression_x"] = _ratio(dense, float(out["physical_total_kv_mb"]))
     return out
 
 
