@@ -93,6 +93,29 @@ TIERKV_API int32_t tierkv_decode_attention(
     float scaling, int32_t splits_hint,
     void* workspace, int64_t workspace_bytes, void* stream);
 
+/* tierkv_decode_attention without a workspace argument and without any
+ * allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  The scratch is a 16 MiB device
+ * array in the library (one copy per GPU, held until the process ends; its
+ * address is taken and the array zeroed on the first call on each device,
+ * with that device current); launches whose tierkv_decode_workspace_bytes
+ * exceed 16 MiB fail with TIERKV_ERR_WORKSPACE.  Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or
+ * host threads) race, and the out-of-range error word is not reported (use
+ * tierkv_decode_attention for that).  Arguments and results otherwise as
+ * tierkv_decode_attention; the stream must belong to the current device. */
+TIERKV_API int32_t tierkv_decode_attention_noalloc(
+    const void* query, int32_t query_dtype, void* out, float* score_sums,
+    const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
+    int64_t table_stride, const int32_t* seq_num_blocks, int32_t num_blocks,
+    const void* hot_k, const void* hot_v, int64_t hot_slots,
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    int32_t warm_format, int32_t cold_mode,
+    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    float scaling, int32_t splits_hint, void* stream);
+
 /* Workspace bytes tierkv_decode_attention needs for this shape. */
 TIERKV_API int64_t tierkv_decode_workspace_bytes(
     int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t num_blocks,

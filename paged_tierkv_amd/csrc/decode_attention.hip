@@ -36,6 +36,7 @@
 #include <type_traits>
 #include <cfloat>
 #include <cmath>
+#include <mutex>
 
 namespace tierkv {
 
@@ -1578,4 +1579,89 @@ extern "C" int32_t tierkv_decode_attention(
   if (bf16) launch_generic<__hip_bfloat16>(p, warm_format, cz, stream);
   else launch_generic<__half>(p, warm_format, cz, stream);
   return check_launch("decode_generic_kernel");
+}
+
+// --------------------------------------------------------------------------
+// Allocation-free variant: the decode workspace is a file-scope device array
+// (`scratch`), one copy per GPU, held until the process ends.
+// --------------------------------------------------------------------------
+
+namespace tierkv {
+constexpr int64_t STATIC_SCRATCH_BYTES = int64_t(16) << 20;
+constexpr int MAX_DEVICES = 64;
+}  // namespace tierkv
+
+static __device__ __align__(256) uint8_t scratch[tierkv::STATIC_SCRATCH_BYTES];
+
+namespace tierkv {
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};   // device address of `scratch` on each GPU
+
+__global__ void scratch_zero_kernel(uint4* p, int64_t n16) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += int64_t(gridDim.x) * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// The current device's copy of `scratch`.  The first call on a device takes
+// its address (host code never passes the array's name to a kernel) and
+// zeroes it on `stream` (refused under capture); later calls reuse the
+// address.  The arrival
+// counters and the error word must start at zero; every complete decode
+// launch leaves the counters at zero again.
+int32_t device_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(TIERKV_ERR_HIP, "tierkv_decode_attention_noalloc: no usable current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    // The zero fill must run now, not at some later graph replay.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone)
+      return fail(TIERKV_ERR_INVALID, "tierkv_decode_attention_noalloc: the first call on a device must not be "
+                                      "under stream capture (it zeroes the device's scratch array)");
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(TIERKV_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    hipLaunchKernelGGL(scratch_zero_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<uint4*>(ptr),
+                       STATIC_SCRATCH_BYTES / 16);
+    const int32_t rc = check_launch("scratch_zero_kernel");
+    if (rc != TIERKV_OK) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return TIERKV_OK;
+}
+
+}  // namespace
+}  // namespace tierkv
+
+extern "C" int32_t tierkv_decode_attention_noalloc(
+    const void* query, int32_t query_dtype, void* out, float* score_sums,
+    const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
+    int64_t table_stride, const int32_t* seq_num_blocks, int32_t num_blocks,
+    const void* hot_k, const void* hot_v, int64_t hot_slots,
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    int32_t warm_format, int32_t cold_mode,
+    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    float scaling, int32_t splits_hint, void* stream_) {
+  clear_error();
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int64_t need = tierkv_decode_workspace_bytes(batch, num_heads, num_kv_heads, num_blocks, block_size,
+                                                     head_dim, score_sums != nullptr, splits_hint);
+  if (need > STATIC_SCRATCH_BYTES)
+    return fail(TIERKV_ERR_WORKSPACE, "tierkv_decode_attention_noalloc: this launch needs " + std::to_string(need) +
+                                          " bytes of scratch; the allocation-free entry point holds " +
+                                          std::to_string(STATIC_SCRATCH_BYTES) + " (use tierkv_decode_attention)");
+  void* ws = nullptr;
+  const int32_t rc = device_scratch(stream, &ws);
+  if (rc != TIERKV_OK) return rc;
+  return tierkv_decode_attention(query, query_dtype, out, score_sums, block_table, block_states, block_lengths,
+                                 table_stride, seq_num_blocks, num_blocks, hot_k, hot_v, hot_slots, warm_k, warm_v,
+                                 warm_slots, k_scale, k_zero, v_scale, v_zero, warm_format, cold_mode, batch,
+                                 num_heads, num_kv_heads, block_size, head_dim, scaling, splits_hint, ws,
+                                 STATIC_SCRATCH_BYTES, stream_);
 }

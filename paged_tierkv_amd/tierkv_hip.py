@@ -29,7 +29,9 @@ Additive, keyword-only extensions:
 * ``workspace``: a ``DecodeWorkspace`` the caller owns (a fixed one is
   required under HIP graph capture); by default each (device, stream) pair
   has its own implicit workspace, so launches on different streams never
-  share scratch memory.
+  share scratch memory.  ``workspace=NOALLOC`` launches through
+  ``tierkv_decode_attention_noalloc`` (the library's own 16 MiB device array
+  per GPU, no allocation; launches on one GPU must not overlap).
 
 ``score_sums`` are reproducible: the same inputs give the same bits on every
 launch (each block's statistics are staged on their own and reduced in a
@@ -46,6 +48,9 @@ import weakref
 import torch
 
 from . import _lib
+
+NOALLOC = "noalloc"   # workspace= value: the allocation-free entry point
+
 
 class DecodeWorkspace:
     """Device scratch of ``tierkv_decode_attention``: the error word, the
@@ -327,17 +332,22 @@ def _bind(
                                              head_dim, int(return_scores), splits_hint)
     if need < 0:
         raise ValueError("invalid decode geometry.")
-    if workspace is not None:
+    if isinstance(workspace, str):
+        if workspace != NOALLOC:
+            raise ValueError(f"workspace must be a DecodeWorkspace, None or {NOALLOC!r}.")
+        ws = None
+    elif workspace is not None:
         ws = workspace
     elif prepared:
         ws = DecodeWorkspace(device, need, growable=False)
     else:
         ws = stream_workspace(device)
-    if ws.device != device:
-        raise ValueError("the decode workspace lives on another device.")
-    ws.reserve(need)
-    if prepared and ws.growable:
-        raise ValueError("a prepared decode needs a fixed workspace (DecodeWorkspace(..., growable=False)).")
+    if ws is not None:
+        if ws.device != device:
+            raise ValueError("the decode workspace lives on another device.")
+        ws.reserve(need)
+        if prepared and ws.growable:
+            raise ValueError("a prepared decode needs a fixed workspace (DecodeWorkspace(..., growable=False)).")
     args = (
         _lib.ptr(query), _lib.DTYPE_BF16 if query.dtype == torch.bfloat16 else _lib.DTYPE_F16,
         _lib.ptr(out), _lib.ptr(score_sums),
@@ -349,8 +359,9 @@ def _bind(
         _lib.ptr(v_scale), _lib.ptr(v_zero) if fmt == _lib.WARM_REF_U8 else None,
         fmt, _COLD_MODES[cold_mode],
         batch, num_heads, kv_heads, block_size, head_dim,
-        float(scaling), splits_hint,
-        ws.data_ptr(), ws.nbytes)
+        float(scaling), splits_hint)
+    if ws is not None:
+        args += (ws.data_ptr(), ws.nbytes)
     # The tensors whose addresses are bound stay referenced with the arguments.
     keep = (query, out, score_sums, snb, block_table, block_states, block_lengths, hot_k_pool, hot_v_pool,
             warm_k_pool, warm_v_pool, k_scale, k_zero, v_scale, v_zero, ws)
@@ -358,6 +369,10 @@ def _bind(
 
 
 def _launch(lib, args, device, ws) -> None:
+    if ws is None:
+        rc = lib.tierkv_decode_attention_noalloc(*args, _lib.stream_of(device))
+        _lib.check(rc, "tierkv_decode_attention_noalloc")
+        return
     rc = lib.tierkv_decode_attention(*args, _lib.stream_of(device))
     _lib.check(rc, "tierkv_decode_attention")
     if _lib.env_flag("TIERKV_CHECK_ERRORS"):
