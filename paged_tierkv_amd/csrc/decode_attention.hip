@@ -566,6 +566,23 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   constexpr int nw = NW;
   const int lane = tid & 63;
   const int w = tid >> 6;
+  // ---- the first table loads leave before anything that needs a kernel
+  // argument beyond the preloaded ones (whose wait would hold them back).
+  // Long rows: PRE_CHUNKS chunks of nthreads entries; short rows (at most
+  // nthreads blocks, which the host guarantees): one entry per thread.  Past
+  // the row's end the last entry is re-read and ignored, so the loads need
+  // no branch.  The three entries of a block (state, length, slot) are
+  // loaded together.
+  constexpr int NLD = LONG ? PRE_CHUNKS : 1;
+  int st0[NLD], len0[NLD], slot0[NLD];
+#pragma unroll
+  for (int k = 0; k < NLD; ++k) {
+    const int64_t o = int64_t(b) * a_stride + min(k * nthreads + tid, a_num_blocks - 1);
+    st0[k] = a_states[o];
+    len0[k] = a_lengths[o];
+    slot0[k] = a_table[o];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   // Blocks of this sequence: the per-sequence count is loaded together with
   // the first row chunk and applied afterwards.
   const int nb_ld = a_seq_nblocks ? a_seq_nblocks[b] : a_num_blocks;
@@ -595,13 +612,15 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     s_next[1] = 0;
   }
 
-  // ---- query: issued first, converted once the list is built ---------------
+  // ---- query: issued right after the first table loads, converted once the
+  // list is built.  Its address needs kernel arguments beyond the preloaded
+  // ones, so their load overlaps the table loads' round trip.
   const int n = lane & 15;
   const int g = lane >> 4;
   const bool head_ok = n < G;
   const int qh = kvh * G + (head_ok ? n : 0);
   uint4 qraw[D / 32], qraw_h[D / 32];
-  {
+  auto load_query = [&]() {
     const QT* qrow = reinterpret_cast<const QT*>(a_q) + (int64_t(b) * p.num_heads + qh) * D;
     // WARM K permutation: for load il of a WARM K tile, dims 64il + 16g .. +15.
 #pragma unroll
@@ -609,15 +628,15 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       qraw[i] = *reinterpret_cast<const uint4*>(qrow + 64 * (i >> 1) + 16 * g + 8 * (i & 1));
 #pragma unroll
     for (int i = 0; i < D / 32; ++i) qraw_h[i] = *reinterpret_cast<const uint4*>(qrow + 32 * i + 8 * g);
-  }
+  };
 
   // ---- this workgroup's share of the resident blocks ------------------------
   // One pass over the table row.  HOT and WARM blocks are ranked separately in
   // logical order; the workgroup keeps rank % splits == split, HOT entries at
   // list positions [0, nhot) from the front, WARM entries from the back
-  // (position MAX_LIST - 1 - k for the k-th).  The three entries of a block
-  // (state, length, slot) are loaded together.  COLD tokens (zero-logit
-  // mode) are counted per thread and reduced per wave.
+  // (position MAX_LIST - 1 - k for the k-th).  The first pass ranks the
+  // entries loaded at the kernel's start.  COLD tokens (zero-logit mode) are
+  // counted per thread and reduced per wave.
   int nb = a_num_blocks;
   int seen_hot = 0, seen_warm = 0;
   int cold_part = 0;
@@ -646,34 +665,28 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     // is ranked, so a row of up to PRE_CHUNKS * nthreads blocks costs one
     // memory round trip and one barrier (the long-context rows of 2048
     // blocks included); the (chunk, wave) counts are scanned across lanes.
-    for (int c0 = 0; c0 < a_num_blocks; c0 += PRE_CHUNKS * nthreads) {
-      const int nch = uniform(min(PRE_CHUNKS, (a_num_blocks - c0 + nthreads - 1) / nthreads));
-      int st[PRE_CHUNKS], len[PRE_CHUNKS], slot[PRE_CHUNKS];
+    // The first pass is written out before the loop over further passes, so
+    // that no wait at the loop's head holds its loads behind the query's.
+    using Chunks = int[PRE_CHUNKS];
+    auto load_chunks = [&](int c0, Chunks& st, Chunks& len, Chunks& slot) {
+      // Past the row's end the last entry is re-read and ignored: the loads
+      // need no per-lane branch.
   #pragma unroll
       for (int k = 0; k < PRE_CHUNKS; ++k) {
-        st[k] = COLD;
-        len[k] = 0;
-        slot[k] = -1;
-        if (k < nch) {
-          // Past the row's end the last entry is re-read and ignored: the
-          // loads of a chunk need no per-lane branch.
-          const int idx = min(c0 + k * nthreads + tid, a_num_blocks - 1);
-          const int64_t o = int64_t(b) * a_stride + idx;
-          st[k] = a_states[o];
-          len[k] = a_lengths[o];
-          slot[k] = a_table[o];
-        }
+        const int idx = min(c0 + k * nthreads + tid, a_num_blocks - 1);
+        const int64_t o = int64_t(b) * a_stride + idx;
+        st[k] = a_states[o];
+        len[k] = a_lengths[o];
+        slot[k] = a_table[o];
       }
-      __builtin_amdgcn_sched_barrier(0);   // every load in flight before any use
-      if (c0 == 0) nb = uniform(min(max(nb_ld, 0), a_num_blocks));
+    };
+    auto rank_chunks = [&](int c0, Chunks& st, Chunks& len, Chunks& slot) {
       // Class of each entry: 1 HOT, 2 WARM, 0 neither.  It is kept per lane
       // and the ballots are taken again after the barrier, so no lane masks
       // stay live across it.
       int cls[PRE_CHUNKS];
   #pragma unroll
       for (int k = 0; k < PRE_CHUNKS; ++k) {
-        cls[k] = 0;
-        if (k >= nch) continue;
         const bool in_row = c0 + k * nthreads + tid < nb;
         len[k] = min(max(len[k], 0), FBS);
         const bool tiered = st[k] == HOT || st[k] == WARM;
@@ -694,7 +707,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       __syncthreads();
       // Exclusive prefix of the (chunk, wave) counts in logical order: lane j
       // holds count j, a wave-wide scan gives every wave every base.
-      const int nj = nch * nw;
+      constexpr int nj = PRE_CHUNKS * nw;
       const int ch = (lane < nj) ? s_wcnt[0][lane] : 0;
       const int cw = (lane < nj) ? s_wcnt[1][lane] : 0;
       const int ih = wave_inclusive_scan(ch);
@@ -702,7 +715,6 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       const uint64_t below = (1ull << lane) - 1ull;
   #pragma unroll
       for (int k = 0; k < PRE_CHUNKS; ++k) {
-        if (k >= nch) continue;
         const int j = uniform(k * nw + w);
         const int hb = seen_hot + __builtin_amdgcn_readlane(ih - ch, j);
         const int wb = seen_warm + __builtin_amdgcn_readlane(iw - cw, j);
@@ -721,66 +733,63 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       }
       seen_hot += __builtin_amdgcn_readlane(ih, 63);
       seen_warm += __builtin_amdgcn_readlane(iw, 63);
-      if (c0 + PRE_CHUNKS * nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
+    };
+    load_query();
+    __builtin_amdgcn_sched_barrier(0);   // every load in flight before any use
+    nb = uniform(min(max(nb_ld, 0), a_num_blocks));
+    rank_chunks(0, st0, len0, slot0);
+    for (int c0 = PRE_CHUNKS * nthreads; c0 < a_num_blocks; c0 += PRE_CHUNKS * nthreads) {
+      __syncthreads();   // s_wcnt is reused
+      int st[PRE_CHUNKS], len[PRE_CHUNKS], slot[PRE_CHUNKS];
+      load_chunks(c0, st, len, slot);
+      __builtin_amdgcn_sched_barrier(0);
+      rank_chunks(c0, st, len, slot);
     }
   } else {
-    // Short rows: one chunk of nthreads entries per pass (load, classify,
-    // rank); the per-wave counts are summed from LDS.
-    for (int c0 = 0; c0 < a_num_blocks; c0 += nthreads) {
-      const int idx = c0 + tid;
-      int st = COLD, len = 0, slot = -1;
-      if (idx < a_num_blocks) {
-        const int64_t o = int64_t(b) * a_stride + idx;
-        st = a_states[o];
-        len = a_lengths[o];
-        slot = a_table[o];
-        __builtin_amdgcn_sched_barrier(0);   // all three in flight before any use
-      }
-      if (c0 == 0) nb = uniform(min(max(nb_ld, 0), a_num_blocks));
-      len = min(max(len, 0), FBS);
-      bool hot = false, warm = false;
-      if (idx < nb) {
-        if (st == HOT || st == WARM) {
-          const bool slot_ok = uint32_t(slot) < ((st == HOT) ? hot_cap : warm_cap);
-          bad |= (!slot_ok && len > 0) ? 1 : 0;
-          hot = slot_ok && len > 0 && st == HOT;
-          warm = slot_ok && len > 0 && st == WARM;
-        } else if (st == COLD) {
-          cold_part += COLD_ZERO ? len : 0;
-        } else {
-          bad |= 2;
-        }
-        if (SCORES && !hot && !warm) stage_init(idx, st, len);
-      }
-      const uint64_t mh = __ballot(hot);
-      const uint64_t mw = __ballot(warm);
-      if (lane == 0) {
-        s_wcnt[0][w] = __popcll(mh);
-        s_wcnt[1][w] = __popcll(mw);
-      }
-      __syncthreads();
-      int hb = seen_hot, wb = seen_warm;
-#pragma unroll
-      for (int i = 0; i < nw; ++i) {
-        const int ch = s_wcnt[0][i], cw = s_wcnt[1][i];
-        hb += (i < w) ? ch : 0;
-        wb += (i < w) ? cw : 0;
-        seen_hot += ch;
-        seen_warm += cw;
-      }
-      const uint64_t below = (1ull << lane) - 1ull;
-      // .w: the entry's stage index (its list position with list staging,
-      // else its logical block).
-      int q;
-      if (hot && mine(hb + __popcll(mh & below), q)) s_list[q] = make_int4(idx, slot, len, list_stage ? q : idx);
-      if (warm && mine(wb + __popcll(mw & below), q))
-        s_list[MAX_LIST - 1 - q] = make_int4(idx, slot, len, list_stage ? p.stage_cap - 1 - q : idx);
-      if (c0 + nthreads < a_num_blocks) __syncthreads();   // s_wcnt is reused
+    // Short rows: one entry per thread, classified without branches (a
+    // branch would let the compiler sink a table load into it, after the
+    // query loads); the per-wave counts are summed from LDS.
+    const int idx = tid;
+    load_query();
+    __builtin_amdgcn_sched_barrier(0);   // every load in flight before any use
+    nb = uniform(min(max(nb_ld, 0), a_num_blocks));
+    const int st = st0[0];
+    const int len = min(max(len0[0], 0), FBS);
+    const int slot = slot0[0];
+    const bool in_row = idx < nb;
+    const bool tiered = st == HOT || st == WARM;
+    const bool slot_ok = uint32_t(slot) < ((st == HOT) ? hot_cap : warm_cap);
+    const bool use = in_row && tiered && slot_ok && len > 0;
+    const bool hot = use && st == HOT;
+    const bool warm = use && st == WARM;
+    bad |= (in_row && tiered && !slot_ok && len > 0) ? 1 : 0;
+    bad |= (in_row && !tiered && st != COLD) ? 2 : 0;
+    if (COLD_ZERO) cold_part += (in_row && st == COLD) ? len : 0;
+    if (SCORES && in_row && !use) stage_init(idx, st, len);
+    const uint64_t mh = __ballot(hot);
+    const uint64_t mw = __ballot(warm);
+    if (lane == 0) {
+      s_wcnt[0][w] = __popcll(mh);
+      s_wcnt[1][w] = __popcll(mw);
     }
+    __syncthreads();
+    int hb = 0, wb = 0;
+#pragma unroll
+    for (int i = 0; i < nw; ++i) {
+      const int ch = s_wcnt[0][i], cw = s_wcnt[1][i];
+      hb += (i < w) ? ch : 0;
+      wb += (i < w) ? cw : 0;
+      seen_hot += ch;
+      seen_warm += cw;
+    }
+    const uint64_t below = (1ull << lane) - 1ull;
+    // .w: the entry's stage index (its list position with list staging, else
+    // its logical block).
+    int q;
+    if (hot && mine(hb + __popcll(mh & below), q)) s_list[q] = make_int4(idx, slot, len, list_stage ? q : idx);
+    if (warm && mine(wb + __popcll(mw & below), q))
+      s_list[MAX_LIST - 1 - q] = make_int4(idx, slot, len, list_stage ? p.stage_cap - 1 - q : idx);
   }
-  // Bit 1: a resident block with an out-of-range slot (skipped); bit 2: a
-  // state that is none of HOT, WARM, COLD.
-  if (bad) atomicOr(p.ws_err, bad);
   if (COLD_ZERO) {
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) cold_part += __shfl_xor(cold_part, m, 64);
@@ -918,6 +927,12 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       }
     } while (lh[0]);
   }
+
+  // Error word: bit 1, a resident block with an out-of-range slot (skipped);
+  // bit 2, a state that is none of HOT, WARM, COLD.  Reported after the tile
+  // loops so that its pointer's kernel-argument load stays off the list
+  // build's path.
+  if (bad) atomicOr(p.ws_err, bad);
 
   // ---- merge the waves in LDS (one barrier) ----------------------------------
   float l = st.l_part + shfl_xor_f(st.l_part, 16);
