@@ -47,10 +47,14 @@ constexpr int PRE_CHUNKS = 4;      // table-row chunks loaded together by the li
 constexpr int MERGE_UNROLL = 8;    // split partials loaded together by the merge
 constexpr int MAX_LDS_STAGE = 48 * 1024;   // bytes of per-block score statistics kept in LDS
 // Where a score launch stages each block's (max, sum) per head:
-//   STAGE_GLOBAL    workspace [B][H][num_blocks], written per tile (fallback);
-//   STAGE_LDS_BLOCK LDS [G][num_blocks] by logical block (unsplit launches);
+//   STAGE_LDS_BLOCK LDS [G][num_blocks] by logical block (unsplit launches),
+//                   finalised by the workgroup itself;
 //   STAGE_LDS_LIST  LDS [G][stage_cap] by list position, copied to the
-//                   workspace once at the end of the workgroup (split launches).
+//                   workspace [B][H][num_blocks] at the end of the workgroup
+//                   (split launches);
+//   STAGE_GLOBAL    the workspace, written per tile (rows too long for LDS).
+// The workspace stages (resident blocks only) are finalised by
+// finalize_scores_kernel, launched after the decode kernel.
 constexpr int STAGE_GLOBAL = 0;
 constexpr int STAGE_LDS_BLOCK = 1;
 constexpr int STAGE_LDS_LIST = 2;
@@ -122,16 +126,6 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
 }
 __device__ __forceinline__ float load_dev(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// A staged (max, sum) pair as one 8-byte device-coherent access.
-__device__ __forceinline__ void store_dev2(float* p, float2 v) {
-  const uint64_t bits = (uint64_t(__float_as_uint(v.y)) << 32) | __float_as_uint(v.x);
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float2 load_dev2(const float* p) {
-  const uint64_t bits = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float(uint32_t(bits)), __uint_as_float(uint32_t(bits >> 32)));
 }
 
 // --------------------------------------------------------------------------
@@ -334,7 +328,9 @@ __device__ __forceinline__ void softmax_step(const DecodeParams& p, const float*
         const int row = (p.lds_stage == STAGE_LDS_LIST) ? p.stage_cap : p.num_blocks;
         reinterpret_cast<float2*>(s_stage)[(lane & 15) * row + si] = make_float2(bm, bs);
       } else {
-        store_dev2(p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + si) * 2, make_float2(bm, bs));
+        // Workspace stage, read by the finalisation kernel after this launch.
+        *reinterpret_cast<float2*>(p.ws_stage + ((int64_t(b) * p.num_heads + qh) * p.num_blocks + si) * 2) =
+            make_float2(bm, bs);
       }
     }
     const float f = __builtin_amdgcn_exp2f(bmr - ws.m_run);
@@ -535,6 +531,30 @@ __device__ __forceinline__ void wave_combine_ms(float& m, float& s) {
   combine_ms(m, s, xor32_f(m), xor32_f(s));
 }
 
+// Staged statistics of a block that no tile visits: (-inf, -len) for a COLD
+// block whose tokens enter the softmax (zero-logit mode), (-inf, 0) for one
+// that contributes nothing.
+template <bool COLD_ZERO>
+__device__ __forceinline__ float2 stage_blank(int st, int len) {
+  return make_float2(-INFINITY, (COLD_ZERO && st == COLD) ? -float(len) : 0.f);
+}
+
+// Probability sum of a block from its staged (bm, bs) and its head's (M, L)
+// (cold_p: the probability of one zero-logit COLD token).
+__device__ __forceinline__ float block_score(float2 e, float M, float inv_l, float cold_p) {
+  if (e.y < 0.f) return -e.y * cold_p;
+  if (e.x != -INFINITY) return e.y * __builtin_amdgcn_exp2f(e.x - M) * inv_l;
+  return 0.f;
+}
+
+// Score reduction tree of a head's row: `parts` contiguous ranges of
+// ceil(nb / parts) blocks, one wave each (lane l folds blocks lo + l,
+// lo + l + 64, ... in ascending order, then wave_combine_ms), the parts
+// combined in ascending order.  parts = nw / G when the unit's G heads fit
+// in its nw waves, else 1; the decode workgroup and the finalisation kernel
+// both follow it, so score sums do not depend on the launch's split count.
+__host__ __device__ inline int score_parts(int groups, int nw) { return groups <= nw ? nw / groups : 1; }
+
 // The arguments the list build needs first come ahead of the parameter block
 // so that they can be preloaded into scalar registers at wave launch.
 template <int D, int WF, bool SCORES, bool COLD_ZERO, typename QT, int NW, bool LONG>
@@ -591,20 +611,36 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   float* s_stage = (SCORES && stage_mode != STAGE_GLOBAL) ? s_dyn + NW * G * D : nullptr;
   const bool list_stage = SCORES && stage_mode == STAGE_LDS_LIST;
   float* const gstage_unit = p.ws_stage + (int64_t(b) * p.num_heads + int64_t(kvh) * G) * p.num_blocks * 2;
-  // A block that no tile will visit gets an entry too, so the staged
-  // statistics describe every block below the row's count: (-inf, -len) for a
-  // COLD block whose tokens enter the softmax (zero-logit mode), (-inf, 0)
-  // for one that contributes nothing.  In the workspace (split launches) the
-  // split whose index is congruent to the block writes it.
-  auto stage_blank = [&](int st, int len) {
-    return make_float2(-INFINITY, (COLD_ZERO && st == COLD) ? -float(len) : 0.f);
+  // A block that no tile will visit gets an entry too (stage_blank), so the
+  // staged statistics describe every block below the row's count (the
+  // finalisation kernel reads the pairs alone): in LDS (block stage) for
+  // every head as the list build classifies it; in the workspace from the
+  // split that owns the block (split s: blocks [s * own, (s + 1) * own), so
+  // a wave's stores are contiguous).  The list build's first pass records
+  // its owned blanks in blank_bits (8 bits per entry: blank, COLD, length)
+  // and they are written at the end of the workgroup, where the stores do
+  // not hold up the tile loads' waits; later passes (rows beyond
+  // PRE_CHUNKS * nthreads blocks) write theirs at once.
+  const int own = (a_num_blocks + splits - 1) / splits;
+  uint32_t blank_bits = 0;
+  auto store_blank = [&](int idx, int st, int len) {
+    for (int h = 0; h < G; ++h)
+      *reinterpret_cast<float2*>(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2) = stage_blank<COLD_ZERO>(st, len);
   };
-  auto stage_init = [&](int idx, int st, int len) {
+  auto stage_init = [&](int idx, int st, int len, int k, bool first_pass) {
     if (stage_mode == STAGE_LDS_BLOCK) {
-      for (int h = 0; h < G; ++h) reinterpret_cast<float2*>(s_stage)[h * p.num_blocks + idx] = stage_blank(st, len);
-    } else if (stage_mode == STAGE_GLOBAL && idx % splits == split) {
       for (int h = 0; h < G; ++h)
-        store_dev2(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2, stage_blank(st, len));
+        reinterpret_cast<float2*>(s_stage)[h * p.num_blocks + idx] = stage_blank<COLD_ZERO>(st, len);
+    } else if (uint32_t(idx - split * own) < uint32_t(own)) {
+      if (first_pass) blank_bits |= uint32_t(1 | ((st == COLD) ? 2 : 0) | (len << 2)) << (8 * k);
+      else store_blank(idx, st, len);
+    }
+  };
+  auto flush_blanks = [&]() {
+#pragma unroll
+    for (int k = 0; k < NLD; ++k) {
+      const uint32_t e = (blank_bits >> (8 * k)) & 0xffu;
+      if (e & 1u) store_blank(k * nthreads + tid, (e & 2u) ? COLD : HOT, int(e >> 2));
     }
   };
   if (tid == 0) {
@@ -696,7 +732,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         bad |= (in_row && tiered && !slot_ok && len[k] > 0) ? 1 : 0;
         bad |= (in_row && !tiered && st[k] != COLD) ? 2 : 0;
         if (COLD_ZERO) cold_part += (in_row && st[k] == COLD) ? len[k] : 0;
-        if (SCORES && in_row && cls[k] == 0) stage_init(c0 + k * nthreads + tid, st[k], len[k]);
+        if (SCORES && in_row && cls[k] == 0) stage_init(c0 + k * nthreads + tid, st[k], len[k], k, c0 == 0);
         const int nh = __popcll(__ballot(cls[k] == 1));
         const int nwm = __popcll(__ballot(cls[k] == 2));
         if (lane == 0) {
@@ -765,7 +801,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     bad |= (in_row && tiered && !slot_ok && len > 0) ? 1 : 0;
     bad |= (in_row && !tiered && st != COLD) ? 2 : 0;
     if (COLD_ZERO) cold_part += (in_row && st == COLD) ? len : 0;
-    if (SCORES && in_row && !use) stage_init(idx, st, len);
+    if (SCORES && in_row && !use) stage_init(idx, st, len, 0, true);
     const uint64_t mh = __ballot(hot);
     const uint64_t mw = __ballot(warm);
     if (lane == 0) {
@@ -998,12 +1034,11 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // registers for the second pass.
   auto finalize_scores = [&]() {
     const int stride = int(p.table_stride);
-    const int parts = (G <= nw) ? nw / G : 1;
+    const int parts = score_parts(G, nw);
     const int ntask = G * parts;
     const int chunk = (nb + parts - 1) / parts;
     auto entry = [&](int h, int blk) -> float2 {
-      if (stage_mode == STAGE_LDS_BLOCK) return reinterpret_cast<const float2*>(s_stage)[h * p.num_blocks + blk];
-      return load_dev2(gstage_unit + (int64_t(h) * p.num_blocks + blk) * 2);
+      return reinterpret_cast<const float2*>(s_stage)[h * p.num_blocks + blk];
     };
     // U entries per lane per round; the caller picks the smallest U that
     // covers a part in one round (rows up to 64 * U blocks per part).
@@ -1054,13 +1089,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
           for (int u = 0; u < U; ++u) {
             const int blk = c0 + u * 64 + lane;
             if (blk >= hi) continue;
-            float v = 0.f;
-            if (blk < hi_nb) {
-              const float2 e = kept[u];
-              if (e.y < 0.f) v = -e.y * cold_p;
-              else if (e.x != -INFINITY) v = e.y * __builtin_amdgcn_exp2f(e.x - M) * inv_l;
-            }
-            dst[blk] = v;
+            dst[blk] = (blk < hi_nb) ? block_score(kept[u], M, inv_l, cold_p) : 0.f;
           }
         }
       }
@@ -1079,7 +1108,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
       out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
     }
-    if (SCORES) finalize_scores();
+    if (SCORES && stage_mode == STAGE_LDS_BLOCK) finalize_scores();
+    if (SCORES && stage_mode != STAGE_LDS_BLOCK) flush_blanks();
     return;
   }
 
@@ -1095,30 +1125,6 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       store_dev(p.ws_ml + pi * 2 + 1, L);
     }
   }
-  if (list_stage) {
-    // The statistics this workgroup staged in LDS go to the workspace by
-    // logical block, and so do the blocks without a tile that it owns (index
-    // congruent to its split): one round of stores, covered by the wait
-    // before the arrival.
-    const int nlist = nhot + nwarm;
-    for (int i = tid; i < G * nlist; i += nthreads) {
-      const int h = i / nlist;
-      const int j = i - h * nlist;
-      const int4 e = (j < nhot) ? s_list[j] : s_list[MAX_LIST - 1 - (j - nhot)];
-      store_dev2(gstage_unit + (int64_t(h) * p.num_blocks + e.x) * 2,
-                 reinterpret_cast<const float2*>(s_stage)[h * p.stage_cap + e.w]);
-    }
-    for (int idx = split + tid * splits; idx < nb; idx += nthreads * splits) {
-      const int64_t o = int64_t(b) * p.table_stride + idx;
-      const int st = p.states[o];
-      const int len = min(max(p.lengths[o], 0), FBS);
-      const int slot = p.table[o];
-      const bool resident = (st == HOT || st == WARM) && len > 0 &&
-                            uint32_t(slot) < ((st == HOT) ? hot_cap : warm_cap);
-      if (!resident)
-        for (int h = 0; h < G; ++h) store_dev2(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2, stage_blank(st, len));
-    }
-  }
   // Every wave's device-coherent stores complete before the arrival is counted.
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -1128,12 +1134,29 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last ? 1 : 0;
   }
+  // The statistics this workgroup staged in LDS go to the workspace by
+  // logical block, for the finalisation kernel that runs after this launch
+  // (no wait covers these stores; the last workgroup issues them after its
+  // merge, whose loads would otherwise wait behind them).
+  auto flush_stage = [&]() {
+    const int nlist = nhot + nwarm;
+    for (int i = tid; i < G * nlist; i += nthreads) {
+      const int h = i / nlist;
+      const int j = i - h * nlist;
+      const int4 e = (j < nhot) ? s_list[j] : s_list[MAX_LIST - 1 - (j - nhot)];
+      *reinterpret_cast<float2*>(gstage_unit + (int64_t(h) * p.num_blocks + e.x) * 2) =
+          reinterpret_cast<const float2*>(s_stage)[h * p.stage_cap + e.w];
+    }
+  };
   __syncthreads();
-  if (!s_last) return;
+  if (!s_last) {
+    if (list_stage) flush_stage();
+    if (SCORES) flush_blanks();
+    return;
+  }
   // Log-sum-exp merge of the splits' partials (tierkv_triton.py:231-264).
   // Each output element loads every split's (m, l, acc) at once (MERGE_UNROLL
-  // splits per round trip) and merges them in registers; the threads of
-  // dimension 0 keep their head's (M, L) for the scores.
+  // splits per round trip) and merges them in registers.
   for (int i = tid; i < G * D; i += nthreads) {
     const int h = i / D;
     const int d = i - h * D;
@@ -1170,7 +1193,106 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
     out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
   }
-  if (SCORES) finalize_scores();
+  if (list_stage) flush_stage();
+  if (SCORES) flush_blanks();
+}
+
+// --------------------------------------------------------------------------
+// Per-block probability sums of launches whose statistics are staged in the
+// workspace (split launches, rows too long for the LDS stage):
+// tierkv_triton.py:121-145 from the staged (bm, bs) pairs, which the decode
+// launch wrote for every block below each row's count (resident blocks by
+// the split that visited them, the others as stage_blank).  One workgroup of
+// eight waves per (sequence, q head) row: the row's pairs are loaded into
+// LDS by all waves (rows up to FIN_LDS_BLOCKS; longer ones are folded from
+// the workspace), the head's (M, L) is reduced along the score tree
+// (score_parts: one wave per part, as in the decode workgroup's own
+// finalisation, so the sums do not depend on the split count), and every
+// thread writes scores.  COLD tokens (zero-logit mode) are read back from
+// the blanks and added in integers.  The row is written up to the table
+// stride (zeros past the sequence's block count).
+// --------------------------------------------------------------------------
+constexpr int FIN_THREADS = 512;
+constexpr int FIN_LDS_BLOCKS = 4096;
+
+// All arguments fit the preloaded kernel-argument registers, so the row's
+// loads need no kernel-argument fetch; they do not wait for the sequence's
+// block count either (the row is read up to num_blocks).
+template <bool COLD_ZERO>
+__global__ __launch_bounds__(FIN_THREADS) void finalize_scores_kernel(const float* __restrict__ ws_stage,
+                                                                      float* __restrict__ score_sums,
+                                                                      const int32_t* __restrict__ seq_nblocks,
+                                                                      int32_t num_heads, int32_t num_blocks,
+                                                                      int32_t stride, int32_t parts) {
+  extern __shared__ float2 s_row[];   // [num_blocks] when num_blocks <= FIN_LDS_BLOCKS
+  __shared__ float s_pm[MAX_WAVES], s_ps[MAX_WAVES];
+  __shared__ int s_pc[MAX_WAVES];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int b = int(blockIdx.x) / num_heads;
+  const int h = int(blockIdx.x) - b * num_heads;
+  const float2* stage = reinterpret_cast<const float2*>(ws_stage + (int64_t(b) * num_heads + h) * num_blocks * 2);
+  const int nb_ld = seq_nblocks ? seq_nblocks[b] : num_blocks;   // used after the row's loads
+  const bool in_lds = num_blocks <= FIN_LDS_BLOCKS;
+  if (in_lds) {
+    constexpr int K = FIN_LDS_BLOCKS / FIN_THREADS;
+    float2 v[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (k * FIN_THREADS < num_blocks) v[k] = stage[min(k * FIN_THREADS + tid, num_blocks - 1)];
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      if (k * FIN_THREADS + tid < num_blocks) s_row[k * FIN_THREADS + tid] = v[k];
+  }
+  const int nb = min(max(nb_ld, 0), num_blocks);
+  if (in_lds) __syncthreads();
+  auto entry = [&](int blk) -> float2 { return in_lds ? s_row[blk] : stage[blk]; };
+
+  // This wave's part of the tree (waves w >= parts have none).
+  const int chunk = (nb + parts - 1) / parts;
+  const int lo = (w < parts) ? min(w * chunk, nb) : nb;
+  const int hi = min(nb, lo + chunk);
+  float m = -INFINITY, sum = 0.f;
+  int cold = 0;
+  constexpr int U = 8;
+  for (int c0 = lo; c0 < hi; c0 += U * 64) {
+    float2 e[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) e[u] = entry(min(c0 + u * 64 + lane, hi - 1));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + u * 64 + lane < hi) {
+        combine_ms(m, sum, e[u].x, e[u].y);
+        cold += (COLD_ZERO && e[u].y < 0.f) ? int(-e[u].y) : 0;
+      }
+    }
+  }
+  wave_combine_ms(m, sum);
+  if (COLD_ZERO) {
+#pragma unroll
+    for (int k = 32; k >= 1; k >>= 1) cold += __shfl_xor(cold, k, 64);
+  }
+  if (lane == 0 && w < parts) {
+    s_pm[w] = m;
+    s_ps[w] = sum;
+    s_pc[w] = cold;
+  }
+  __syncthreads();
+  float M = -INFINITY, L = 0.f;
+  int cold_total = 0;
+  for (int k = 0; k < parts; ++k) {
+    combine_ms(M, L, s_pm[k], s_ps[k]);
+    cold_total += s_pc[k];
+  }
+  float f;
+  cold_adjust<COLD_ZERO>(M, L, f, float(cold_total));
+  const float inv_l = (L > 0.f) ? 1.f / L : 0.f;
+  const float cold_p = COLD_ZERO ? __builtin_amdgcn_exp2f(-M) * inv_l : 0.f;
+
+  float* dst = score_sums + (int64_t(b) * num_heads + h) * stride;
+  for (int blk = tid; blk < stride; blk += FIN_THREADS)
+    dst[blk] = (blk < nb) ? block_score(entry(blk), M, inv_l, cold_p) : 0.f;
 }
 
 // --------------------------------------------------------------------------
@@ -1541,8 +1663,9 @@ extern "C" int32_t tierkv_decode_attention(
     p.splits = pl.splits;
     p.split_magic = 0;
     // Unsplit score launches keep the per-block statistics in LDS (up to
-    // MAX_LDS_STAGE bytes per workgroup); split ones share them through the
-    // workspace, since the last workgroup of a unit finalises every block.
+    // MAX_LDS_STAGE bytes per workgroup) and finalise them in the workgroup;
+    // split ones stage them in LDS by list position and copy them to the
+    // workspace, where finalize_scores_kernel reads them.
     p.lds_stage = STAGE_GLOBAL;
     p.stage_cap = 0;
     if (scores) {
@@ -1588,7 +1711,21 @@ extern "C" int32_t tierkv_decode_attention(
       if (bf16) dispatch_fast<__hip_bfloat16>(pc, warm_format, scores, cz, pl.nw, grid, stream);
       else dispatch_fast<__half>(pc, warm_format, scores, cz, pl.nw, grid, stream);
     }
-    return check_launch("tiered_decode_kernel");
+    const int32_t rc = check_launch("tiered_decode_kernel");
+    if (rc != TIERKV_OK || !scores || p.lds_stage == STAGE_LDS_BLOCK) return rc;
+    // One workgroup per (sequence, q head) row.
+    const int parts = score_parts(p.groups, pl.nw);
+    const int64_t rows = int64_t(batch) * num_heads;
+    if (rows > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
+    const size_t lds = num_blocks <= FIN_LDS_BLOCKS ? size_t(num_blocks) * sizeof(float2) : 0;
+    const int32_t stride32 = int32_t(table_stride);
+    if (cz)
+      hipLaunchKernelGGL((finalize_scores_kernel<true>), dim3(unsigned(rows)), dim3(FIN_THREADS), lds, stream,
+                         p.ws_stage, score_sums, seq_num_blocks, num_heads, num_blocks, stride32, parts);
+    else
+      hipLaunchKernelGGL((finalize_scores_kernel<false>), dim3(unsigned(rows)), dim3(FIN_THREADS), lds, stream,
+                         p.ws_stage, score_sums, seq_num_blocks, num_heads, num_blocks, stride32, parts);
+    return check_launch("finalize_scores_kernel");
   }
   p.splits = 1;
   if (bf16) launch_generic<__hip_bfloat16>(p, warm_format, cz, stream);
