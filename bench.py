@@ -967,6 +967,26 @@ def run_decode(args, device):
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) / 1e3 / args.steps
     assert workspace_error_word(device) == 0, "kernel flagged an out-of-range slot"
+    ratio = None
+    if scores:
+        # The reference's only published kernel-level figure: no-score over
+        # score latency of the decode launch, 0.73-0.86 on an A10G
+        # (main.py:3410-3412).  The same layers without scores, timed the
+        # same way right after (clocks already steady).
+        plain = [PreparedDecode(**L["args"], return_scores=False, cold_mode=args.cold, splits=args.splits or None)
+                 for L in layers]
+        for i in range(max(args.warmup, len(plain))):
+            plain[i % len(plain)].launch()
+        f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        f0.record()
+        for i in range(args.steps):
+            plain[i % len(plain)].launch()
+        f1.record()
+        torch.cuda.synchronize()
+        sec0 = f0.elapsed_time(f1) / 1e3 / args.steps
+        ratio = {"no_score_us_per_layer_step": round(sec0 * 1e6, 3), "score_us_per_layer_step": round(sec * 1e6, 3),
+                 "no_score_over_score": round(sec0 / sec, 4), "reference_a10g": "0.73-0.86"}
+        log(f"[bench] no-score {sec0 * 1e6:.2f} us, score {sec * 1e6:.2f} us: ratio {sec0 / sec:.3f}")
     gbs = nbytes / sec / 1e9
     log(f"[bench] measured ceilings: gather {ceil['gather_4k_tiles_GBps']} GB/s, stream read "
         f"{ceil['stream_read_grid4096_GBps']} GB/s")
@@ -1023,6 +1043,8 @@ def run_decode(args, device):
         "measured_ceiling": measured_ceiling,
         "cpu_baseline": cpu,
     }
+    if ratio is not None:
+        line["score_path"] = ratio
     print(json.dumps(line), flush=True)
 
 

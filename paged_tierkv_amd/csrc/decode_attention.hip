@@ -627,13 +627,20 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     for (int h = 0; h < G; ++h)
       *reinterpret_cast<float2*>(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2) = stage_blank<COLD_ZERO>(st, len);
   };
-  auto stage_init = [&](int idx, int st, int len, int k, bool first_pass) {
+  // blank: the entry is below the row's count and has no tile.  The stage
+  // mode and the pass are uniform; the first pass's bookkeeping is
+  // branch-free.
+  auto stage_init = [&](bool blank, int idx, int st, int len, int k, bool first_pass) {
     if (stage_mode == STAGE_LDS_BLOCK) {
-      for (int h = 0; h < G; ++h)
-        reinterpret_cast<float2*>(s_stage)[h * p.num_blocks + idx] = stage_blank<COLD_ZERO>(st, len);
-    } else if (uint32_t(idx - split * own) < uint32_t(own)) {
-      if (first_pass) blank_bits |= uint32_t(1 | ((st == COLD) ? 2 : 0) | (len << 2)) << (8 * k);
-      else store_blank(idx, st, len);
+      if (blank)
+        for (int h = 0; h < G; ++h)
+          reinterpret_cast<float2*>(s_stage)[h * p.num_blocks + idx] = stage_blank<COLD_ZERO>(st, len);
+    } else {
+      const bool mine_blank = blank && uint32_t(idx - split * own) < uint32_t(own);
+      if (first_pass)
+        blank_bits |= mine_blank ? uint32_t(1 | ((st == COLD) ? 2 : 0) | (len << 2)) << (8 * k) : 0u;
+      else if (mine_blank)
+        store_blank(idx, st, len);
     }
   };
   auto flush_blanks = [&]() {
@@ -732,7 +739,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         bad |= (in_row && tiered && !slot_ok && len[k] > 0) ? 1 : 0;
         bad |= (in_row && !tiered && st[k] != COLD) ? 2 : 0;
         if (COLD_ZERO) cold_part += (in_row && st[k] == COLD) ? len[k] : 0;
-        if (SCORES && in_row && cls[k] == 0) stage_init(c0 + k * nthreads + tid, st[k], len[k], k, c0 == 0);
+        if (SCORES) stage_init(in_row && cls[k] == 0, c0 + k * nthreads + tid, st[k], len[k], k, c0 == 0);
         const int nh = __popcll(__ballot(cls[k] == 1));
         const int nwm = __popcll(__ballot(cls[k] == 2));
         if (lane == 0) {
@@ -801,7 +808,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     bad |= (in_row && tiered && !slot_ok && len > 0) ? 1 : 0;
     bad |= (in_row && !tiered && st != COLD) ? 2 : 0;
     if (COLD_ZERO) cold_part += (in_row && st == COLD) ? len : 0;
-    if (SCORES && in_row && !use) stage_init(idx, st, len, 0, true);
+    if (SCORES) stage_init(in_row && !use, idx, st, len, 0, true);
     const uint64_t mh = __ballot(hot);
     const uint64_t mw = __ballot(warm);
     if (lane == 0) {
