@@ -187,9 +187,9 @@ TIERKV_API int32_t tierkv_write_hot_tokens_inline(
 
 /* Batched runtime (one layer of B sequences whose tables live on the device).
  * Free-slot stacks: int32 [capacity] arrays whose first `top` entries are free
- * slots; ctl is int32 [4] = {hot_top, warm_top, error bits, 0}.  Error bits:
- * 1 no free HOT slot, 2 no free WARM slot, 4 a table row is full, 8 a
- * sequence's last block was not HOT. */
+ * slots; ctl is int32 [4] = {hot_top, warm_top, error bits, last append
+ * applied (1) or refused (0)}.  Error bits: 1 no free HOT slot, 2 no free
+ * WARM slot, 4 a table row is full, 8 a sequence's last block was not HOT. */
 
 /* Append `tokens` new tokens per sequence from src_k/src_v [batch, kv_heads,
  * tokens, head_dim] fp16 at the end of each sequence's block list: the open
@@ -201,11 +201,15 @@ TIERKV_API int32_t tierkv_write_hot_tokens_inline(
  * tierkv_policy.py:1764-1766).  seq_num_blocks, open_blocks and the table
  * rows are updated on the device.  All-or-nothing when slots run out.  The
  * per-step part of append_to_layer (tierkv_policy.py:1768-1816) for a batch
- * of sequences, without host involvement. */
+ * of sequences, without host involvement.  blocks_hint: the block count the
+ * caller expects every sequence to hold before the append (the lockstep
+ * count a decode loop tracks), or 0; with it the last blocks' entries are
+ * read together with the counts (one memory round trip less).  Results do
+ * not depend on it. */
 TIERKV_API int32_t tierkv_runtime_append(
     const void* src_k, const void* src_v, int32_t tokens,
     int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
-    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch, int32_t blocks_hint,
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
 
@@ -227,7 +231,7 @@ TIERKV_API int32_t tierkv_runtime_append_rope(
     const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
     const void* cos, const void* sin, int64_t cs_stride_b, int64_t cs_stride_t, int32_t tokens,
     int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
-    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch, int32_t blocks_hint,
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream);
 

@@ -83,7 +83,7 @@ SIGNATURES = {
     "tierkv_runtime_append": (c_int32, [
         _P, _P, c_int32,
         _P, _P, _P, c_int64,
-        _P, _P, c_int32,
+        _P, _P, c_int32, c_int32,
         _P, _P, c_int64, _P, _P,
         c_int32, c_int32, c_int32, _P]),
     "tierkv_runtime_append_rope": (c_int32, [
@@ -92,7 +92,7 @@ SIGNATURES = {
         _P, c_int64, c_int64, c_int64,
         _P, _P, c_int64, c_int64, c_int32,
         _P, _P, _P, c_int64,
-        _P, _P, c_int32,
+        _P, _P, c_int32, c_int32,
         _P, _P, c_int64, _P, _P,
         c_int32, c_int32, c_int32, _P]),
     "tierkv_runtime_tick": (c_int32, [

@@ -43,7 +43,9 @@ HIP_SOURCES = {
                              "-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
-    "runtime.hip": ["-ffp-contract=off"],
+    # The append kernel's leading arguments are preloaded (as the decode
+    # kernel's); the other runtime kernels take a parameter block first.
+    "runtime.hip": ["-ffp-contract=off", "-mllvm", "-amdgpu-kernarg-preload-count=8"],
     # MFMA accumulators in ordinary VGPRs: the logits are consumed by VALU
     # code right away, and accumulators in AGPRs cost a copy per element.
     "prefill_score.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],

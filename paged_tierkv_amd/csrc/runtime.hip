@@ -14,7 +14,7 @@
 //
 // Free stacks: int32 [capacity] arrays whose first `top` entries are free
 // slots; the top counters live in a per-layer control word array
-// ctl = {hot_top, warm_top, error bits, 0}.  Allocation pops from the top in
+// ctl = {hot_top, warm_top, error bits, last append applied}.  Allocation pops from the top in
 // a fixed order (sequence, then logical block), so slot ids are deterministic.
 
 #include <algorithm>
@@ -160,13 +160,9 @@ constexpr int APPEND_MAX_BATCH = 4096;   // sequences per append call (LDS bookk
 // sequence of transformers' apply_rotary_pos_emb:
 //   out = fp16(fp16(x * cos) + fp16(rotate_half(x) * sin)),
 //   rotate_half(x)[d] = -x[d + D/2] (d < D/2), x[d - D/2] (d >= D/2).
-__device__ __forceinline__ uint4 rope8(const __half* row, const __half* cosr, const __half* sinr, int c, int D) {
-  const int C2 = D / 16;                        // chunks per half row
-  const bool lo = c < C2;
-  const uint4 xv = *reinterpret_cast<const uint4*>(row + 8 * c);
-  const uint4 yv = *reinterpret_cast<const uint4*>(row + 8 * (lo ? c + C2 : c - C2));
-  const uint4 cv = *reinterpret_cast<const uint4*>(cosr + 8 * c);
-  const uint4 sv = *reinterpret_cast<const uint4*>(sinr + 8 * c);
+// xv: the chunk, yv: its partner chunk in the other half, cv / sv: cos and
+// sin of the chunk; lo: the chunk lies in the first half.
+__device__ __forceinline__ uint4 rope8_vals(uint4 xv, uint4 yv, uint4 cv, uint4 sv, bool lo) {
   const __half* x = reinterpret_cast<const __half*>(&xv);
   const __half* y = reinterpret_cast<const __half*>(&yv);
   const __half* cs = reinterpret_cast<const __half*>(&cv);
@@ -181,6 +177,25 @@ __device__ __forceinline__ uint4 rope8(const __half* row, const __half* cosr, co
     o[i] = __float2half_rn(p + r);
   }
   return ov;
+}
+
+__device__ __forceinline__ uint4 rope8(const __half* row, const __half* cosr, const __half* sinr, int c, int D) {
+  const int C2 = D / 16;                        // chunks per half row
+  const bool lo = c < C2;
+  return rope8_vals(*reinterpret_cast<const uint4*>(row + 8 * c),
+                    *reinterpret_cast<const uint4*>(row + 8 * (lo ? c + C2 : c - C2)),
+                    *reinterpret_cast<const uint4*>(cosr + 8 * c), *reinterpret_cast<const uint4*>(sinr + 8 * c), lo);
+}
+
+// Source row of an item.  The K / V choice is a select between the two
+// parameter values: indexing the parameter arrays with a per-lane value
+// would read them from the kernel-argument segment with vector loads, a
+// dependent memory round trip per item.
+template <typename P>
+__device__ __forceinline__ const __half* kv_row(const P& a, int kv, int b, int h, int t) {
+  const bool v = kv != 0;
+  return (v ? a.src[1] : a.src[0]) + b * (v ? a.ss_b[1] : a.ss_b[0]) + h * (v ? a.ss_h[1] : a.ss_h[0]) +
+         t * (v ? a.ss_t[1] : a.ss_t[0]);
 }
 
 // K / V item e of an append, e in [0, B * 2 * kv_heads * T * D / 8): eight
@@ -204,32 +219,165 @@ __device__ __forceinline__ KVItem kv_item(int e, int H, int T, int C) {
   return it;
 }
 
-// The 16 bytes item `it` writes into the pool: the source row's elements,
-// rotated for K when the append carries the rotary embedding.
-__device__ __forceinline__ uint4 kv_value(const AppendParams& a, const KVItem& it) {
-  const __half* row = a.src[it.kv] + it.b * a.ss_b[it.kv] + it.h * a.ss_h[it.kv] + it.t * a.ss_t[it.kv];
-  if (a.rope && it.kv == 0)
-    return rope8(row, a.cos + it.b * a.cs_b + it.t * a.cs_t, a.sin + it.b * a.cs_b + it.t * a.cs_t, it.c, a.D);
-  return reinterpret_cast<const uint4*>(row)[it.c];
+// The loads of an item's 16 bytes, issued without using them: the chunk,
+// and with the rotary embedding (ROPE) its partner chunk, cos and sin, for V
+// items too (all in bounds; unused), so that no load sits behind a per-lane
+// branch; kv_finish combines them (K rotated with ROPE).
+struct KVRaw {
+  uint4 x, y, c, s;
+};
+template <bool ROPE>
+__device__ __forceinline__ KVRaw kv_raw(const AppendParams& a, const KVItem& it) {
+  const uint4* row = reinterpret_cast<const uint4*>(kv_row(a, it.kv, it.b, it.h, it.t));
+  KVRaw r;
+  r.x = row[it.c];
+  if constexpr (ROPE) {
+    const int C2 = a.D / 16;
+    r.y = row[it.c < C2 ? it.c + C2 : it.c - C2];
+    r.c = reinterpret_cast<const uint4*>(a.cos + it.b * a.cs_b + it.t * a.cs_t)[it.c];
+    r.s = reinterpret_cast<const uint4*>(a.sin + it.b * a.cs_b + it.t * a.cs_t)[it.c];
+  }
+  return r;
+}
+template <bool ROPE>
+__device__ __forceinline__ uint4 kv_finish(const AppendParams& a, const KVItem& it, const KVRaw& r) {
+  if constexpr (ROPE) return it.kv == 0 ? rope8_vals(r.x, r.y, r.c, r.s, it.c < a.D / 16) : r.x;
+  return r.x;
 }
 
-constexpr int APPEND_PF = 4;                          // K / V items per thread fetched before the bookkeeping
 constexpr int APPEND_NIT = APPEND_MAX_BATCH / RT;     // sequences per thread, at most
 
-// Workgroup 0 does the bookkeeping and the K / V copies: it loads (and
-// rotates) its first APPEND_PF K / V items per thread before the table
-// round trips, since only their destination depends on them, reads each
-// sequence's state once, and keeps the slot of the first block each
-// sequence writes in LDS.  With the rotary embedding, workgroups 1.. rotate
-// the query rows, which depend on nothing else.
-__global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
+// Append bookkeeping (one workgroup): per sequence, the open block (flagged,
+// last, HOT, not full) is filled first, then new HOT blocks popped from the
+// free stack in sequence order; all-or-nothing over the batch.  Writes the
+// table rows, block counts, open flags and the stack top, and ctl[3] = 1
+// when the append was applied (0 when it was refused), which the copy
+// kernel that follows reads.
+// The leading arguments (read-only views of the counts, open flags and
+// table rows, the row stride, the caller's block-count hint and the batch)
+// are preloaded into scalar registers at wave launch, so the first table
+// round trip needs no kernel-argument fetch; `hint` is the block count the
+// caller expects every sequence to hold (0: none).  With it, the entries of
+// the sequences' last blocks are loaded together with their counts, and
+// only a sequence whose count differs takes another round trip.
+__global__ __launch_bounds__(RT) void append_plan_kernel(const int32_t* r_nblocks, const int32_t* r_open,
+                                                         const int32_t* r_lengths, const int32_t* r_states,
+                                                         const int32_t* r_table, int32_t stride32, int32_t hint,
+                                                         int32_t batch, AppendParams a) {
+  __shared__ int sh[RT / 64 + 1];
+  __shared__ int s_ok;
   const int tid = threadIdx.x;
+  const int nit = (batch + RT - 1) / RT;
+  int nb[APPEND_NIT], opn[APPEND_NIT], ln[APPEND_NIT], stt[APPEND_NIT], slot_open[APPEND_NIT];
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    if (it < nit) {
+      const int b = min(it * RT + tid, batch - 1);
+      const int64_t o = int64_t(b) * stride32 + min(max(hint - 1, 0), stride32 - 1);
+      nb[it] = r_nblocks[b];
+      opn[it] = r_open[b];
+      ln[it] = r_lengths[o];
+      stt[it] = r_states[o];
+      slot_open[it] = r_table[o];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int B = batch, bs = a.bs, T = a.T;
+  const int top = a.ctl[0];
+  if (tid == 0) s_ok = 1;
+  int room[APPEND_NIT], len_open[APPEND_NIT], need[APPEND_NIT], excl[APPEND_NIT];
+  // Sequences whose count is not the hint reload their last block's entries.
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    if (it < nit && nb[it] != hint) {
+      const int b = min(it * RT + tid, B - 1);
+      const int64_t o = int64_t(b) * stride32 + min(max(nb[it] - 1, 0), stride32 - 1);
+      ln[it] = r_lengths[o];
+      stt[it] = r_states[o];
+      slot_open[it] = r_table[o];
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    room[it] = len_open[it] = need[it] = excl[it] = 0;
+    const int b = it * RT + tid;
+    if (it < nit && b < B) {
+      if (nb[it] > 0 && nb[it] <= stride32 && opn[it] != 0) {
+        const int len = min(max(ln[it], 0), bs);
+        if (stt[it] != HOT) {
+          if (len < bs) atomicOr(a.ctl + 2, ERR_OPEN_STATE);
+        } else {
+          len_open[it] = len;
+          room[it] = bs - len;
+        }
+      }
+      need[it] = T > room[it] ? (T - room[it] + bs - 1) / bs : 0;
+    }
+  }
+  __syncthreads();
+  int run = 0;
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    if (it < nit) {
+      const int b = it * RT + tid;
+      if (b < B && (nb[it] < 0 || nb[it] + need[it] > stride32)) s_ok = 0;
+      int tot;
+      excl[it] = run + block_scan(need[it], sh, &tot) - need[it];
+      run += tot;
+    }
+  }
+  __syncthreads();
+  if (!s_ok || run > top) {
+    if (tid == 0) {
+      atomicOr(a.ctl + 2, !s_ok ? ERR_TABLE_FULL : ERR_HOT_EMPTY);
+      a.ctl[3] = 0;
+    }
+    return;
+  }
+  // Table entries; new blocks pop the stack in sequence order.
+#pragma unroll
+  for (int it = 0; it < APPEND_NIT; ++it) {
+    const int b = it * RT + tid;
+    if (it < nit && b < B) {
+      const int take_open = min(room[it], T);
+      if (take_open > 0) a.lengths[int64_t(b) * a.stride + nb[it] - 1] = len_open[it] + take_open;
+      for (int j = 0; j < need[it]; ++j) {
+        const int64_t o = int64_t(b) * a.stride + nb[it] + j;
+        a.table[o] = a.hot_free[top - 1 - (excl[it] + j)];
+        a.states[o] = HOT;
+        a.lengths[o] = min(T - take_open - j * bs, bs);
+      }
+      a.nblocks[b] = nb[it] + need[it];
+      const int last_len = need[it] > 0 ? min(T - take_open - (need[it] - 1) * bs, bs) : len_open[it] + take_open;
+      a.open[b] = last_len < bs ? 1 : 0;
+    }
+  }
+  if (tid == 0) {
+    a.ctl[0] = top - run;
+    a.ctl[3] = 1;
+  }
+}
+
+// Append copies (after append_plan_kernel): one 16-byte K / V item per
+// thread, rotated for K with the rotary embedding (ROPE), stored into the
+// HOT pool; workgroups past the K / V items rotate the query rows (ROPE).
+// The destination comes from the rows the plan wrote: an append fills its
+// sequence contiguously (the open block's free rows, then new blocks from
+// row 0), so its T tokens are the last T valid rows of the row list, and
+// token t lies T - 1 - t rows before the end.  Nothing is stored when the
+// plan refused the append (ctl[3] == 0).  The source loads, the status and
+// the block count are issued together; the last block's entries follow.
+// Rows past a block's length are not cleared: pools start zeroed and only
+// ever hold finite fp16 values, and every consumer masks rows by length.
+template <bool ROPE>
+__global__ __launch_bounds__(CT) void append_copy_kernel(AppendParams a, int32_t kv_groups) {
   const int B = a.batch, bs = a.bs, T = a.T;
   const int D = a.D, C = D / 8, H = a.kv_heads;
-  if (blockIdx.x > 0) {
+  if (ROPE && int(blockIdx.x) >= kv_groups) {
     const int per_seq = a.heads * T * C;
     const int total = B * per_seq;
-    for (int e = (blockIdx.x - 1) * RT + tid; e < total; e += (gridDim.x - 1) * RT) {
+    const int nq = int(gridDim.x) - kv_groups;
+    for (int e = (int(blockIdx.x) - kv_groups) * CT + int(threadIdx.x); e < total; e += nq * CT) {
       const int b = e / per_seq;
       int r = e - b * per_seq;
       const int c = r % C;
@@ -243,116 +391,29 @@ __global__ __launch_bounds__(RT) void append_tokens_kernel(AppendParams a) {
     }
     return;
   }
-  __shared__ int sh[RT / 64 + 1];
-  __shared__ int s_ok;
-  __shared__ int s_fb[APPEND_MAX_BATCH];     // first block receiving a token, per sequence
-  __shared__ int s_fp[APPEND_MAX_BATCH];     // row of the first new token in it
-  __shared__ int s_slot[APPEND_MAX_BATCH];   // HOT slot of that block
-  const int top = a.ctl[0];
   const int total_kv = B * 2 * H * T * C;
-  uint4 pf[APPEND_PF];
-#pragma unroll
-  for (int k = 0; k < APPEND_PF; ++k) {
-    const int e = tid + k * RT;
-    if (e < total_kv) pf[k] = kv_value(a, kv_item(e, H, T, C));
+  const int e = int(blockIdx.x) * CT + int(threadIdx.x);
+  if (e >= total_kv) return;
+  const KVItem it = kv_item(e, H, T, C);
+  const KVRaw raw = kv_raw<ROPE>(a, it);
+  const int applied = a.ctl[3];
+  int blk = a.nblocks[it.b] - 1;
+  __builtin_amdgcn_sched_barrier(0);
+  if (!applied || blk < 0) return;
+  // Walk back over the row list to the token's block.
+  int r = T - 1 - it.t;
+  int len = min(max(a.lengths[int64_t(it.b) * a.stride + blk], 0), bs);
+  while (r >= len && blk > 0) {
+    r -= len;
+    --blk;
+    len = min(max(a.lengths[int64_t(it.b) * a.stride + blk], 0), bs);
   }
-  // Phase 1: per sequence, the open block (flagged, last, HOT, not full) and
-  // the new blocks needed; all-or-nothing check over the batch.
-  if (tid == 0) s_ok = 1;
-  int nb[APPEND_NIT], room[APPEND_NIT], len_open[APPEND_NIT], slot_open[APPEND_NIT], need[APPEND_NIT];
-  int excl[APPEND_NIT];
-  const int nit = (B + RT - 1) / RT;
-#pragma unroll
-  for (int it = 0; it < APPEND_NIT; ++it) {
-    nb[it] = room[it] = len_open[it] = need[it] = excl[it] = 0;
-    slot_open[it] = -1;
-    const int b = it * RT + tid;
-    if (it < nit && b < B) {
-      nb[it] = a.nblocks[b];
-      if (nb[it] > 0 && a.open[b] != 0) {
-        const int64_t o = int64_t(b) * a.stride + nb[it] - 1;
-        const int len = min(max(a.lengths[o], 0), bs);
-        if (a.states[o] != HOT) {
-          if (len < bs) atomicOr(a.ctl + 2, ERR_OPEN_STATE);
-        } else {
-          len_open[it] = len;
-          room[it] = bs - len;
-          slot_open[it] = a.table[o];
-        }
-      }
-      need[it] = T > room[it] ? (T - room[it] + bs - 1) / bs : 0;
-    }
-  }
-  __syncthreads();
-  int run = 0;
-#pragma unroll
-  for (int it = 0; it < APPEND_NIT; ++it) {
-    if (it < nit) {
-      const int b = it * RT + tid;
-      if (b < B && (nb[it] < 0 || nb[it] + need[it] > a.stride)) s_ok = 0;
-      int tot;
-      excl[it] = run + block_scan(need[it], sh, &tot) - need[it];
-      run += tot;
-    }
-  }
-  __syncthreads();
-  if (!s_ok) {
-    if (tid == 0) atomicOr(a.ctl + 2, ERR_TABLE_FULL);
-    return;
-  }
-  if (run > top) {
-    if (tid == 0) atomicOr(a.ctl + 2, ERR_HOT_EMPTY);
-    return;
-  }
-  // Phase 2: table entries; new blocks pop the stack in sequence order.
-#pragma unroll
-  for (int it = 0; it < APPEND_NIT; ++it) {
-    const int b = it * RT + tid;
-    if (it < nit && b < B) {
-      const int take_open = min(room[it], T);
-      if (take_open > 0) {
-        a.lengths[int64_t(b) * a.stride + nb[it] - 1] = len_open[it] + take_open;
-        s_fb[b] = nb[it] - 1;
-        s_fp[b] = len_open[it];
-        s_slot[b] = slot_open[it];
-      } else {
-        s_fb[b] = nb[it];
-        s_fp[b] = 0;
-        s_slot[b] = need[it] > 0 ? a.hot_free[top - 1 - excl[it]] : -1;
-      }
-      for (int j = 0; j < need[it]; ++j) {
-        const int64_t o = int64_t(b) * a.stride + nb[it] + j;
-        a.table[o] = a.hot_free[top - 1 - (excl[it] + j)];
-        a.states[o] = HOT;
-        a.lengths[o] = min(T - take_open - j * bs, bs);
-      }
-      a.nblocks[b] = nb[it] + need[it];
-      const int last_len = need[it] > 0 ? min(T - take_open - (need[it] - 1) * bs, bs) : len_open[it] + take_open;
-      a.open[b] = last_len < bs ? 1 : 0;
-    }
-  }
-  __syncthreads();
-  if (tid == 0) a.ctl[0] = top - run;
-  // Phase 3: store the K / V items.  Token t of sequence b lands at row
-  // fp + t counted from row 0 of its first touched block.  Rows past a
-  // block's length are not cleared: pools start zeroed and only ever hold
-  // finite fp16 values, and every consumer masks rows by length.
-  auto store = [&](const KVItem& it, const uint4& v) {
-    const int g = s_fp[it.b] + it.t;
-    const int blk = g / bs;
-    const int64_t slot = blk == 0 ? s_slot[it.b] : a.table[int64_t(it.b) * a.stride + s_fb[it.b] + blk];
-    if (slot < 0 || slot >= a.hot_slots) return;
-    reinterpret_cast<uint4*>(a.hot[it.kv] + ((slot * H + it.h) * int64_t(bs) + g % bs) * D)[it.c] = v;
-  };
-#pragma unroll
-  for (int k = 0; k < APPEND_PF; ++k) {
-    const int e = tid + k * RT;
-    if (e < total_kv) store(kv_item(e, H, T, C), pf[k]);
-  }
-  for (int e = tid + APPEND_PF * RT; e < total_kv; e += RT) {
-    const KVItem it = kv_item(e, H, T, C);
-    store(it, kv_value(a, it));
-  }
+  if (r >= len) return;
+  const int64_t slot = a.table[int64_t(it.b) * a.stride + blk];
+  if (slot < 0 || slot >= a.hot_slots) return;
+  __half* pool = it.kv ? a.hot[1] : a.hot[0];
+  reinterpret_cast<uint4*>(pool + ((slot * H + it.h) * int64_t(bs) + (len - 1 - r)) * D)[it.c] =
+      kv_finish<ROPE>(a, it, raw);
 }
 
 // ---------------------------------------------------------------------------
@@ -744,10 +805,27 @@ extern "C" int32_t tierkv_write_hot_tokens(
   return check_launch("write_hot_kernel");
 }
 
+// The two launches of an append: bookkeeping (one workgroup), then one
+// copy thread per 16-byte K / V item (and q_groups query-rotation
+// workgroups with ROPE).
+template <bool ROPE>
+static int32_t launch_append(const AppendParams& a, const int32_t* nblocks, const int32_t* open,
+                             const int32_t* lengths, const int32_t* states, const int32_t* table, int32_t stride32,
+                             int32_t hint, int32_t batch, int q_groups, hipStream_t stream) {
+  hipLaunchKernelGGL(append_plan_kernel, dim3(1), dim3(RT), 0, stream, nblocks, open, lengths, states, table, stride32,
+                     hint, batch, a);
+  const int32_t rc = check_launch("append_plan_kernel");
+  if (rc != TIERKV_OK) return rc;
+  const int64_t total_kv = int64_t(batch) * 2 * a.kv_heads * a.T * (a.D / 8);
+  const int kv_groups = static_cast<int>((total_kv + CT - 1) / CT);
+  hipLaunchKernelGGL(append_copy_kernel<ROPE>, dim3(kv_groups + q_groups), dim3(CT), 0, stream, a, kv_groups);
+  return check_launch("append_copy_kernel");
+}
+
 extern "C" int32_t tierkv_runtime_append(
     const void* src_k, const void* src_v, int32_t tokens,
     int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
-    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch, int32_t blocks_hint,
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
   clear_error();
@@ -755,6 +833,7 @@ extern "C" int32_t tierkv_runtime_append(
       !hot_k || !hot_v || !hot_free || !ctl)
     return fail(TIERKV_ERR_INVALID, "null pointer");
   if (batch <= 0 || tokens <= 0 || table_stride <= 0) return fail(TIERKV_ERR_INVALID, "empty append");
+  if (table_stride > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "table rows too long");
   if (batch > APPEND_MAX_BATCH) return fail(TIERKV_ERR_UNSUPPORTED, "append supports at most 4096 sequences per call");
   if (int64_t(batch) * 2 * num_kv_heads * tokens * (head_dim / 8) >= (int64_t(1) << 31))
     return fail(TIERKV_ERR_UNSUPPORTED, "append too large for one call");
@@ -787,8 +866,8 @@ extern "C" int32_t tierkv_runtime_append(
   a.kv_heads = num_kv_heads;
   a.bs = block_size;
   a.D = head_dim;
-  hipLaunchKernelGGL(append_tokens_kernel, dim3(1), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
-  return check_launch("append_tokens_kernel");
+  return launch_append<false>(a, seq_num_blocks, open_blocks, block_lengths, block_states, block_table,
+                              int32_t(table_stride), blocks_hint, batch, 0, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t tierkv_runtime_append_rope(
@@ -797,7 +876,7 @@ extern "C" int32_t tierkv_runtime_append_rope(
     const void* v, int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
     const void* cos, const void* sin, int64_t cs_stride_b, int64_t cs_stride_t, int32_t tokens,
     int32_t* block_table, int32_t* block_states, int32_t* block_lengths, int64_t table_stride,
-    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch,
+    int32_t* seq_num_blocks, int32_t* open_blocks, int32_t batch, int32_t blocks_hint,
     void* hot_k, void* hot_v, int64_t hot_slots, int32_t* hot_free, int32_t* ctl,
     int32_t num_kv_heads, int32_t block_size, int32_t head_dim, void* stream) {
   clear_error();
@@ -805,6 +884,7 @@ extern "C" int32_t tierkv_runtime_append_rope(
       !seq_num_blocks || !open_blocks || !hot_k || !hot_v || !hot_free || !ctl)
     return fail(TIERKV_ERR_INVALID, "null pointer");
   if (batch <= 0 || tokens <= 0 || table_stride <= 0 || num_heads <= 0) return fail(TIERKV_ERR_INVALID, "empty append");
+  if (table_stride > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "table rows too long");
   if (batch > APPEND_MAX_BATCH) return fail(TIERKV_ERR_UNSUPPORTED, "append supports at most 4096 sequences per call");
   if (int64_t(batch) * (2 * num_kv_heads + num_heads) * tokens * (head_dim / 8) >= (int64_t(1) << 31))
     return fail(TIERKV_ERR_UNSUPPORTED, "append too large for one call");
@@ -855,11 +935,11 @@ extern "C" int32_t tierkv_runtime_append_rope(
   a.sin = reinterpret_cast<const __half*>(sin);
   a.cs_b = cs_stride_b;
   a.cs_t = cs_stride_t;
-  // Workgroup 0: bookkeeping and K / V; the rest: query rotation.
+  // Copy workgroups past the K / V items rotate the query rows.
   const int64_t q_items = int64_t(batch) * num_heads * tokens * (head_dim / 8);
-  const int q_groups = static_cast<int>(std::min<int64_t>((q_items + RT - 1) / RT, 256));
-  hipLaunchKernelGGL(append_tokens_kernel, dim3(1 + q_groups), dim3(RT), 0, reinterpret_cast<hipStream_t>(stream), a);
-  return check_launch("append_tokens_kernel");
+  const int q_groups = static_cast<int>(std::min<int64_t>((q_items + CT - 1) / CT, 1024));
+  return launch_append<true>(a, seq_num_blocks, open_blocks, block_lengths, block_states, block_table,
+                             int32_t(table_stride), blocks_hint, batch, q_groups, reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t tierkv_runtime_tick(

@@ -111,7 +111,7 @@ class LayerStorage:
     open: torch.Tensor        # [B] 1 while the last block takes further appended tokens
     hot_free: torch.Tensor    # [hot capacity] free-slot stack
     warm_free: torch.Tensor   # [warm capacity]
-    ctl: torch.Tensor         # [4] hot_top, warm_top, error bits, 0
+    ctl: torch.Tensor         # [4] hot_top, warm_top, error bits, last append applied
 
 
 class BatchedTieredKVRuntime:
@@ -392,8 +392,11 @@ class BatchedTieredKVRuntime:
         dev = self.device
         stream = _lib.stream_of(dev)
         tokens = int(key_states.shape[2])
+        # blocks_hint: the lockstep block count before this append (none for
+        # captured steps, whose arguments are fixed at capture).
+        hint = 0 if self.fixed_launch_bound else self._blocks[layer]
         table_args = (_lib.ptr(st.table), _lib.ptr(st.states), _lib.ptr(st.lengths), self.max_blocks,
-                      _lib.ptr(st.nblocks), _lib.ptr(st.open), self.batch,
+                      _lib.ptr(st.nblocks), _lib.ptr(st.open), self.batch, hint,
                       _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), self.hot_slots, _lib.ptr(st.hot_free),
                       _lib.ptr(st.ctl), self.kv_heads, self.block_size, self.head_dim, stream)
         if rope is not None:

@@ -194,7 +194,7 @@ def test_fused_rope_append_is_bit_exact(device):
         _lib.ptr(kx), kx.stride(0), kx.stride(1), kx.stride(2), _lib.ptr(kx), kx.stride(0), kx.stride(1), kx.stride(2),
         _lib.ptr(cos), _lib.ptr(sin), 0, cos.stride(1), 1,
         _lib.ptr(st.table), _lib.ptr(st.states), _lib.ptr(st.lengths), rts[1].max_blocks, _lib.ptr(st.nblocks),
-        _lib.ptr(st.open), B, _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), rts[1].hot_slots, _lib.ptr(st.hot_free),
+        _lib.ptr(st.open), B, 0, _lib.ptr(st.hot_k), _lib.ptr(st.hot_v), rts[1].hot_slots, _lib.ptr(st.hot_free),
         _lib.ptr(st.ctl), kv, bs, D, _lib.stream_of(device))
     _lib.check(rc)
     assert torch.equal(q_rot, q_ref.contiguous())
