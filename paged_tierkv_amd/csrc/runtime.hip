@@ -441,184 +441,194 @@ struct TickParams {
   int32_t max_dem, max_pro;
 };
 
-__global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
-  __shared__ int sh[RT / 64 + 1];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int B = t.batch;
-  // 1. Block scores: mean over heads of the per-block probability sums,
-  //    divided by max(length, 1) (block_scores_from_probability_sums), for
-  //    every (sequence, block) at once; head rows are loaded in batches of 8
-  //    before they are summed.
-  const int64_t NB = int64_t(B) * t.stride;
-  for (int64_t e = tid; e < NB; e += RT) {
-    const int b = static_cast<int>(e / t.stride);
-    const int i = static_cast<int>(e - int64_t(b) * t.stride);
-    const int n = min(max(t.nblocks[b], 0), int(t.stride));
-    if (i >= n) continue;
-    // The same operations, in the same order, as tierkv_block_scores_from_sums.
+// Block scores and tier labels, one workgroup per sequence.
+//   Scores: the mean over heads of the per-block probability sums, divided
+//   by max(length, 1) (block_scores_from_probability_sums), with the same
+//   operations in the same order as tierkv_block_scores_from_sums; a
+//   thread's head values are loaded together (TICK_HEADS per round) before
+//   they are summed in head order.
+//   Labels: reserved HOT {0, n-1}; candidates ranked by score descending
+//   with ties to the lower index (Python's stable sort, as the 64-bit label
+//   keys order them); COLD never leaves COLD.  The row's scores are kept in
+//   LDS (rows up to TICK_LDS_BLOCKS; longer rows read them back from the
+//   scratch), and every thread ranks its candidates against the whole row.
+constexpr int LT = 512;
+constexpr int TICK_HEADS = 32;
+constexpr int TICK_LDS_BLOCKS = 8192;
+__global__ __launch_bounds__(LT) void tick_label_kernel(TickParams t) {
+  extern __shared__ float s_sc[];   // [n] scores when n <= TICK_LDS_BLOCKS
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int n = min(max(t.nblocks[b], 0), int(t.stride));
+  const int64_t ob = int64_t(b) * t.stride;
+  const bool in_lds = n <= TICK_LDS_BLOCKS;
+  for (int i0 = 0; i0 < n; i0 += LT) {
+    const int i = min(i0 + tid, n - 1);
     const float* p = t.score_sums + int64_t(b) * t.heads * t.sums_stride + i;
+    const int len = max(t.lengths[ob + i], 1);
     float acc = 0.f;
-    for (int h0 = 0; h0 < t.heads; h0 += 8) {
-      float v[8];
+    for (int h0 = 0; h0 < t.heads; h0 += TICK_HEADS) {
+      float v[TICK_HEADS];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) v[k] = (h0 + k < t.heads) ? p[int64_t(h0 + k) * t.sums_stride] : 0.f;
+      for (int k = 0; k < TICK_HEADS; ++k) v[k] = p[int64_t(min(h0 + k, t.heads - 1)) * t.sums_stride];
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (int k = 0; k < TICK_HEADS; ++k)
         if (h0 + k < t.heads) acc += v[k];
     }
-    const float sm = __fdiv_rn(acc, float(t.heads));
-    const int len = max(t.lengths[e], 1);
-    t.scores[e] = __fdiv_rn(sm, float(len));
-  }
-  __syncthreads();
-  // 2. Labels, one wave per sequence: reserved HOT {0, n-1}, candidates
-  //    ranked by score descending with ties to the lower index (Python's
-  //    stable sort, as the 64-bit label keys order them), COLD never leaves
-  //    COLD.  The keys of 64 blocks are loaded at once (one per lane) and
-  //    broadcast lane by lane.
-  for (int b = w; b < B; b += RT / 64) {
-    const int n = min(max(t.nblocks[b], 0), int(t.stride));
-    const float* sc = t.scores + int64_t(b) * t.stride;
-    const int64_t ob = int64_t(b) * t.stride;
-    const int extra_hot = max(t.hot_budget - 2, 0);
-    const uint64_t k_first = n > 2 ? label_key(sc[0], 0) : 0;
-    const uint64_t k_last = n > 2 ? label_key(sc[n - 1], n - 1) : 0;
-    for (int i0 = 0; i0 < n; i0 += 64) {
-      const int i = i0 + lane;
-      const bool cand = n > 2 && i > 0 && i < n - 1;
-      const uint64_t ki = cand ? label_key(sc[i], i) : ~uint64_t(0);
-      int rank = 0;
-      for (int j0 = 0; j0 < n; j0 += 64) {
-        const int jj = j0 + lane;
-        const uint64_t kj = jj < n ? label_key(sc[jj], jj) : 0;   // 0 ranks above nothing
-        const int lo = static_cast<int>(static_cast<uint32_t>(kj));
-        const int hi = static_cast<int>(static_cast<uint32_t>(kj >> 32));
-#pragma unroll
-        for (int l = 0; l < 64; ++l) {
-          const uint64_t k = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(hi, l))) << 32) |
-                             static_cast<uint32_t>(__builtin_amdgcn_readlane(lo, l));
-          rank += k > ki ? 1 : 0;
-        }
-      }
-      // blocks 0 and n - 1 are reserved, not candidates
-      rank -= (k_first > ki ? 1 : 0) + (k_last > ki ? 1 : 0);
-      if (i < n) {
-        const int cur = t.states[ob + i];
-        int want;
-        if (!cand) {
-          want = HOT;
-        } else if (rank < extra_hot) {
-          want = HOT;
-        } else if (t.mode == 2) {
-          want = (rank < extra_hot + max(t.warm_budget, 0)) ? WARM : COLD;
-        } else {
-          want = WARM;
-        }
-        if (cur == COLD) want = COLD;
-        t.labels[ob + i] = want;
-      }
+    const float sc = __fdiv_rn(__fdiv_rn(acc, float(t.heads)), float(len));
+    if (i0 + tid < n) {
+      t.scores[ob + i] = sc;
+      if (in_lds) s_sc[i] = sc;
     }
   }
   __syncthreads();
-  // 3. Allocation in (sequence, block) order: pops first from the stacks as
-  //    they stand, pushes of the freed slots afterwards, so no slot is both
-  //    read and written by this tick's data movement.
+  auto score = [&](int j) -> float { return in_lds ? s_sc[j] : t.scores[ob + j]; };
+  const int extra_hot = max(t.hot_budget - 2, 0);
+  const uint64_t k_first = n > 2 ? label_key(score(0), 0) : 0;
+  const uint64_t k_last = n > 2 ? label_key(score(n - 1), n - 1) : 0;
+  for (int i = tid; i < n; i += LT) {
+    const bool cand = n > 2 && i > 0 && i < n - 1;
+    const uint64_t ki = cand ? label_key(score(i), i) : ~uint64_t(0);
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += label_key(score(j), j) > ki ? 1 : 0;
+    // blocks 0 and n - 1 are reserved, not candidates
+    rank -= (k_first > ki ? 1 : 0) + (k_last > ki ? 1 : 0);
+    const int cur = t.states[ob + i];
+    int want;
+    if (!cand) {
+      want = HOT;
+    } else if (rank < extra_hot) {
+      want = HOT;
+    } else if (t.mode == 2) {
+      want = (rank < extra_hot + max(t.warm_budget, 0)) ? WARM : COLD;
+    } else {
+      want = WARM;
+    }
+    if (cur == COLD) want = COLD;
+    t.labels[ob + i] = want;
+  }
+}
+
+// Slot allocation and table rewrite of a tick (one workgroup), after
+// tick_label_kernel.  Allocation in (sequence, block) order: pops first from
+// the stacks as they stand, pushes of the freed slots afterwards, so no slot
+// is both read and written by this tick's data movement.  Two passes over
+// the (sequence, block) cells: job lists, then frees and the table rewrite.
+// With at most TICK_KEPT * RT cells, each thread loads its cells' state,
+// label, slot and length once, in one round trip, for both passes; two
+// 0/1 flags share one block scan (16 bits each: a scan's prefix is at most
+// RT).
+constexpr int TICK_KEPT = 4;
+struct TickCell {
+  int cur, want, slot, len;
+};
+__global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
+  __shared__ int sh[RT / 64 + 1];
+  const int tid = threadIdx.x;
+  const int B = t.batch;
   const int hot_top = t.ctl[0];
   const int warm_top = t.ctl[1];
+  // Cells past the last sequence's count are never live: N bounds them.
+  const int64_t N = int64_t(B - 1) * t.stride + min(max(t.nblocks[B - 1], 0), int(t.stride));
+  auto load_cell = [&](int64_t e) -> TickCell {
+    const int64_t ec = min(e, max(N - 1, int64_t(0)));
+    const int b = int(ec / t.stride);
+    const int i = int(ec - int64_t(b) * t.stride);
+    const int n = t.nblocks[b];
+    TickCell c{t.states[ec], t.labels[ec], t.table[ec], t.lengths[ec]};
+    if (!(e < N && i < min(max(n, 0), int(t.stride)))) c.cur = c.want = COLD;
+    return c;
+  };
+  const bool kept = N <= int64_t(TICK_KEPT) * RT;
+  TickCell cell[TICK_KEPT];
+  if (kept) {
+#pragma unroll
+    for (int k = 0; k < TICK_KEPT; ++k) cell[k] = load_cell(int64_t(k) * RT + tid);
+  }
+
   int dem_run = 0, pro_run = 0;
-  int64_t N = 0;
-  for (int b = 0; b < B; ++b) N = max(N, int64_t(b) * t.stride + min(max(t.nblocks[b], 0), int(t.stride)));
-  for (int64_t e0 = 0; e0 < N; e0 += RT) {
-    const int64_t e = e0 + tid;
-    int d = 0, p = 0;
-    int b = 0, i = 0, cur = COLD, want = COLD;
-    if (e < N) {
-      b = int(e / t.stride);
-      i = int(e % t.stride);
-      const int n = min(max(t.nblocks[b], 0), int(t.stride));
-      if (i < n) {
-        cur = t.states[e];
-        want = t.labels[e];
-        d = (cur == HOT && want == WARM) ? 1 : 0;
-        p = (cur == WARM && want == HOT) ? 1 : 0;
-      }
-    }
-    int dt, pt;
-    const int dk = block_scan(d, sh, &dt) - d + dem_run;
-    const int pk = block_scan(p, sh, &pt) - p + pro_run;
+  auto pass1 = [&](int64_t e, const TickCell& c) {
+    const int d = (c.cur == HOT && c.want == WARM) ? 1 : 0;
+    const int p = (c.cur == WARM && c.want == HOT) ? 1 : 0;
+    int tot;
+    const int inc = block_scan(d | (p << 16), sh, &tot);
+    const int dk = (inc & 0xffff) - d + dem_run;
+    const int pk = (inc >> 16) - p + pro_run;
     if (d) {
       if (dk < warm_top && dk < t.max_dem) {
-        const int slot = t.warm_free[warm_top - 1 - dk];
-        t.dem[dk] = t.table[e];
-        t.dem[t.max_dem + dk] = slot;
-        t.dem[2 * t.max_dem + dk] = t.lengths[e];
+        t.dem[dk] = c.slot;
+        t.dem[t.max_dem + dk] = t.warm_free[warm_top - 1 - dk];
+        t.dem[2 * t.max_dem + dk] = c.len;
       } else {
         atomicOr(t.ctl + 2, ERR_WARM_EMPTY);
       }
     }
     if (p) {
       if (pk < hot_top && pk < t.max_pro) {
-        const int slot = t.hot_free[hot_top - 1 - pk];
-        t.pro[pk] = t.table[e];
-        t.pro[t.max_pro + pk] = slot;
-        t.pro[2 * t.max_pro + pk] = t.lengths[e];
+        t.pro[pk] = c.slot;
+        t.pro[t.max_pro + pk] = t.hot_free[hot_top - 1 - pk];
+        t.pro[2 * t.max_pro + pk] = c.len;
       } else {
         atomicOr(t.ctl + 2, ERR_HOT_EMPTY);
       }
     }
-    dem_run += dt;
-    pro_run += pt;
+    dem_run += tot & 0xffff;
+    pro_run += tot >> 16;
+  };
+  if (kept) {
+#pragma unroll
+    for (int k = 0; k < TICK_KEPT; ++k)
+      if (int64_t(k) * RT < N) pass1(int64_t(k) * RT + tid, cell[k]);
+  } else {
+    for (int64_t e0 = 0; e0 < N; e0 += RT) pass1(e0 + tid, load_cell(e0 + tid));
   }
   const int ndem = min(min(dem_run, warm_top), t.max_dem);
   const int npro = min(min(pro_run, hot_top), t.max_pro);
   __syncthreads();
+
   // Frees and table rewrite (second pass, same order).  A migration that got
   // no slot leaves its block as it was.
   int hf_run = 0, wf_run = 0;
   dem_run = 0;
   pro_run = 0;
-  for (int64_t e0 = 0; e0 < N; e0 += RT) {
-    const int64_t e = e0 + tid;
-    int d = 0, p = 0, fh = 0, fw = 0;
-    int cur = COLD, want = COLD, slot_now = -1;
-    if (e < N) {
-      const int b = int(e / t.stride);
-      const int i = int(e % t.stride);
-      const int n = min(max(t.nblocks[b], 0), int(t.stride));
-      if (i < n) {
-        cur = t.states[e];
-        want = t.labels[e];
-        slot_now = t.table[e];
-        d = (cur == HOT && want == WARM) ? 1 : 0;
-        p = (cur == WARM && want == HOT) ? 1 : 0;
-      }
-    }
-    int dt, pt;
-    const int dk = block_scan(d, sh, &dt) - d + dem_run;
-    const int pk = block_scan(p, sh, &pt) - p + pro_run;
+  auto pass2 = [&](int64_t e, const TickCell& c) {
+    const int d = (c.cur == HOT && c.want == WARM) ? 1 : 0;
+    const int p = (c.cur == WARM && c.want == HOT) ? 1 : 0;
+    int tot;
+    const int inc = block_scan(d | (p << 16), sh, &tot);
+    const int dk = (inc & 0xffff) - d + dem_run;
+    const int pk = (inc >> 16) - p + pro_run;
     const bool d_ok = d && dk < ndem;
     const bool p_ok = p && pk < npro;
-    fh = (d_ok || (cur == HOT && want == COLD)) ? 1 : 0;
-    fw = (p_ok || (cur == WARM && want == COLD)) ? 1 : 0;
-    int fht, fwt;
-    const int fhk = block_scan(fh, sh, &fht) - fh + hf_run;
-    const int fwk = block_scan(fw, sh, &fwt) - fw + wf_run;
-    if (fh) t.hot_free[hot_top - npro + fhk] = slot_now;
-    if (fw) t.warm_free[warm_top - ndem + fwk] = slot_now;
+    const int fh = (d_ok || (c.cur == HOT && c.want == COLD)) ? 1 : 0;
+    const int fw = (p_ok || (c.cur == WARM && c.want == COLD)) ? 1 : 0;
+    int ftot;
+    const int finc = block_scan(fh | (fw << 16), sh, &ftot);
+    const int fhk = (finc & 0xffff) - fh + hf_run;
+    const int fwk = (finc >> 16) - fw + wf_run;
+    if (fh) t.hot_free[hot_top - npro + fhk] = c.slot;
+    if (fw) t.warm_free[warm_top - ndem + fwk] = c.slot;
     if (d_ok) {
       t.table[e] = t.dem[t.max_dem + dk];
       t.states[e] = WARM;
     } else if (p_ok) {
       t.table[e] = t.pro[t.max_pro + pk];
       t.states[e] = HOT;
-    } else if (want == COLD && cur != COLD) {
+    } else if (c.want == COLD && c.cur != COLD) {
       t.table[e] = -1;
       t.states[e] = COLD;
     }
-    dem_run += dt;
-    pro_run += pt;
-    hf_run += fht;
-    wf_run += fwt;
+    dem_run += tot & 0xffff;
+    pro_run += tot >> 16;
+    hf_run += ftot & 0xffff;
+    wf_run += ftot >> 16;
+  };
+  if (kept) {
+#pragma unroll
+    for (int k = 0; k < TICK_KEPT; ++k)
+      if (int64_t(k) * RT < N) pass2(int64_t(k) * RT + tid, cell[k]);
+  } else {
+    for (int64_t e0 = 0; e0 < N; e0 += RT) pass2(e0 + tid, load_cell(e0 + tid));
   }
   __syncthreads();
   if (tid == 0) {
@@ -992,8 +1002,12 @@ extern "C" int32_t tierkv_runtime_tick(
   t.counts = t.pro + 3 * int64_t(max_promotions);
   t.max_dem = max_demotions;
   t.max_pro = max_promotions;
+  const size_t lds = table_stride <= TICK_LDS_BLOCKS ? size_t(table_stride) * sizeof(float) : 0;
+  hipLaunchKernelGGL(tick_label_kernel, dim3(batch), dim3(LT), lds, stream, t);
+  int32_t rc = check_launch("tick_label_kernel");
+  if (rc != TIERKV_OK) return rc;
   hipLaunchKernelGGL(tick_plan_kernel, dim3(1), dim3(RT), 0, stream, t);
-  int32_t rc = check_launch("tick_plan_kernel");
+  rc = check_launch("tick_plan_kernel");
   if (rc != TIERKV_OK) return rc;
 
   QuantJobs q{};
