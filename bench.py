@@ -830,8 +830,9 @@ def run_c5(args, device):
     rt.check_errors()
     metrics = rt.memory_metrics()
     tps = B * steps / sec
-    log(f"[c5] tiered ({mode}): {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step), resident KV "
-        f"{metrics['resident_kv_bytes'] / 2**20:.1f} MiB vs dense {metrics['dense_equivalent_bytes'] / 2**20:.1f} MiB")
+    log(f"[c5] tiered ({mode}): {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step), KV pools "
+        f"{metrics['physical_pool_bytes'] / 2**20:.1f} MiB allocated ({metrics['resident_kv_bytes'] / 2**20:.1f} MiB "
+        f"resident) vs dense {metrics['dense_equivalent_bytes'] / 2**20:.1f} MiB")
     dense = None
     if not args.no_dense_baseline:
         del rt
@@ -867,10 +868,14 @@ def run_c5(args, device):
                    "cold": "masked", "attention": "tiered HIP decode kernel; prefill via the model's SDPA",
                    "decode_steps_as": mode},
         "tiered_eager_steps": eager,
-        "kv_resident_bytes": metrics["resident_kv_bytes"],
-        "kv_dense_equivalent_bytes": metrics["dense_equivalent_bytes"],
-        "kv_compression_x": round(metrics["compression_x"], 3),
+        # Headline memory figure: the HBM the tiered pools hold (allocated,
+        # free slots included) against the dense fp16 cache; the bytes of the
+        # blocks resident at the end beside it.
         "kv_physical_pool_bytes": metrics["physical_pool_bytes"],
+        "kv_dense_equivalent_bytes": metrics["dense_equivalent_bytes"],
+        "kv_physical_compression_x": round(metrics["physical_compression_x"], 3),
+        "kv_resident_bytes": metrics["resident_kv_bytes"],
+        "kv_resident_compression_x": round(metrics["compression_x"], 3),
         "tiers_at_end": {k: metrics[k] for k in ("hot_blocks", "warm_blocks", "cold_blocks")},
         "dense_hf_baseline": dense,
     }

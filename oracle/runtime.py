@@ -20,10 +20,14 @@ Each sequence follows the reference runtime's rules (tierkv_policy.py):
 
 What the reference leaves open -- it serves one sequence with host free
 lists -- is fixed here the way the device runtime fixes it: one pool pair
-per layer shared by the batch, free-slot stacks popped from the top, all
-pops of a tick (in sequence, then block order) before its pushes, a
-migration with no free slot left undone.  The scores' fp32 sum over heads
-is sequential (the device order); ATen's order is not pinned.
+per layer shared by the batch, free-slot stacks popped from the top, and a
+tick's slots reused within it in five steps, each in (sequence, block)
+order: WARM->COLD slots pushed on the WARM stack, demotions popping it,
+demoted and HOT->COLD slots pushed on the HOT stack, promotions popping it,
+promoted blocks' WARM slots pushed last; a migration with no free slot is
+left undone; the demotions' data moves before the promotions'.  The
+scores' fp32 sum over heads is sequential (the device order); ATen's
+order is not pinned.
 """
 
 from __future__ import annotations
@@ -62,7 +66,7 @@ class BatchedRuntimeOracle:
         self.v_scale = np.zeros_like(self.k_scale) if warm_format == "absmax_i8" else np.ones_like(self.k_scale)
         self.hot_free: list[int] = []
         self.warm_free: list[int] = []
-        self.migrations = {"demote": 0, "promote": 0, "evict": 0}
+        self.migrations = {"demote": 0, "promote": 0, "evict": 0, "promote_into_freed": 0}
 
     # -- codec ---------------------------------------------------------------
 
@@ -163,51 +167,56 @@ class BatchedRuntimeOracle:
         scores = np.asarray(scores, np.float32)
         want = tier_labels(scores, self.states[:, :n], hot_budget, warm_budget, mode=self.mode)
         want = np.where(self.states[:, :n] == COLD, COLD, want)
-        dem, pro = [], []
-        for b in range(self.B):
-            for i in range(n):
-                cur, w = int(self.states[b, i]), int(want[b, i])
-                if cur == HOT and w == WARM:
-                    dem.append((b, i))
-                elif cur == WARM and w == HOT:
-                    pro.append((b, i))
-        # Pops from the stacks as they stand (top = end of the list).
-        wtop, htop = len(self.warm_free), len(self.hot_free)
-        ndem, npro = min(len(dem), wtop), min(len(pro), htop)
+        cells = [(b, i) for b in range(self.B) for i in range(n)]
+        cur = {c: int(self.states[c]) for c in cells}
+        want_of = {c: int(want[c]) for c in cells}
+        slot_of = {c: int(self.table[c]) for c in cells}
+        dem = [c for c in cells if cur[c] == HOT and want_of[c] == WARM]
+        pro = [c for c in cells if cur[c] == WARM and want_of[c] == HOT]
+        # 1. WARM -> COLD slots go on the WARM stack (top = end of the list).
+        self.warm_free += [slot_of[c] for c in cells if cur[c] == WARM and want_of[c] == COLD]
+        # 2. Demotions pop the WARM stack.
+        wtop = len(self.warm_free)
+        ndem = min(len(dem), wtop)
         dem_slot = {dem[k]: self.warm_free[wtop - 1 - k] for k in range(ndem)}
-        pro_slot = {pro[k]: self.hot_free[htop - 1 - k] for k in range(npro)}
         self.warm_free = self.warm_free[: wtop - ndem]
+        # 3. Demoted and HOT -> COLD slots go on the HOT stack.
+        hot_before = len(self.hot_free)
+        self.hot_free += [slot_of[c] for c in cells
+                          if c in dem_slot or (cur[c] == HOT and want_of[c] == COLD)]
+        # 4. Promotions pop the HOT stack.
+        htop = len(self.hot_free)
+        npro = min(len(pro), htop)
+        # promotions landing in a slot this tick freed (the stack's top)
+        self.migrations["promote_into_freed"] += min(npro, htop - hot_before)
+        pro_slot = {pro[k]: self.hot_free[htop - 1 - k] for k in range(npro)}
         self.hot_free = self.hot_free[: htop - npro]
-        moves = []
-        for b in range(self.B):
-            for i in range(n):
-                cur, w = int(self.states[b, i]), int(want[b, i])
-                slot = int(self.table[b, i])
-                ln = int(self.lengths[b, i])
-                if (b, i) in dem_slot:
-                    self.hot_free.append(slot)
-                    moves.append(("dem", slot, dem_slot[(b, i)], ln))
-                    self.table[b, i] = dem_slot[(b, i)]
-                    self.states[b, i] = WARM
-                elif (b, i) in pro_slot:
-                    self.warm_free.append(slot)
-                    moves.append(("pro", slot, pro_slot[(b, i)], ln))
-                    self.table[b, i] = pro_slot[(b, i)]
-                    self.states[b, i] = HOT
-                elif w == COLD and cur != COLD:
-                    self.migrations["evict"] += 1
-                    (self.hot_free if cur == HOT else self.warm_free).append(slot)
-                    self.table[b, i] = -1
-                    self.states[b, i] = COLD
+        # 5. Promoted blocks' WARM slots go on the WARM stack.
+        self.warm_free += [slot_of[c] for c in pro[:npro]]
+        moves_dem, moves_pro = [], []
+        for c in cells:
+            ln = int(self.lengths[c])
+            if c in dem_slot:
+                moves_dem.append((slot_of[c], dem_slot[c], ln))
+                self.table[c] = dem_slot[c]
+                self.states[c] = WARM
+            elif c in pro_slot:
+                moves_pro.append((slot_of[c], pro_slot[c], ln))
+                self.table[c] = pro_slot[c]
+                self.states[c] = HOT
+            elif want_of[c] == COLD and cur[c] != COLD:
+                self.migrations["evict"] += 1
+                self.table[c] = -1
+                self.states[c] = COLD
         self.migrations["demote"] += ndem
         self.migrations["promote"] += npro
-        # Data movement after the bookkeeping (sources are never overwritten
-        # within a tick: no slot is both popped and pushed).
-        for kind, src, dst, ln in moves:
-            if kind == "dem":
-                self._quantize_into(dst, self.hot_k[src, :, :ln], self.hot_v[src, :, :ln], ln, pad_tail=False)
-            else:
-                k, v = self._dequantize(src, ln)
-                self.hot_k[dst, :, :ln] = k
-                self.hot_v[dst, :, :ln] = v
+        # Data movement: every demotion reads its HOT slot before any
+        # promotion writes one (a promotion may land in a slot a demotion
+        # freed); no demotion lands in a slot a promotion reads.
+        for src, dst, ln in moves_dem:
+            self._quantize_into(dst, self.hot_k[src, :, :ln], self.hot_v[src, :, :ln], ln, pad_tail=False)
+        for src, dst, ln in moves_pro:
+            k, v = self._dequantize(src, ln)
+            self.hot_k[dst, :, :ln] = k
+            self.hot_v[dst, :, :ln] = v
         return scores, want

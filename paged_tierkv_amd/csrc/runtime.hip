@@ -510,14 +510,24 @@ __global__ __launch_bounds__(LT) void tick_label_kernel(TickParams t) {
 }
 
 // Slot allocation and table rewrite of a tick (one workgroup), after
-// tick_label_kernel.  Allocation in (sequence, block) order: pops first from
-// the stacks as they stand, pushes of the freed slots afterwards, so no slot
-// is both read and written by this tick's data movement.  Two passes over
-// the (sequence, block) cells: job lists, then frees and the table rewrite.
-// With at most TICK_KEPT * RT cells, each thread loads its cells' state,
-// label, slot and length once, in one round trip, for both passes; two
-// 0/1 flags share one block scan (16 bits each: a scan's prefix is at most
-// RT).
+// tick_label_kernel.  Slots freed by the tick are reused within it, in the
+// order the data movement allows (demotions run before promotions):
+//   1. the WARM slots of WARM -> COLD blocks are pushed on the WARM stack;
+//   2. demotions (HOT -> WARM) pop the WARM stack;
+//   3. the HOT slots of demoted and HOT -> COLD blocks are pushed on the
+//      HOT stack;
+//   4. promotions (WARM -> HOT) pop the HOT stack;
+//   5. the WARM slots of promoted blocks are pushed on the WARM stack.
+// Every step goes in (sequence, block) order, so slot ids are
+// deterministic.  A demotion never lands in a slot a promotion still has to
+// read (promoted slots are pushed last) and a promotion may land in a slot a
+// demotion reads (the demotion kernel runs first).  So the pools need the
+// budgets, not twice the HOT budget: between ticks a sequence holds at most
+// its HOT budget plus the blocks appended since, and at most its WARM budget
+// plus its promotions during a tick.  A migration that gets no slot is left
+// undone.  Three passes over the (sequence, block) cells, one block scan of
+// two 0/1 flags each (16 bits per flag: a scan's prefix is at most RT); with
+// at most TICK_KEPT * RT cells each thread loads its cells once.
 constexpr int TICK_KEPT = 4;
 struct TickCell {
   int cur, want, slot, len;
@@ -545,95 +555,100 @@ __global__ __launch_bounds__(RT) void tick_plan_kernel(TickParams t) {
 #pragma unroll
     for (int k = 0; k < TICK_KEPT; ++k) cell[k] = load_cell(int64_t(k) * RT + tid);
   }
+  // One sweep over the cells with a pass body f(e, cell).
+  auto sweep = [&](auto&& f) {
+    if (kept) {
+#pragma unroll
+      for (int k = 0; k < TICK_KEPT; ++k)
+        if (int64_t(k) * RT < N) f(int64_t(k) * RT + tid, cell[k]);
+    } else {
+      for (int64_t e0 = 0; e0 < N; e0 += RT) f(e0 + tid, load_cell(e0 + tid));
+    }
+    __syncthreads();
+  };
+  auto is_dem = [](const TickCell& c) { return (c.cur == HOT && c.want == WARM) ? 1 : 0; };
+  auto is_pro = [](const TickCell& c) { return (c.cur == WARM && c.want == HOT) ? 1 : 0; };
 
-  int dem_run = 0, pro_run = 0;
-  auto pass1 = [&](int64_t e, const TickCell& c) {
-    const int d = (c.cur == HOT && c.want == WARM) ? 1 : 0;
-    const int p = (c.cur == WARM && c.want == HOT) ? 1 : 0;
+  // Pass A: push the WARM slots of WARM -> COLD blocks; count demotions and
+  // promotions.
+  __shared__ int s_np;
+  if (tid == 0) s_np = 0;
+  __syncthreads();
+  int ev_run = 0, d_run = 0;
+  sweep([&](int64_t, const TickCell& c) {
+    const int ew = (c.cur == WARM && c.want == COLD) ? 1 : 0;
     int tot;
-    const int inc = block_scan(d | (p << 16), sh, &tot);
-    const int dk = (inc & 0xffff) - d + dem_run;
-    const int pk = (inc >> 16) - p + pro_run;
+    const int inc = block_scan(ew | (is_dem(c) << 16), sh, &tot);
+    if (ew) t.warm_free[warm_top + ev_run + (inc & 0xffff) - 1] = c.slot;
+    if (is_pro(c)) atomicAdd(&s_np, 1);
+    ev_run += tot & 0xffff;
+    d_run += tot >> 16;
+  });
+  const int np_total = s_np;
+  const int wtop1 = warm_top + ev_run;                      // WARM stack after step 1
+  const int ndem = min(min(d_run, wtop1), t.max_dem);
+
+  // Pass B: demotion jobs (the first ndem demotions pop the WARM stack) and
+  // the pushes of freed HOT slots (demoted or HOT -> COLD blocks): a cell's
+  // push position counts the demoted and the HOT -> COLD cells before it.
+  int dk_run = 0, eh_run = 0;
+  sweep([&](int64_t, const TickCell& c) {
+    const int d = is_dem(c);
+    const int eh = (c.cur == HOT && c.want == COLD) ? 1 : 0;
+    int tot;
+    const int inc = block_scan(d | (eh << 16), sh, &tot);
+    const int dk = (inc & 0xffff) - d + dk_run;
+    const int ehk = (inc >> 16) - eh + eh_run;
     if (d) {
-      if (dk < warm_top && dk < t.max_dem) {
+      if (dk < ndem) {
         t.dem[dk] = c.slot;
-        t.dem[t.max_dem + dk] = t.warm_free[warm_top - 1 - dk];
+        t.dem[t.max_dem + dk] = t.warm_free[wtop1 - 1 - dk];
         t.dem[2 * t.max_dem + dk] = c.len;
       } else {
         atomicOr(t.ctl + 2, ERR_WARM_EMPTY);
       }
     }
-    if (p) {
-      if (pk < hot_top && pk < t.max_pro) {
-        t.pro[pk] = c.slot;
-        t.pro[t.max_pro + pk] = t.hot_free[hot_top - 1 - pk];
-        t.pro[2 * t.max_pro + pk] = c.len;
-      } else {
-        atomicOr(t.ctl + 2, ERR_HOT_EMPTY);
-      }
-    }
-    dem_run += tot & 0xffff;
-    pro_run += tot >> 16;
-  };
-  if (kept) {
-#pragma unroll
-    for (int k = 0; k < TICK_KEPT; ++k)
-      if (int64_t(k) * RT < N) pass1(int64_t(k) * RT + tid, cell[k]);
-  } else {
-    for (int64_t e0 = 0; e0 < N; e0 += RT) pass1(e0 + tid, load_cell(e0 + tid));
-  }
-  const int ndem = min(min(dem_run, warm_top), t.max_dem);
-  const int npro = min(min(pro_run, hot_top), t.max_pro);
-  __syncthreads();
+    if ((d && dk < ndem) || eh) t.hot_free[hot_top + min(dk, ndem) + ehk] = c.slot;
+    dk_run += tot & 0xffff;
+    eh_run += tot >> 16;
+  });
+  const int htop1 = hot_top + ndem + eh_run;                // HOT stack after step 3
+  const int npro = min(min(np_total, htop1), t.max_pro);
 
-  // Frees and table rewrite (second pass, same order).  A migration that got
-  // no slot leaves its block as it was.
-  int hf_run = 0, wf_run = 0;
-  dem_run = 0;
-  pro_run = 0;
-  auto pass2 = [&](int64_t e, const TickCell& c) {
-    const int d = (c.cur == HOT && c.want == WARM) ? 1 : 0;
-    const int p = (c.cur == WARM && c.want == HOT) ? 1 : 0;
+  // Pass C: promotion jobs (the first npro promotions pop the HOT stack),
+  // the pushes of promoted blocks' WARM slots, and the table rewrite.
+  int pk_run = 0, dk2_run = 0;
+  sweep([&](int64_t e, const TickCell& c) {
+    const int d = is_dem(c);
+    const int p = is_pro(c);
     int tot;
-    const int inc = block_scan(d | (p << 16), sh, &tot);
-    const int dk = (inc & 0xffff) - d + dem_run;
-    const int pk = (inc >> 16) - p + pro_run;
+    const int inc = block_scan(p | (d << 16), sh, &tot);
+    const int pk = (inc & 0xffff) - p + pk_run;
+    const int dk = (inc >> 16) - d + dk2_run;
     const bool d_ok = d && dk < ndem;
     const bool p_ok = p && pk < npro;
-    const int fh = (d_ok || (c.cur == HOT && c.want == COLD)) ? 1 : 0;
-    const int fw = (p_ok || (c.cur == WARM && c.want == COLD)) ? 1 : 0;
-    int ftot;
-    const int finc = block_scan(fh | (fw << 16), sh, &ftot);
-    const int fhk = (finc & 0xffff) - fh + hf_run;
-    const int fwk = (finc >> 16) - fw + wf_run;
-    if (fh) t.hot_free[hot_top - npro + fhk] = c.slot;
-    if (fw) t.warm_free[warm_top - ndem + fwk] = c.slot;
-    if (d_ok) {
+    if (p && !p_ok) atomicOr(t.ctl + 2, ERR_HOT_EMPTY);
+    if (p_ok) {
+      const int hs = t.hot_free[htop1 - 1 - pk];
+      t.pro[pk] = c.slot;
+      t.pro[t.max_pro + pk] = hs;
+      t.pro[2 * t.max_pro + pk] = c.len;
+      t.warm_free[wtop1 - ndem + pk] = c.slot;
+      t.table[e] = hs;
+      t.states[e] = HOT;
+    } else if (d_ok) {
       t.table[e] = t.dem[t.max_dem + dk];
       t.states[e] = WARM;
-    } else if (p_ok) {
-      t.table[e] = t.pro[t.max_pro + pk];
-      t.states[e] = HOT;
     } else if (c.want == COLD && c.cur != COLD) {
       t.table[e] = -1;
       t.states[e] = COLD;
     }
-    dem_run += tot & 0xffff;
-    pro_run += tot >> 16;
-    hf_run += ftot & 0xffff;
-    wf_run += ftot >> 16;
-  };
-  if (kept) {
-#pragma unroll
-    for (int k = 0; k < TICK_KEPT; ++k)
-      if (int64_t(k) * RT < N) pass2(int64_t(k) * RT + tid, cell[k]);
-  } else {
-    for (int64_t e0 = 0; e0 < N; e0 += RT) pass2(e0 + tid, load_cell(e0 + tid));
-  }
-  __syncthreads();
+    pk_run += tot & 0xffff;
+    dk2_run += tot >> 16;
+  });
   if (tid == 0) {
-    t.ctl[0] = hot_top - npro + hf_run;
-    t.ctl[1] = warm_top - ndem + wf_run;
+    t.ctl[0] = htop1 - npro;
+    t.ctl[1] = wtop1 - ndem + npro;
     t.counts[0] = ndem;
     t.counts[1] = npro;
   }

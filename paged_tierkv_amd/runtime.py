@@ -161,16 +161,18 @@ class BatchedTieredKVRuntime:
         # "attention" = the prefill block-score kernel.
         self.prefill_scoring = prefill_scoring
         n = self.max_blocks
-        # Capacities per sequence.  HOT: the budget, the blocks appended between
-        # ticks, and room for a tick's promotions before its demotions free
-        # slots.  WARM: the budget plus room for a tick's demotions.
+        # Capacities per sequence, from the budgets: a tick reuses the slots it
+        # frees (demotions take evicted WARM slots, promotions the HOT slots
+        # that demotions free), so HOT holds at most its budget plus the
+        # blocks appended between ticks, and WARM its budget plus a tick's
+        # promotions (blocks still WARM until the promotion has read them).
         hot_max = max(2, budget_blocks(self.hot_fraction, n))
         appended = _ceil_div(self.policy_interval, self.block_size) + 2
-        self.hot_per_seq = min(n, 2 * hot_max + appended)
+        self.hot_per_seq = min(n, hot_max + appended)
         if policy_mode == "hot_warm":
             self.warm_per_seq = n
         else:
-            self.warm_per_seq = min(n, budget_blocks(self.warm_fraction, n) + self.hot_per_seq + 2)
+            self.warm_per_seq = min(n, budget_blocks(self.warm_fraction, n) + hot_max + 2)
         self.hot_slots = self.batch * self.hot_per_seq
         self.warm_slots = max(1, self.batch * self.warm_per_seq)
         self.layers = [self._new_layer() for _ in range(self.num_layers)]
@@ -503,5 +505,8 @@ class BatchedTieredKVRuntime:
             "hot_tokens": hot_tok, "warm_tokens": warm_tok, "cold_tokens": cold_tok,
             "resident_kv_bytes": resident, "dense_equivalent_bytes": dense,
             "compression_x": dense / resident if resident else 0.0,
+            # HBM the pools hold (what the runtime allocates, free slots
+            # included) against the dense fp16 cache of the same tokens.
             "physical_pool_bytes": physical,
+            "physical_compression_x": dense / physical if physical else 0.0,
         }

@@ -108,8 +108,11 @@ def test_batched_runtime_matches_model(device, warm_format, policy_mode, cold_mo
         torch.cuda.synchronize()
         _compare(rt, orc, f"step {step}{' (tick)' if tick else ''}")
     rt.check_errors()
-    # The ticks did move blocks between tiers (the comparison above is not vacuous).
+    # The ticks did move blocks between tiers (the comparison above is not
+    # vacuous), and promotions landed in HOT slots their own tick freed (the
+    # demotion data moves first).
     assert orc.migrations["demote"] > 0 and orc.migrations["promote"] > 0, orc.migrations
+    assert orc.migrations["promote_into_freed"] > 0, orc.migrations
     if policy_mode == "hot_warm_cold":
         assert orc.migrations["evict"] > 0, orc.migrations
     m = rt.memory_metrics()
