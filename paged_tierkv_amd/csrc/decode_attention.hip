@@ -562,7 +562,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     const int32_t* __restrict__ a_table, const int32_t* __restrict__ a_states,
     const int32_t* __restrict__ a_lengths, const void* __restrict__ a_q,
     const int32_t* __restrict__ a_seq_nblocks, int32_t a_stride, int32_t a_num_blocks,
-    int32_t a_kv_heads, int32_t a_splits, DecodeParams p) {
+    int32_t a_kvh_splits, uint32_t a_split_magic, DecodeParams p) {
   constexpr int DS = D / 16;
   extern __shared__ float s_dyn[];               // [NW][G][D] wave accumulators, then the LDS stage
   __shared__ int4 s_list[MAX_LIST];              // (block, slot, len, state)
@@ -576,7 +576,10 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   __shared__ float s_ts[16];
 
   const int G = p.groups;
-  const int splits = a_splits;
+  // kv heads (low 16 bits) and splits (high 16 bits) share one preloaded
+  // argument, so that the split magic (used by the rank) is preloaded too.
+  const int a_kv_heads = a_kvh_splits & 0xffff;
+  const int splits = int(uint32_t(a_kvh_splits) >> 16);
   const int split = blockIdx.x % splits;
   const int unit = int(blockIdx.x) / splits;
   const int b = unit / a_kv_heads;
@@ -694,8 +697,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       q = r;
       return true;
     }
-    if (p.split_magic != 0) {
-      uint32_t qq = __umulhi(uint32_t(r), p.split_magic);
+    if (a_split_magic != 0) {
+      uint32_t qq = __umulhi(uint32_t(r), a_split_magic);
       if (qq * uint32_t(splits) > uint32_t(r)) qq -= 1u;
       q = int(qq);
     } else {
@@ -766,12 +769,14 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         const int idx = c0 + k * nthreads + tid;
         const uint64_t mh = __ballot(cls[k] == 1);
         const uint64_t mw = __ballot(cls[k] == 2);
+        // One rank and one list write per entry, whichever its tier (the
+        // wave runs both tiers' lanes at once).
+        const bool is_hot = cls[k] == 1;
+        const int r = is_hot ? hb + __popcll(mh & below) : wb + __popcll(mw & below);
         int q;
-        if (cls[k] == 1) {
-          if (mine(hb + __popcll(mh & below), q)) s_list[q] = make_int4(idx, slot[k], len[k], list_stage ? q : idx);
-        } else if (cls[k] == 2) {
-          if (mine(wb + __popcll(mw & below), q))
-            s_list[MAX_LIST - 1 - q] = make_int4(idx, slot[k], len[k], list_stage ? p.stage_cap - 1 - q : idx);
+        if (cls[k] != 0 && mine(r, q)) {
+          const int pos = is_hot ? q : MAX_LIST - 1 - q;
+          s_list[pos] = make_int4(idx, slot[k], len[k], list_stage ? (is_hot ? q : p.stage_cap - 1 - q) : idx);
         }
       }
       seen_hot += __builtin_amdgcn_readlane(ih, 63);
@@ -828,10 +833,12 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     const uint64_t below = (1ull << lane) - 1ull;
     // .w: the entry's stage index (its list position with list staging, else
     // its logical block).
+    const int r = hot ? hb + __popcll(mh & below) : wb + __popcll(mw & below);
     int q;
-    if (hot && mine(hb + __popcll(mh & below), q)) s_list[q] = make_int4(idx, slot, len, list_stage ? q : idx);
-    if (warm && mine(wb + __popcll(mw & below), q))
-      s_list[MAX_LIST - 1 - q] = make_int4(idx, slot, len, list_stage ? p.stage_cap - 1 - q : idx);
+    if ((hot || warm) && mine(r, q)) {
+      const int pos = hot ? q : MAX_LIST - 1 - q;
+      s_list[pos] = make_int4(idx, slot, len, list_stage ? (hot ? q : p.stage_cap - 1 - q) : idx);
+    }
   }
   if (COLD_ZERO) {
 #pragma unroll
@@ -1519,12 +1526,15 @@ static void launch_nw(const DecodeParams& p, bool long_rows, int grid, hipStream
   if (SC && p.lds_stage == STAGE_LDS_BLOCK) shmem += size_t(p.groups) * p.num_blocks * 2 * sizeof(float);
   if (SC && p.lds_stage == STAGE_LDS_LIST) shmem += size_t(p.groups) * p.stage_cap * 2 * sizeof(float);
   const int32_t stride = int32_t(p.table_stride);
+  const int32_t kvh_splits = int32_t(uint32_t(p.kv_heads) | (uint32_t(p.splits) << 16));
   if (long_rows)
     hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, true>), dim3(grid), dim3(NW * 64), shmem, stream,
-                       p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, p.kv_heads, p.splits, p);
+                       p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, kvh_splits,
+                       p.split_magic, p);
   else
     hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, false>), dim3(grid), dim3(NW * 64), shmem, stream,
-                       p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, p.kv_heads, p.splits, p);
+                       p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, kvh_splits,
+                       p.split_magic, p);
 }
 
 // Rows longer than one chunk of the workgroup's threads take the long-row
@@ -1667,6 +1677,8 @@ extern "C" int32_t tierkv_decode_attention(
       if (m & 7u) return fail(TIERKV_ERR_INVALID, "reference-format scale/zero pools must be 8-byte aligned");
     }
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, p.groups, splits_hint);
+    if (pl.splits > 0xffff || num_kv_heads > 0xffff)
+      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or splits");
     p.splits = pl.splits;
     p.split_magic = 0;
     // Unsplit score launches keep the per-block statistics in LDS (up to
