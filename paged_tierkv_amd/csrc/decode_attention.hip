@@ -678,7 +678,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
 
   // ---- this workgroup's share of the resident blocks ------------------------
   // One pass over the table row.  HOT and WARM blocks are ranked separately in
-  // logical order; the workgroup keeps rank % splits == split, HOT entries at
+  // logical order; the workgroup keeps rank % splits == split (rows of one
+  // pass of the long-row build: a contiguous range of ranks), HOT entries at
   // list positions [0, nhot) from the front, WARM entries from the back
   // (position MAX_LIST - 1 - k for the k-th).  The first pass ranks the
   // entries loaded at the kernel's start.  COLD tokens (zero-logit mode) are
@@ -692,6 +693,19 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // Whether rank r belongs to this split (r % splits == split), and its list
   // position q = r / splits: one multiply-high by ceil(2^32 / splits) and a
   // correction (exact while r * splits < 2^32, which the host checks).
+  // x / splits for 0 <= x <= num_blocks * splits (the same multiply-high).
+  auto div_splits = [&](int x) -> int {
+    if (splits == 1) return x;
+    if (a_split_magic != 0) {
+      uint32_t qq = __umulhi(uint32_t(x), a_split_magic);
+      if (qq * uint32_t(splits) > uint32_t(x)) qq -= 1u;
+      return int(qq);
+    }
+    return int(uint32_t(x) / uint32_t(splits));
+  };
+  // This workgroup's HOT / WARM entry counts when it owns contiguous rank
+  // ranges (rows of one pass of the long-row build), else -1.
+  int own_h = -1, own_w = -1;
   auto mine = [&](int r, int& q) -> bool {
     if (splits == 1) {
       q = r;
@@ -714,6 +728,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     // The first pass is written out before the loop over further passes, so
     // that no wait at the loop's head holds its loads behind the query's.
     using Chunks = int[PRE_CHUNKS];
+    const bool one_pass = a_num_blocks <= PRE_CHUNKS * nthreads;
     auto load_chunks = [&](int c0, Chunks& st, Chunks& len, Chunks& slot) {
       // Past the row's end the last entry is re-read and ignored: the loads
       // need no per-lane branch.
@@ -758,6 +773,37 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       const int cw = (lane < nj) ? s_wcnt[1][lane] : 0;
       const int ih = wave_inclusive_scan(ch);
       const int iw = wave_inclusive_scan(cw);
+      if (one_pass) {
+        // Rows of one pass: split s owns the contiguous ranks
+        // [tot * s / splits, tot * (s + 1) / splits) of each tier.  Lane j
+        // holds chunk j's bases relative to this workgroup's ranges; the
+        // chunks are ranked without branches, so their scalar reads overlap.
+        const int tot_h = __builtin_amdgcn_readlane(ih, nj - 1);
+        const int tot_w = __builtin_amdgcn_readlane(iw, nj - 1);
+        const int lo_h = div_splits(tot_h * split), lo_w = div_splits(tot_w * split);
+        own_h = div_splits(tot_h * (split + 1)) - lo_h;
+        own_w = div_splits(tot_w * (split + 1)) - lo_w;
+        const int rh = ih - ch - lo_h;
+        const int rw = iw - cw - lo_w;
+        const int wu = uniform(w);
+  #pragma unroll
+        for (int k = 0; k < PRE_CHUNKS; ++k) {
+          const int hb = __builtin_amdgcn_readlane(rh, k * nw + wu);
+          const int wb = __builtin_amdgcn_readlane(rw, k * nw + wu);
+          const uint64_t mh = __ballot(cls[k] == 1);
+          const uint64_t mw = __ballot(cls[k] == 2);
+          const bool is_hot = cls[k] == 1;
+          const uint64_t m = is_hot ? mh : mw;
+          const int q = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32), __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u))) +
+                        (is_hot ? hb : wb);
+          if (cls[k] != 0 && uint32_t(q) < uint32_t(is_hot ? own_h : own_w)) {
+            const int idx = k * nthreads + tid;
+            const int pos = is_hot ? q : MAX_LIST - 1 - q;
+            s_list[pos] = make_int4(idx, slot[k], len[k], list_stage ? (is_hot ? q : p.stage_cap - 1 - q) : idx);
+          }
+        }
+        return;
+      }
       const uint64_t below = (1ull << lane) - 1ull;
   #pragma unroll
       for (int k = 0; k < PRE_CHUNKS; ++k) {
@@ -846,8 +892,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     if (lane == 0) s_wcold[w] = cold_part;
   }
   __syncthreads();
-  const int nhot = uniform((seen_hot > split) ? (seen_hot - split + splits - 1) / splits : 0);
-  const int nwarm = uniform((seen_warm > split) ? (seen_warm - split + splits - 1) / splits : 0);
+  const int nhot = uniform(own_h >= 0 ? own_h : (seen_hot > split) ? (seen_hot - split + splits - 1) / splits : 0);
+  const int nwarm = uniform(own_w >= 0 ? own_w : (seen_warm > split) ? (seen_warm - split + splits - 1) / splits : 0);
 
   // ---- query (fp16) and its per-head sum ------------------------------------
   // qv: dims 64(i/2) + 16g + 8(i%2) .. +7 in word group i (the WARM K
