@@ -38,9 +38,13 @@ HIP_SOURCES = {
     # one dynamically indexed store and push the tiles to scratch memory.
     # The decode kernel's leading scalar arguments (table row pointers, query,
     # geometry) are preloaded into SGPRs at wave launch, saving a kernarg
-    # round trip before the table row can be read.
+    # round trip before the table row can be read.  The atomic optimizer is
+    # off: the kernel's atomics are already issued by one lane (tile hand-out,
+    # arrival) or are rare (error bits), and its wave-reduction wrapper added
+    # about ten instructions to every tile hand-out.
     "decode_attention.hip": ["-mllvm", "-simplifycfg-sink-common=false",
-                             "-mllvm", "-amdgpu-kernarg-preload-count=9"],
+                             "-mllvm", "-amdgpu-kernarg-preload-count=9",
+                             "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
     "quantize.hip": ["-ffp-contract=off"],
     "block_score.hip": ["-ffp-contract=off"],
     # The append kernel's leading arguments are preloaded (as the decode

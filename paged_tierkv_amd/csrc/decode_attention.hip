@@ -65,6 +65,7 @@ constexpr float FOLD_MAX = 2.f;    // WARM V scales above this are applied to V
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float BIAS_I8 = 1152.f;  // fp16 value of an int8 code c is 1152 + c
 constexpr float BIAS_U8 = 1024.f;  // fp16 value of a uint8 code u is 1024 + u
+constexpr uint32_t BIAS_I8_F16X2 = 0x64806480u;   // two fp16 1152s
 
 struct DecodeParams {
   const void* q;
@@ -273,10 +274,13 @@ __device__ __forceinline__ float half_of(const uint32_t* pair, int r) {
 
 // Per-wave softmax state.  acc holds O^T: acc[s][r] = O[head n][(4g + r) * DS + s]
 // scaled by PBOOST and 2^-m_run; l and corr are this lane's partial sums
-// over its four tokens (reduced over g at the end).
+// over its four tokens (reduced over g at the end).  ocorr is the int8
+// codes' offset term summed by the MFMA: 1152 * (the sum of head n's fp16 P
+// over all tokens of the tiles), the same in every lane of the head.
 template <int D>
 struct WaveState {
   f32x4 acc[D / 16];
+  float ocorr;
   float m_run;
   float l_part;
   float corr;
@@ -287,6 +291,7 @@ __device__ __forceinline__ void rescale_state(float m_new, WaveState<D>& ws) {
   const float alpha = (ws.m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ws.m_run - m_new);
 #pragma unroll
   for (int s = 0; s < D / 16; ++s) ws.acc[s] *= alpha;
+  ws.ocorr *= alpha;
   ws.l_part *= alpha;
   ws.corr *= alpha;
   ws.m_run = m_new;
@@ -416,25 +421,31 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
   mask_tail(x, lane >> 4, len);
   softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, si, s_stage, ws);
 
-  // O^T += V^T P^T: transpose the four rows' codes so that vt[s] holds the
-  // four tokens of dim n*DS + s.
-  uint32_t vt[DS];
+  // O^T += V^T P^T: the A operand of step s holds the four tokens of dim
+  // n*DS + s (a byte transpose of the four rows' codes: vt[s]).
+  auto transpose_v = [&](uint32_t* vt) {
 #pragma unroll
-  for (int w4 = 0; w4 < RW; ++w4)
-    transpose_bytes4x4(t.v[0 * RW + w4], t.v[1 * RW + w4], t.v[2 * RW + w4], t.v[3 * RW + w4], &vt[4 * w4]);
+    for (int w4 = 0; w4 < RW; ++w4)
+      transpose_bytes4x4(t.v[0 * RW + w4], t.v[1 * RW + w4], t.v[2 * RW + w4], t.v[3 * RW + w4], &vt[4 * w4]);
+  };
+  uint32_t vt[DS];
   if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
     const float sv = __uint_as_float(t.m[1]);
     if (sv <= FOLD_MAX) {
       const float f = PBOOST * sv;
-      const uint32_t p01 = pack_f16x2(pr[0] * f, pr[1] * f);
-      const uint32_t p23 = pack_f16x2(pr[2] * f, pr[3] * f);
-      // The offset is removed with the same fp16 P values the MFMA multiplies.
-      ws.corr += BIAS_I8 * ((half_lo(p01) + half_hi(p01)) + (half_lo(p23) + half_hi(p23)));
-      const f16x4 pf = as_f16x4(p01, p23);
+      const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * f, pr[1] * f), pack_f16x2(pr[2] * f, pr[3] * f));
+      // The offset 1152 of every code is removed with the same fp16 P values
+      // the MFMA multiplies: an A operand of 1152s gives 1152 * sum(P) per
+      // head (in every element of its result).
+      const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+      ws.ocorr += __builtin_amdgcn_mfma_f32_16x16x16f16(as_f16x4(BIAS_I8_F16X2, BIAS_I8_F16X2), pf, zero4, 0, 0, 0)[0];
 #pragma unroll
       for (int s = 0; s < DS; ++s)
-        ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_plus1152(vt[s]), pf, ws.acc[s], 0, 0, 0);
+        ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+            i8_col_plus1152(t.v[0 * RW + s / 4], t.v[1 * RW + s / 4], t.v[2 * RW + s / 4], t.v[3 * RW + s / 4], s % 4),
+            pf, ws.acc[s], 0, 0, 0);
     } else {
+      transpose_v(vt);
       // Large V scale: apply it to V (fp16(c * s_v)) so that P stays in range.
       const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
 #pragma unroll
@@ -449,6 +460,7 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
       }
     }
   } else {
+    transpose_v(vt);
     float sv[4], zv[4];
     bool big = false;
 #pragma unroll
@@ -943,6 +955,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   st.m_run = -INFINITY;
   st.l_part = 0.f;
   st.corr = 0.f;
+  st.ocorr = 0.f;
 
   auto grab = [&](int c) -> int {
     int v = 0;
@@ -1034,7 +1047,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   float l = st.l_part + shfl_xor_f(st.l_part, 16);
   l += shfl_xor_f(l, 32);
   float corr = st.corr + shfl_xor_f(st.corr, 16);
-  corr += shfl_xor_f(corr, 32);
+  corr += shfl_xor_f(corr, 32) + st.ocorr;
   float* s_acc = s_dyn;   // [nw][G][D]
   if (head_ok) {
     if (g == 0) {
