@@ -187,6 +187,35 @@ def test_long_row_list_build(device, groups):
     _check(case, "ref_u8", device, cold_mode="zero_logit", return_scores=True)
 
 
+@pytest.mark.parametrize("scores", [False, True])
+def test_one_pass_long_rows_split_ranges(device, scores):
+    # Rows longer than one 512-entry chunk but within one pass of the long-row
+    # build (at most 4 x 512 blocks): each split owns a contiguous range of
+    # the HOT ranks and of the WARM ranks.  Many split counts, ragged lengths
+    # (zero-length blocks are skipped), and a sparse row where most splits own
+    # nothing.
+    g = torch.Generator().manual_seed(5)
+    lengths = torch.randint(0, 17, (2, 1500), generator=g, dtype=torch.int32)
+    lengths[:, -1] = 3
+    dense = W.make_tiered_case("one_pass", 2, 8, 2, 64, 1500, 60, 500, seed=81, lengths=lengths, max_blocks=1510)
+    sparse = W.make_tiered_case("one_pass_sparse", 1, 8, 2, 64, 700, 2, 3, seed=82, recent_hot=1)
+    for case, fmt, cold in ((dense, "absmax_i8", "masked"), (sparse, "ref_u8", "zero_logit")):
+        warm = oracle_warm(case, fmt)
+        args = to_gpu_inputs(case, warm, device)
+        res = oracle_decode(case, warm, fmt, cold, scores)
+        exp_out, exp_sc = res if scores else (res, None)
+        for splits in (1, 2, 3, 5, 8, 13):
+            print(f"[decode] one-pass long rows: case={case.name} fmt={fmt} splits={splits} scores={scores}",
+                  flush=True)
+            out, sc = tierkv_decode_attention(**args, return_scores=scores, cold_mode=cold, splits=splits)
+            torch.cuda.synchronize()
+            assert_close(out[:, 0].float().cpu().numpy(), exp_out, what=f"{case.name} splits={splits} output")
+            if scores:
+                sc = sc.cpu().numpy()
+                assert_close(sc[None] if sc.ndim == 2 else sc, exp_sc, what=f"{case.name} splits={splits} score_sums")
+            assert workspace_error_word(device) == 0
+
+
 @pytest.mark.parametrize("fmt", ["absmax_i8", "ref_u8"])
 def test_split_list_capacity(device, fmt):
     # 1 HOT + 1023 WARM blocks asked to run in 2 splits: split 0 would get
