@@ -199,14 +199,90 @@ def tierkv_decode_attention(
 ):
     """Decode attention over a tiered paged KV cache (see module docstring)."""
     lib = _lib.lib()  # RuntimeError if the HIP library is not built
+    statics = (block_table, block_states, block_lengths, hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool,
+               k_scale, k_zero, v_scale, v_zero)
+    simple = workspace is None and seq_num_blocks is None and splits is None
+    if simple:
+        hit = _rebind(lib, query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode)
+        if hit is not None:
+            args, out, score_sums, ws, batched = hit
+            _launch(lib, args, query_states.device, ws)
+            if score_sums is not None and not batched:
+                score_sums = score_sums[0]
+            return out, score_sums
     args, out, score_sums, ws, batched, _ = _bind(
         query_states, block_table, block_states, block_lengths, hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool,
         k_scale, k_zero, v_scale, v_zero, num_blocks, num_key_value_groups, scaling, return_scores,
         cold_mode=cold_mode, seq_num_blocks=seq_num_blocks, splits=splits, workspace=workspace)
+    if simple:
+        _remember(query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode,
+                  args, batched)
     _launch(lib, args, query_states.device, ws)
     if score_sums is not None and not batched:
         score_sums = score_sums[0]
     return out, score_sums
+
+
+# Calls that pass the same table, pool and metadata tensors again (a decode
+# loop: the drop-in's per-layer launch every step) skip the validation of
+# those tensors.  An entry holds them by weak reference and records their
+# addresses; it matches only while every one is still the same live tensor at
+# the same address, and everything that varies per call (the query, the block
+# count, the output, the stream's workspace) is checked or made per call.
+_REBIND: dict = {}
+_REBIND_MAX = 64
+
+
+def _rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode):
+    return (tuple(id(t) for t in statics), query_states.dtype, tuple(query_states.shape), query_states.device,
+            int(num_key_value_groups), float(scaling), bool(return_scores), cold_mode)
+
+
+def _remember(query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode, args,
+              batched):
+    if len(_REBIND) >= _REBIND_MAX:
+        _REBIND.pop(next(iter(_REBIND)))
+    key = _rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode)
+    refs = tuple(None if t is None else weakref.ref(t) for t in statics)
+    ptrs = tuple(None if t is None else t.data_ptr() for t in statics)
+    # args: query, dtype, out, scores | table, states, lengths, stride, None | num_blocks | pools ... splits hint
+    _REBIND[key] = (refs, ptrs, args[1], args[4:9], args[10:29], batched, {int(num_blocks): None})
+
+
+def _rebind(lib, query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode):
+    """The bound arguments of a repeated call, or None (bind in full)."""
+    if not _REBIND or not query_states.is_cuda:
+        return None
+    e = _REBIND.get(_rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode))
+    if e is None:
+        return None
+    refs, ptrs, dtype_code, mid, tail, batched, needs = e
+    for r, p, t in zip(refs, ptrs, statics):
+        if (r is None) != (t is None) or (t is not None and (r() is not t or t.data_ptr() != p)):
+            return None
+    n = int(num_blocks)
+    if n <= 0:
+        raise ValueError("num_blocks must be positive.")
+    if n > mid[3]:
+        raise ValueError("num_blocks exceeds the provided block table length.")
+    query = query_states.contiguous()
+    batch, num_heads, _, head_dim = query.shape
+    device = query.device
+    out = torch.empty((batch, 1, num_heads, head_dim), device=device, dtype=query.dtype)
+    score_sums = torch.empty((batch, num_heads, mid[3]), device=device, dtype=torch.float32) if return_scores else None
+    need = needs.get(n)
+    if need is None:
+        # tail: hot_k, hot_v, hot_slots, warm_k, warm_v, warm_slots, k_scale, k_zero, v_scale, v_zero,
+        # fmt, cold, batch, heads, kv_heads, block_size, head_dim, scaling, splits hint
+        need = needs[n] = lib.tierkv_decode_workspace_bytes(batch, num_heads, tail[14], n, tail[15], head_dim,
+                                                            int(return_scores), tail[18])
+        if need < 0:
+            raise ValueError("invalid decode geometry.")
+    ws = stream_workspace(device)
+    ws.reserve(need)
+    args = ((_lib.ptr(query), dtype_code, _lib.ptr(out), _lib.ptr(score_sums)) + mid + (n,) + tail +
+            (ws.data_ptr(), ws.nbytes))
+    return args, out, score_sums, ws, batched
 
 
 class PreparedDecode:

@@ -182,6 +182,7 @@ class _Tables:
         for i, f in enumerate(self.fills):
             self.dev[:, i, :].fill_(f)
         self.pending: dict[int, int] = {}
+        self._rows: dict = {}   # (k, layer) -> dev[layer, k] (dev is never replaced)
 
     def _flat(self, k: int, layer: int, idx: int) -> int:
         return (layer * self.shape[1] + k) * self.shape[2] + idx
@@ -193,6 +194,8 @@ class _Tables:
         if not (-self.shape[2] <= idx < self.shape[2]):
             raise IndexError(f"index {idx} is out of bounds for dimension 1 with size {self.shape[2]}")
         idx %= self.shape[2]
+        if self.host[layer, k, idx] == value:
+            return   # the device row already holds it, or a queued entry does
         self.host[layer, k, idx] = value
         self.pending[self._flat(k, layer, idx)] = value
 
@@ -226,6 +229,17 @@ class _Tables:
     def view(self, k: int) -> torch.Tensor:
         self.flush()
         return self.dev[:, k, :]
+
+    def row_view(self, k: int, layer: int) -> torch.Tensor:
+        """One layer's row of table k (queued entries pushed first); the
+        decode path asks for the same rows every step, so the views are kept."""
+        self.flush()
+        v = self._rows.get((k, layer))
+        if v is None:
+            if not -self.shape[0] <= layer < self.shape[0]:
+                raise IndexError(f"index {layer} is out of bounds for dimension 0 with size {self.shape[0]}")
+            v = self._rows[(k, layer)] = self.dev[layer, k]
+        return v
 
 
 def _scatter(dev: torch.Tensor, pairs: np.ndarray, n: int) -> None:
@@ -672,6 +686,11 @@ class _PoolBase(_QueuedStorage):
         b = self._blocks.get(int(physical_idx))
         return None if b is None else b.state
 
+    def _append_token(self, physical_idx: int, pos: int, src_k, src_v) -> None:
+        """One token at position pos of a HOT block that has room (the
+        runtime's decode-step append)."""
+        self._write_hot_range(physical_idx, pos, src_k, src_v, 0, 1)
+
     def _check_physical_idx(self, physical_idx: int) -> int:
         physical_idx = int(physical_idx)
         if not 0 <= physical_idx < self.pool_blocks:
@@ -791,11 +810,12 @@ class _PoolBase(_QueuedStorage):
     def get_layer_table(self, layer_idx: int):
         self._require_allocated()
         self._before_decode()
-        return self._tables.view(self._t_table)[int(layer_idx)], self._tables.view(self._t_state)[int(layer_idx)]
+        layer_idx = int(layer_idx)
+        return self._tables.row_view(self._t_table, layer_idx), self._tables.row_view(self._t_state, layer_idx)
 
     def get_layer_lengths(self, layer_idx: int):
         self._require_allocated()
-        return self._tables.view(self._t_len)[int(layer_idx)]
+        return self._tables.row_view(self._t_len, int(layer_idx))
 
     def _before_decode(self) -> None:
         pass
@@ -1267,6 +1287,24 @@ class CompactTieredKVTensorPool(_PoolBase):
         slot = self._hot.take() if held is None else self._blocks[physical_idx].slot
         self._queue_write(src_k, src_v, tok0, tokens, slot, start)
         self._record(physical_idx, HOT_STATE, slot, start + tokens)
+
+    def _append_token(self, physical_idx: int, pos: int, src_k, src_v) -> None:
+        """_write_hot_range's effect for one token into a HOT block with room
+        and nothing queued: the write launch, the block's new length and its
+        table entry; anything else takes the general path."""
+        b = self._blocks.get(physical_idx)
+        if (b is None or b.state != HOT_STATE or self._depth or self._q_write or self._q_stage or self._q_dem
+                or self._q_pro or not 0 <= pos < self.block_size or self._tables is None
+                or src_k.shape[1] != self.kv_heads or src_k.shape[-1] != self.head_dim
+                or src_k.device != self.device):
+            self._write_hot_range(physical_idx, pos, src_k, src_v, 0, 1)
+            return
+        self._launch_writes(_lib.lib(), src_k, src_v, [(0, 1, b.slot, pos)], self.hot_k_pool, self.hot_v_pool,
+                            _lib.stream_of(self.device))
+        self._blocks[physical_idx] = _Block(HOT_STATE, b.slot, pos + 1)
+        where = self._where.get(physical_idx)
+        if where is not None:
+            self._tables.set(self._t_len, where[0], where[1], pos + 1)
 
     def _write_warm_range(self, physical_idx, src_k, src_v, tok0, length) -> None:
         if src_k.ndim != 4 or src_k.shape[0] != 1:
@@ -1800,6 +1838,16 @@ class TieredKVRuntime:
         cursor = self.layer_states[seq_id]
         pool = self.kv_pool
         src_k, src_v = pool._source(key_states, value_states)
+        p = cursor.open_physical_idx
+        if p is not None and src_k.shape[-2] == 1 and pool.get_physical_state(p) == HOT_STATE:
+            # A decode step's token into the open HOT block (an open block has
+            # room: a full one is closed): the one write of the general path
+            # below, without its placement loop.
+            pool._append_token(p, cursor.open_token_count, src_k, src_v)
+            cursor.open_token_count += 1
+            if cursor.open_token_count == self.block_size:
+                cursor.open_physical_idx, cursor.open_token_count = None, 0
+            return False
         opened = False
         consumed = 0
         with pool._batch():
