@@ -216,6 +216,38 @@ def test_one_pass_long_rows_split_ranges(device, scores):
             assert workspace_error_word(device) == 0
 
 
+def test_repeated_calls_reuse_bound_arguments(device):
+    # A decode loop passes the same tables and pools every step with a new
+    # query and block count: the second and later calls skip the tensors'
+    # validation (tierkv_hip's rebind entries) and must give what a full
+    # bind gives; per-call arguments are still checked, and a replaced pool
+    # tensor is bound anew.
+    import paged_tierkv_amd.tierkv_hip as th
+    case = W.make_tiered_case("rebind", 1, 8, 2, 64, 40, 8, 20, seed=91, recent_hot=2)
+    warm = oracle_warm(case, "absmax_i8")
+    args = to_gpu_inputs(case, warm, device)
+    th._REBIND.clear()
+    first, _ = tierkv_decode_attention(**args, cold_mode="masked")
+    assert len(th._REBIND) == 1
+    for nb in (40, 25, 40):
+        a = dict(args, num_blocks=nb, query_states=args["query_states"].clone())
+        got, _ = tierkv_decode_attention(**a, cold_mode="masked")
+        case_nb = W.make_tiered_case("rebind", 1, 8, 2, 64, 40, 8, 20, seed=91, recent_hot=2)
+        case_nb.num_blocks = nb
+        exp = oracle_decode(case_nb, warm, "absmax_i8", "masked")
+        assert_close(got[:, 0].float().cpu().numpy(), exp, what=f"rebind num_blocks={nb}")
+    assert len(th._REBIND) == 1
+    with pytest.raises(ValueError, match="exceeds"):
+        tierkv_decode_attention(**dict(args, num_blocks=41), cold_mode="masked")
+    with pytest.raises(ValueError, match="positive"):
+        tierkv_decode_attention(**dict(args, num_blocks=0), cold_mode="masked")
+    moved = dict(args, hot_k_pool=args["hot_k_pool"].clone())
+    again, _ = tierkv_decode_attention(**moved, cold_mode="masked")
+    assert len(th._REBIND) == 2
+    torch.cuda.synchronize()
+    assert torch.allclose(again.float(), first.float(), atol=2e-3, rtol=1e-2)
+
+
 @pytest.mark.parametrize("fmt", ["absmax_i8", "ref_u8"])
 def test_split_list_capacity(device, fmt):
     # 1 HOT + 1023 WARM blocks asked to run in 2 splits: split 0 would get
