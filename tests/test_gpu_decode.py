@@ -249,6 +249,39 @@ def test_repeated_calls_reuse_bound_arguments(device):
 
 
 @pytest.mark.parametrize("fmt", ["absmax_i8", "ref_u8"])
+def test_large_warm_v_scales(device, fmt):
+    # WARM V blocks whose scale exceeds 2 take the kernel's unfolded path
+    # (the scale applied to V before the MFMA, so fp16 P cannot overflow);
+    # every other slot's V stays small, so the waves meet both paths, and
+    # the offset sums of the folded tiles must not absorb the unfolded ones.
+    case = W.make_tiered_case("big_v", 2, 8, 2, 64, 48, 6, 30, seed=95, recent_hot=2)
+    v = case.warm_src_v.float()
+    v[0::2] *= 600.0
+    case.warm_src_v = v.to(torch.float16)
+    warm = oracle_warm(case, fmt)
+    sv = np.asarray(warm[4], dtype=np.float32)
+    assert (sv > 2).any() and (sv <= 2).any()
+    # The unfolded path rounds each dequantized V value to fp16 before the
+    # MFMA (the oracle keeps it in fp32): an output element can differ by up
+    # to half an fp16 ulp of the largest |V|, 2^-11 * max|V|.  A wrong scale,
+    # offset or tile would be off by far more.
+    vmax = float(np.abs(case.warm_src_v.float().numpy()).max())
+    atol = 2.0 ** -11 * vmax
+    cold = "zero_logit" if fmt == "ref_u8" else "masked"
+    args = to_gpu_inputs(case, warm, device)
+    exp_out, exp_sc = oracle_decode(case, warm, fmt, cold, True)
+    for splits in (None, 3):
+        print(f"[decode] large WARM V scales fmt={fmt} splits={splits} atol={atol:.3f}", flush=True)
+        out, sc = tierkv_decode_attention(**args, return_scores=True, cold_mode=cold, splits=splits)
+        torch.cuda.synchronize()
+        report(f"big_v {fmt} splits={splits} output",
+               assert_close(out[:, 0].float().cpu().numpy(), exp_out, atol=atol, what="big_v output"))
+        report(f"big_v {fmt} splits={splits} score_sums",
+               assert_close(sc.cpu().numpy(), exp_sc, what="big_v score_sums"))
+        assert workspace_error_word(device) == 0
+
+
+@pytest.mark.parametrize("fmt", ["absmax_i8", "ref_u8"])
 def test_split_list_capacity(device, fmt):
     # 1 HOT + 1023 WARM blocks asked to run in 2 splits: split 0 would get
     # ceil(1/2) + ceil(1023/2) = 513 list entries, one more than the LDS list
