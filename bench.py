@@ -332,7 +332,7 @@ def run_c1(args, device):
     import torch
 
     from paged_tierkv_amd import kernels, workloads as W
-    from paged_tierkv_amd.tierkv_hip import tierkv_decode_attention, workspace_error_word
+    from paged_tierkv_amd.tierkv_hip import PreparedDecode, tierkv_decode_attention, workspace_error_word
 
     case = W.config1()
     hot_k, hot_v = case.hot_k.to(device), case.hot_v.to(device)
@@ -355,7 +355,10 @@ def run_c1(args, device):
         tierkv_decode_attention(**dargs, cold_mode="masked")
 
     # 50 launches per graph: a one-launch graph would time the graph launch.
-    sec, steps = graph_timed(step, 1, args.steps, 20, passes=50)
+    # The captured launch owns a fixed workspace (a capturing stream has no
+    # implicit one).
+    prepared = PreparedDecode(**dargs, cold_mode="masked")
+    sec, steps = graph_timed(lambda i: prepared.launch(), 1, args.steps, 20, passes=50)
     for _ in range(20):
         step(0)
     torch.cuda.synchronize()
