@@ -2,7 +2,8 @@
 random tier mixes (hypothesis, derandomized so every run draws the same
 cases): batch, kv heads, GQA group, head_dim, row length, HOT/WARM/COLD
 fractions, ragged block lengths, dense or compact pools, both WARM formats,
-both COLD modes, score sums on or off, and automatic or forced splits.
+both COLD modes, score sums on or off, and automatic or forced splits; and
+rows of the long-row list build (513 to 2600 blocks) at many split counts.
 
 Tolerance: BASELINE's 2e-3 absolute / 1e-2 relative vs the fp32 oracle for
 outputs and per-block probability sums (the same bar as test_gpu_decode)."""
@@ -67,3 +68,46 @@ def test_decode_matches_oracle_on_random_tier_mixes(device, c):
     assert_close(out[:, 0].float().cpu().numpy(), exp_out, what="output")
     if c["scores"]:
         assert_close(sums.cpu().numpy(), exp_sc, what="score sums")
+
+
+@st.composite
+def long_row_cases(draw):
+    # Rows of the long-row list build: 513..2600 blocks (one pass up to
+    # 2048, several beyond), sparse or dense tier mixes, many split counts.
+    nb = draw(st.sampled_from([513, 700, 1100, 1500, 2048, 2600]))
+    hot_frac = draw(st.sampled_from([0.0, 0.01, 0.05, 0.3]))
+    warm_frac = draw(st.sampled_from([0.0, 0.02, 0.45, 0.6]))
+    n_hot = int(round(nb * hot_frac))
+    n_warm = min(nb - n_hot, int(round(nb * warm_frac)))
+    if n_hot + n_warm == 0:
+        n_hot = 1
+    seed = draw(st.integers(0, 2 ** 16))
+    lengths = None
+    if draw(st.booleans()):
+        g = torch.Generator().manual_seed(seed)
+        lengths = torch.randint(0, 17, (1, nb), generator=g)
+    case = W.make_tiered_case("prop_long", 1, 8, 2, 64, nb, n_hot, n_warm, seed=seed, lengths=lengths,
+                              recent_hot=draw(st.integers(0, 2)))
+    return dict(case=case, fmt=draw(st.sampled_from(["absmax_i8", "ref_u8"])),
+                cold=draw(st.sampled_from(["masked", "zero_logit"])), scores=draw(st.booleans()),
+                splits=draw(st.sampled_from([None, 1, 2, 3, 5, 8, 13])))
+
+
+@settings(max_examples=16, deadline=None, derandomize=True, database=None,
+          suppress_health_check=[HealthCheck.function_scoped_fixture, HealthCheck.too_slow])
+@given(long_row_cases())
+def test_long_rows_match_oracle(device, c):
+    case = c["case"]
+    print(f"[prop-long] nb={case.num_blocks} tiers={case.tier_counts()} fmt={c['fmt']} cold={c['cold']} "
+          f"scores={c['scores']} splits={c['splits']}", flush=True)
+    warm = oracle_warm(case, c["fmt"])
+    out, sums = tierkv_decode_attention(**to_gpu_inputs(case, warm, device), return_scores=c["scores"],
+                                        cold_mode=c["cold"], splits=c["splits"])
+    torch.cuda.synchronize()
+    assert workspace_error_word(device) == 0
+    res = oracle_decode(case, warm, c["fmt"], c["cold"], c["scores"])
+    exp_out, exp_sc = res if c["scores"] else (res, None)
+    assert_close(out[:, 0].float().cpu().numpy(), exp_out, what="output")
+    if c["scores"]:
+        s = sums.cpu().numpy()
+        assert_close(s[None] if s.ndim == 2 else s, exp_sc, what="score sums")
