@@ -391,10 +391,13 @@ class _QueuedStorage:
     def _launch_writes(self, lib, src_k, src_v, rows, dst_k, dst_v, stream) -> None:
         n = len(rows)
         if n <= _INLINE_JOBS:
-            # A decode step's few jobs ride in the kernel's arguments.
-            jobs = np.zeros((n, 5), np.int32)     # src_seq, src_tok, count, dst_slot, dst_pos
+            # A decode step's few jobs ride in the kernel's arguments (the C
+            # call copies them, so one host array serves every call).
+            jobs = self.__dict__.get("_jobs_host")
+            if jobs is None:
+                jobs = self._jobs_host = np.zeros((_INLINE_JOBS, 5), np.int32)
             for i, (tok0, count, slot, pos) in enumerate(rows):
-                jobs[i, 1], jobs[i, 2], jobs[i, 3], jobs[i, 4] = tok0, count, slot, pos
+                jobs[i] = (0, tok0, count, slot, pos)   # src_seq, src_tok, count, dst_slot, dst_pos
             rc = lib.tierkv_write_hot_tokens_inline(
                 _lib.ptr(src_k), _lib.ptr(src_v), int(src_k.shape[0]), int(src_k.shape[2]), jobs.ctypes.data, n, 1,
                 _lib.ptr(dst_k), _lib.ptr(dst_v), int(dst_k.shape[0]),
