@@ -301,6 +301,65 @@ TIERKV_API int32_t tierkv_scatter_i32(int32_t* dst, int64_t dst_len, const int32
 TIERKV_API int32_t tierkv_scatter_i32_inline(int32_t* dst, int64_t dst_len, const int32_t* pairs_host, int32_t n,
                                              void* stream);
 
+/* One decode step of a layer in one call: the token write of
+ * tierkv_write_hot_tokens_inline (n_jobs 0..4), the table writes of
+ * tierkv_scatter_i32_inline (n_pairs 0..16), then tierkv_decode_attention,
+ * in stream order, each validated as its own entry point validates it.  It
+ * replaces the three calls the reference's decode forward makes per layer
+ * and step (append_to_layer's token write, the table update it queues, and
+ * tierkv_decode_attention: modeling_llama.py:419-456, tierkv_policy.py:
+ * 1768-1816, 1869-1872), so that a host-bound caller pays one C call.  The
+ * fields are those of the three entry points (8-byte fields first, so the
+ * layout has no interior padding); tierkv_decode_step_size() returns
+ * sizeof(TierkvDecodeStep) for bindings to check theirs against. */
+typedef struct TierkvDecodeStep {
+  const void* src_k;        /* token write: fp16 [src_seqs, kv_heads, src_tokens, head_dim] */
+  const void* src_v;
+  void* hot_k;              /* HOT pools: written by the token write, read by the decode */
+  void* hot_v;
+  int32_t* table_dst;       /* table writes: int32 [table_len] */
+  const void* query;        /* decode: as tierkv_decode_attention */
+  void* out;
+  float* score_sums;
+  const int32_t* block_table;
+  const int32_t* block_states;
+  const int32_t* block_lengths;
+  const int32_t* seq_num_blocks;
+  const void* warm_k;
+  const void* warm_v;
+  const void* k_scale;
+  const void* k_zero;
+  const void* v_scale;
+  const void* v_zero;
+  void* workspace;
+  int64_t src_seqs;
+  int64_t hot_slots;
+  int64_t table_len;
+  int64_t table_stride;
+  int64_t warm_slots;
+  int64_t workspace_bytes;
+  int32_t src_tokens;
+  int32_t n_jobs;
+  int32_t zero_tail;
+  int32_t n_pairs;
+  int32_t query_dtype;
+  int32_t num_blocks;
+  int32_t warm_format;
+  int32_t cold_mode;
+  int32_t batch;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t block_size;
+  int32_t head_dim;
+  float scaling;
+  int32_t splits_hint;
+  int32_t jobs[4][5];       /* {src_seq, src_tok, count, dst_slot, dst_pos} */
+  int32_t pairs[16][2];     /* {table index, value} */
+} TierkvDecodeStep;
+
+TIERKV_API int32_t tierkv_decode_step(const TierkvDecodeStep* step, void* stream);
+TIERKV_API int64_t tierkv_decode_step_size(void);
+
 /* ---------------------------------------------------------------------- */
 /* Block scores.  Per-block probability mass from softmax probabilities
  * probs fp32 [batch, num_heads, tokens] -> out fp32 [batch, tokens/block_size]:

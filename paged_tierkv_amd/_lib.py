@@ -35,6 +35,22 @@ COLD_MASKED = 1
 _P = c_void_p
 _I32P = POINTER(c_int32)
 
+
+class DecodeStep(ctypes.Structure):
+    """TierkvDecodeStep (include/tierkv_hip.h): the token write, the table
+    writes and the decode launch of one layer step, for tierkv_decode_step.
+    The library's sizeof is checked against this layout when it loads."""
+
+    _fields_ = [(name, _P) for name in (
+        "src_k", "src_v", "hot_k", "hot_v", "table_dst", "query", "out", "score_sums", "block_table",
+        "block_states", "block_lengths", "seq_num_blocks", "warm_k", "warm_v", "k_scale", "k_zero", "v_scale",
+        "v_zero", "workspace")] + [(name, c_int64) for name in (
+            "src_seqs", "hot_slots", "table_len", "table_stride", "warm_slots", "workspace_bytes")] + [
+        (name, c_int32) for name in (
+            "src_tokens", "n_jobs", "zero_tail", "n_pairs", "query_dtype", "num_blocks", "warm_format", "cold_mode",
+            "batch", "num_heads", "num_kv_heads", "block_size", "head_dim")] + [
+        ("scaling", c_float), ("splits_hint", c_int32), ("jobs", (c_int32 * 5) * 4), ("pairs", (c_int32 * 2) * 16)]
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "tierkv_last_error": (c_char_p, []),
@@ -108,6 +124,8 @@ SIGNATURES = {
     "tierkv_scatter_i32": (c_int32, [_P, c_int64, _P, c_int32, _P]),
     "tierkv_tier_counts": (c_int32, [_P, _P, c_int64, _P, c_int32, _P, _P]),
     "tierkv_scatter_i32_inline": (c_int32, [_P, c_int64, _P, c_int32, _P]),
+    "tierkv_decode_step": (c_int32, [_P, _P]),
+    "tierkv_decode_step_size": (c_int64, []),
     "tierkv_write_hot_tokens_inline": (c_int32, [
         _P, _P, c_int64, c_int32, _P, c_int32,
         c_int32, _P, _P, c_int64,
@@ -156,6 +174,9 @@ def lib():
             version = handle.tierkv_abi_version()
             if version != ABI_VERSION:
                 raise RuntimeError(f"{LIB_PATH.name} ABI version {version} != expected {ABI_VERSION}; rebuild it.")
+            if handle.tierkv_decode_step_size() != ctypes.sizeof(DecodeStep):
+                raise RuntimeError(f"{LIB_PATH.name}: TierkvDecodeStep is {handle.tierkv_decode_step_size()} bytes, "
+                                   f"the binding's {ctypes.sizeof(DecodeStep)}; rebuild it.")
             _lib = handle
     return _lib
 

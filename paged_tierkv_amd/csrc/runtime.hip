@@ -85,12 +85,22 @@ struct CopyJobs {
   // dst_pos} (the pointers above are unused).
   int32_t inl_n;
   int32_t inl[INLINE_JOBS][5];
+  // sc_n > 0: workgroup (0, 0, 0) also writes sc_dst[sc[i][0]] = sc[i][1]
+  // (the table update of the same decode step, tierkv_decode_step).
+  int32_t sc_n;
+  int32_t* sc_dst;
+  int64_t sc_len;
+  int32_t sc[16][2];
 };
 
 __global__ __launch_bounds__(CT) void write_hot_kernel(CopyJobs c) {
   const int job = blockIdx.x;
   const int h = blockIdx.y;
   const int kv = blockIdx.z;
+  if (c.sc_n > 0 && job == 0 && h == 0 && kv == 0 && int(threadIdx.x) < c.sc_n) {
+    const int pos = c.sc[threadIdx.x][0], val = c.sc[threadIdx.x][1];
+    if (pos >= 0 && pos < c.sc_len) c.sc_dst[pos] = val;
+  }
   const bool inl = c.inl_n > 0;
   const int64_t sq = inl ? c.inl[job][0] : c.src_seq[job];
   const int64_t slot = inl ? c.inl[job][3] : c.dst_slot[job];
@@ -754,6 +764,62 @@ extern "C" int32_t tierkv_scatter_i32_inline(int32_t* dst, int64_t dst_len, cons
                      dst_len, p);
   return check_launch("scatter_i32_inline_kernel");
 }
+
+static int32_t check_write_geometry(const void* src_k, const void* src_v, const void* hot_k, const void* hot_v,
+                                    int32_t src_tokens, int32_t num_kv_heads, int32_t block_size, int32_t head_dim);
+
+extern "C" int32_t tierkv_decode_step(const TierkvDecodeStep* s, void* stream) {
+  clear_error();
+  if (!s) return fail(TIERKV_ERR_INVALID, "null pointer");
+  if (s->n_jobs < 0 || s->n_jobs > INLINE_JOBS) return fail(TIERKV_ERR_INVALID, "a step carries 0..4 write jobs");
+  if (s->n_pairs < 0 || s->n_pairs > INLINE_PAIRS) return fail(TIERKV_ERR_INVALID, "a step carries 0..16 table writes");
+  if (s->n_jobs > 0) {
+    // The token write and the table writes in one launch: workgroup (0, 0, 0)
+    // of the write kernel also applies the pairs.
+    int32_t rc = check_write_geometry(s->src_k, s->src_v, s->hot_k, s->hot_v, s->src_tokens, s->num_kv_heads,
+                                      s->block_size, s->head_dim);
+    if (rc != TIERKV_OK) return rc;
+    if (s->n_pairs > 0 && !s->table_dst) return fail(TIERKV_ERR_INVALID, "null pointer");
+    if (s->table_len > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "scatter target above 2^31 entries");
+    CopyJobs c{};
+    c.src[0] = reinterpret_cast<const __half*>(s->src_k);
+    c.src[1] = reinterpret_cast<const __half*>(s->src_v);
+    c.src_seqs = s->src_seqs;
+    c.src_tokens = s->src_tokens;
+    c.hot[0] = reinterpret_cast<__half*>(s->hot_k);
+    c.hot[1] = reinterpret_cast<__half*>(s->hot_v);
+    c.hot_slots = s->hot_slots;
+    c.kv_heads = s->num_kv_heads;
+    c.bs = s->block_size;
+    c.D = s->head_dim;
+    c.zero_tail = s->zero_tail;
+    c.inl_n = s->n_jobs;
+    for (int i = 0; i < s->n_jobs; ++i)
+      for (int f = 0; f < 5; ++f) c.inl[i][f] = s->jobs[i][f];
+    c.sc_n = s->n_pairs;
+    c.sc_dst = s->table_dst;
+    c.sc_len = s->table_len;
+    for (int i = 0; i < s->n_pairs; ++i) {
+      c.sc[i][0] = s->pairs[i][0];
+      c.sc[i][1] = s->pairs[i][1];
+    }
+    hipLaunchKernelGGL(write_hot_kernel, dim3(s->n_jobs, s->num_kv_heads, 2), dim3(CT), 0,
+                       reinterpret_cast<hipStream_t>(stream), c);
+    rc = check_launch("write_hot_kernel");
+    if (rc != TIERKV_OK) return rc;
+  } else if (s->n_pairs > 0) {
+    const int32_t rc = tierkv_scatter_i32_inline(s->table_dst, s->table_len, &s->pairs[0][0], s->n_pairs, stream);
+    if (rc != TIERKV_OK) return rc;
+  }
+  return tierkv_decode_attention(s->query, s->query_dtype, s->out, s->score_sums, s->block_table, s->block_states,
+                                 s->block_lengths, s->table_stride, s->seq_num_blocks, s->num_blocks, s->hot_k,
+                                 s->hot_v, s->hot_slots, s->warm_k, s->warm_v, s->warm_slots, s->k_scale, s->k_zero,
+                                 s->v_scale, s->v_zero, s->warm_format, s->cold_mode, s->batch, s->num_heads,
+                                 s->num_kv_heads, s->block_size, s->head_dim, s->scaling, s->splits_hint,
+                                 s->workspace, s->workspace_bytes, stream);
+}
+
+extern "C" int64_t tierkv_decode_step_size(void) { return int64_t(sizeof(TierkvDecodeStep)); }
 
 static int32_t check_write_geometry(const void* src_k, const void* src_v, const void* hot_k, const void* hot_v,
                                     int32_t src_tokens, int32_t num_kv_heads, int32_t block_size, int32_t head_dim) {

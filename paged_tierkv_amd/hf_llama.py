@@ -188,11 +188,20 @@ def tierkv_attention_forward(self, hidden_states: torch.Tensor, position_embeddi
         attn_output = attn_output.reshape(*input_shape, -1).contiguous()
         return self.o_proj(attn_output), attn_weights
 
+    output_attentions = bool(kwargs.get("output_attentions", False))
+    mask_safe = bool(kwargs.get("tierkv_triton_mask_safe", False))
+    if runtime.attention_backend == "triton" and not output_attentions and mask_safe and query_states.is_cuda:
+        # The plain decode step (token into the open HOT block, no policy, no
+        # scores): append, table and decode in one C call.
+        out = runtime.fused_decode_step(seq_id, query_states, key_states, value_states, self.num_key_value_groups,
+                                        self.scaling)
+        if out is not None:
+            attn_output = self.o_proj(out.reshape(*input_shape, -1).contiguous())
+            runtime.profile_end("decode_total_ms", decode_total_start)
+            return attn_output, None
     start = runtime.profile_start()
     allocated_new_block = runtime.append_to_layer(seq_id, key_states, value_states)
     runtime.profile_end("decode_kv_append_ms", start)
-    output_attentions = bool(kwargs.get("output_attentions", False))
-    mask_safe = bool(kwargs.get("tierkv_triton_mask_safe", False))
     run_policy = runtime.should_run_decode_policy(seq_id, allocated_new_block)
     collect_scores = runtime.should_collect_decode_scores(seq_id, run_policy)
     use_kernel = (runtime.attention_backend == "triton" and not output_attentions and mask_safe

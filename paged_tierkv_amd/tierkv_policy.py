@@ -51,6 +51,7 @@ stay the same across calls on one device.
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import os
 from dataclasses import dataclass
 
@@ -1309,6 +1310,84 @@ class CompactTieredKVTensorPool(_PoolBase):
         if where is not None:
             self._tables.set(self._t_len, where[0], where[1], pos + 1)
 
+    def _decode_step(self, layer_idx: int, physical_idx: int, pos: int, num_blocks: int, query_states, key_states,
+                     value_states, num_key_value_groups: int, scaling: float, cache: dict):
+        """_append_token's token write and table update, the queued table
+        entries and the layer's decode launch as one tierkv_decode_step call.
+        Returns the attention output, or None (nothing done) when the step is
+        not the plain case: an fp16 token into a HOT block with room, nothing
+        queued, at most 16 table entries to push, tensors as the cached launch
+        was validated for."""
+        from . import tierkv_hip
+        b = self._blocks.get(physical_idx)
+        where = self._where.get(physical_idx)
+        tables = self._tables
+        if (b is None or b.state != HOT_STATE or where is None or tables is None or self._depth or self._q_write
+                or self._q_stage or self._q_dem or self._q_pro or not 0 <= pos < self.block_size
+                or len(tables.pending) > _INLINE_PAIRS - 1):
+            return None
+        if (key_states.dtype != torch.float16 or value_states.dtype != torch.float16 or key_states.ndim != 4
+                or key_states.shape != value_states.shape or key_states.shape[0] != 1
+                or key_states.shape[1] != self.kv_heads or key_states.shape[-1] != self.head_dim
+                or not key_states.is_cuda or key_states.device != self.device
+                or not key_states.is_contiguous() or not value_states.is_contiguous()
+                or not query_states.is_contiguous()):
+            return None
+        self._before_decode()
+        # The cached launch holds the tensors it was bound to, so a replaced
+        # pool (growth) is a different object and binds anew.
+        tensors = (self.hot_k_pool, self.hot_v_pool, self.warm_k_pool, self.warm_v_pool, self.k_scale, self.k_zero,
+                   self.v_scale, self.v_zero)
+        key = (query_states.dtype, tuple(query_states.shape), int(num_key_value_groups), float(scaling))
+        entry = cache.get(layer_idx)
+        if entry is None or entry[0] != key or any(a is not t for a, t in zip(entry[1], tensors)):
+            # Validate the launch once with the ordinary binding (it raises
+            # what tierkv_decode_attention raises) and keep its arguments.
+            args = tierkv_hip._bind(
+                query_states, tables.row_view(self._t_table, layer_idx), tables.row_view(self._t_state, layer_idx),
+                tables.row_view(self._t_len, layer_idx), self.hot_k_pool, self.hot_v_pool, self.warm_k_pool,
+                self.warm_v_pool, self.k_scale, self.k_zero, self.v_scale, self.v_zero, num_blocks,
+                num_key_value_groups, scaling, False, cold_mode="zero_logit")[0]
+            st = _lib.DecodeStep()
+            (_, st.query_dtype, _, _, st.block_table, st.block_states, st.block_lengths, st.table_stride, _, _,
+             st.hot_k, st.hot_v, st.hot_slots, st.warm_k, st.warm_v, st.warm_slots, st.k_scale, st.k_zero,
+             st.v_scale, st.v_zero, st.warm_format, st.cold_mode, st.batch, st.num_heads, st.num_kv_heads,
+             st.block_size, st.head_dim, st.scaling, st.splits_hint) = args[:29]
+            st.table_dst = _lib.ptr(tables.dev)
+            st.table_len = tables.dev.numel()
+            st.src_seqs, st.n_jobs, st.zero_tail = 1, 1, 0
+            st.jobs[0][0], st.jobs[0][1], st.jobs[0][2] = 0, 0, 1   # src_seq, src_tok, count
+            entry = cache[layer_idx] = (key, tensors, st, {}, ctypes.byref(st), st.jobs[0])
+        st, needs, st_ref, job = entry[2], entry[3], entry[4], entry[5]
+        n = int(num_blocks)
+        if not 0 < n <= st.table_stride:
+            return None
+        need = needs.get(n)
+        lib = _lib.lib()
+        if need is None:
+            need = needs[n] = lib.tierkv_decode_workspace_bytes(st.batch, st.num_heads, st.num_kv_heads, n,
+                                                                st.block_size, st.head_dim, 0, st.splits_hint)
+            if need < 0:
+                return None
+        ws = tierkv_hip.stream_workspace(self.device)
+        ws.reserve(need)
+        out = torch.empty((1, 1, st.num_heads, st.head_dim), device=self.device, dtype=query_states.dtype)
+        # Host state first, as the general path records it before launching.
+        self._blocks[physical_idx] = _Block(HOT_STATE, b.slot, pos + 1)
+        tables.set(self._t_len, where[0], where[1], pos + 1)
+        pending = tables.pending
+        for i, (flat, value) in enumerate(pending.items()):
+            st.pairs[i][0], st.pairs[i][1] = flat, value
+        st.n_pairs = len(pending)
+        pending.clear()
+        st.src_k, st.src_v = key_states.data_ptr(), value_states.data_ptr()
+        st.src_tokens = key_states.shape[2]
+        job[3], job[4] = b.slot, pos
+        st.query, st.out, st.num_blocks = query_states.data_ptr(), out.data_ptr(), n
+        st.workspace, st.workspace_bytes = ws.data_ptr(), ws.nbytes
+        _lib.check(lib.tierkv_decode_step(st_ref, _lib.stream_of(self.device)), "tierkv_decode_step")
+        return out
+
     def _write_warm_range(self, physical_idx, src_k, src_v, tok0, length) -> None:
         if src_k.ndim != 4 or src_k.shape[0] != 1:
             raise ValueError("KV tensors must have shape [1, kv_heads, tokens, head_dim].")
@@ -1715,6 +1794,7 @@ class TieredKVRuntime:
 
     def _restart(self) -> None:
         self.layer_states = {layer_idx: LayerRuntimeState() for layer_idx in range(self.num_layers)}
+        self._step_cache: dict = {}   # layer -> the validated one-call decode launch (fused_decode_step)
         self.decode_step = 0
         self.current_query_length = 0
         self.policy_tick_this_forward = False
@@ -1902,6 +1982,32 @@ class TieredKVRuntime:
     def get_layer_table(self, seq_id: int):
         table, states = self.kv_pool.get_layer_table(seq_id)
         return table, states, self.kv_pool.get_layer_lengths(seq_id), self.layer_states[seq_id].num_blocks
+
+    def fused_decode_step(self, seq_id: int, query_states, key_states, value_states, num_key_value_groups: int,
+                          scaling: float):
+        """The decode forward's append_to_layer, get_layer_table and
+        tierkv_decode_attention (modeling_llama.py:419-456) as one C call,
+        for the steps that are nothing else: the token goes into the layer's
+        open HOT block, no block is allocated, and no policy runs and no
+        scores are collected.  Returns the attention output [1, 1, H, D], or
+        None (nothing done) for any other step, which then takes the general
+        path; both leave the same state."""
+        if self._tiered(seq_id) and (self.policy_tick_this_forward or self.score_accumulation_mode == "every_step"):
+            return None
+        if (self._timer.enabled or _lib.env_flag("TIERKV_CHECK_ERRORS") or os.environ.get("TIERKV_FUSED_STEP") == "0"
+                or not hasattr(self.kv_pool, "_decode_step")):
+            return None
+        cursor = self.layer_states[seq_id]
+        p = cursor.open_physical_idx
+        if p is None or key_states.shape[-2] != 1 or value_states.shape[-2] != 1:
+            return None
+        out = self.kv_pool._decode_step(seq_id, p, cursor.open_token_count, cursor.num_blocks, query_states,
+                                        key_states, value_states, num_key_value_groups, scaling, self._step_cache)
+        if out is not None:
+            cursor.open_token_count += 1
+            if cursor.open_token_count == self.block_size:
+                cursor.open_physical_idx, cursor.open_token_count = None, 0
+        return out
 
     # -- policy ---------------------------------------------------------------
     def _tiered(self, seq_id: int) -> bool:

@@ -94,6 +94,44 @@ def test_dropin_tiered_kernel_matches_eager_backend(model, device):
     assert m["warm_blocks"] > 0 and m["logical_compression_x"] > 1.0
 
 
+def test_dropin_fused_step_matches_general_path(model, device, monkeypatch):
+    # The one-call decode step (append, table update and decode launch in
+    # tierkv_decode_step) against the general path of three calls: the same
+    # logits and HOT pool contents (to the decode kernel's run-to-run
+    # rounding, which reaches the later tokens' K/V through the hidden
+    # states), the same tables, WARM pools (written by the prefill) and block
+    # cursors.
+    print("[hf] drop-in fused decode step vs three calls", flush=True)
+    ids = _tokens(1, device)
+    kw = dict(hot_budget=3, policy_interval=10_000, policy_mode="hot_warm", attention_backend="triton")
+    rt_f = _dropin_runtime(model, **kw)
+    taken = []
+    orig = rt_f.fused_decode_step
+
+    def counted(*a, **k):
+        out = orig(*a, **k)
+        taken.append(out is not None)
+        return out
+
+    monkeypatch.setattr(rt_f, "fused_decode_step", counted)
+    got = _teacher_forced(model, ids, rt_f.cache)
+    monkeypatch.setenv("TIERKV_FUSED_STEP", "0")
+    rt_g = _dropin_runtime(model, **kw)
+    ref = _teacher_forced(model, ids, rt_g.cache)
+    assert sum(taken) >= STEPS * model.config.num_hidden_layers // 2 and not all(taken)
+    torch.testing.assert_close(got, ref, atol=2e-3, rtol=2e-3)
+    pf, pg = rt_f.kv_pool, rt_g.kv_pool
+    for k in range(pf._tables.shape[1]):
+        assert torch.equal(pf._tables.view(k), pg._tables.view(k))
+    torch.testing.assert_close(pf.hot_k_pool, pg.hot_k_pool, atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(pf.hot_v_pool, pg.hot_v_pool, atol=2e-2, rtol=2e-2)
+    assert torch.equal(pf.warm_k_pool, pg.warm_k_pool) and torch.equal(pf.warm_v_pool, pg.warm_v_pool)
+    for layer in range(model.config.num_hidden_layers):
+        cf, cg = rt_f.layer_states[layer], rt_g.layer_states[layer]
+        assert (cf.open_physical_idx, cf.open_token_count, cf.num_blocks) == \
+            (cg.open_physical_idx, cg.open_token_count, cg.num_blocks)
+
+
 def test_dropin_policy_ticks_run(model, device):
     print("[hf] drop-in hot_warm_cold with ticks", flush=True)
     ids = _tokens(1, device)
