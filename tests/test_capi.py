@@ -76,3 +76,36 @@ def test_missing_library_raises_runtime_error(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libtierkv_hip.so")
     with pytest.raises(RuntimeError, match="not built"):
         _lib.lib()
+
+
+def test_decode_step_struct_layout_matches_header(tmp_path):
+    """Every TierkvDecodeStep field sits where the ctypes mirror puts it:
+    offsets printed by a C program compiled against the header."""
+    fields = [name for name, _ in _lib.DecodeStep._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "tierkv_hip.h"\nint main(void) {\n'
+                   '  printf("%zu\\n", sizeof(TierkvDecodeStep));\n'
+                   + "".join(f'  printf("%zu\\n", offsetof(TierkvDecodeStep, {f}));\n' for f in fields)
+                   + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                    str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got[0] == ctypes.sizeof(_lib.DecodeStep) == _lib.lib().tierkv_decode_step_size()
+    assert got[1:] == [getattr(_lib.DecodeStep, f).offset for f in fields]
+
+
+def test_decode_step_rejects_bad_counts_without_gpu():
+    lib = _lib.lib()
+    assert lib.tierkv_decode_step(None, None) == _lib.TIERKV_ERR_INVALID
+    assert "null" in _lib.last_error()
+    st = _lib.DecodeStep()
+    st.n_jobs = 5
+    assert lib.tierkv_decode_step(ctypes.byref(st), None) == _lib.TIERKV_ERR_INVALID
+    assert "write jobs" in _lib.last_error()
+    st.n_jobs, st.n_pairs = 0, 17
+    assert lib.tierkv_decode_step(ctypes.byref(st), None) == _lib.TIERKV_ERR_INVALID
+    assert "table writes" in _lib.last_error()
+    st.n_jobs, st.n_pairs = 1, 0   # a write job with no source or pool pointers
+    assert lib.tierkv_decode_step(ctypes.byref(st), None) == _lib.TIERKV_ERR_INVALID
+    assert "null" in _lib.last_error()
