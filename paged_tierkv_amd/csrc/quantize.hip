@@ -403,6 +403,18 @@ __device__ __forceinline__ float div_rn_by_unsigned_zero(float x, float s, float
 
 constexpr float kRcp255 = 1.f / 255.f;   // RN(1 / 255)
 
+// RN(1 / s) for s a positive finite fp16 value held as fp32: the hardware
+// reciprocal (within one ulp) and one FMA Newton step.  The residual
+// 1 - s y0 is exact, the step leaves y0 (2 - s y0) within 2^-44 of 1 / s,
+// and 1 / s lies at least 2^-36 (relative) from every fp32 rounding
+// midpoint because s has an 11-bit significand, so the result is the
+// correctly rounded reciprocal.  tests/native/rcp_newton_check.c checks
+// every such s from both one-ulp neighbours of RN(1 / s) and itself.
+__device__ __forceinline__ float rcp_rn_f16_value(float s) {
+  const float y0 = __builtin_amdgcn_rcpf(s);
+  return __builtin_fmaf(__builtin_fmaf(-s, y0, 1.f), y0, y0);
+}
+
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 // Min and max of a token row held by 2^r_log2 consecutive lanes (8 fp16
@@ -443,8 +455,11 @@ __device__ __forceinline__ void row_min_max(const u32x4& w, int r_log2, float& m
   mx = -static_cast<float>(m[1]);
 }
 
-template <int NV>
-__global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_t n_jobs, int32_t r_log2) {
+// RL >= 0: r_log2 is RL (the common head dims, so the row reduction has no
+// runtime branches); RL < 0: r_log2 comes from the argument.
+template <int NV, int RL>
+__global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_t n_jobs, int32_t r_log2_arg) {
+  const int r_log2 = RL >= 0 ? RL : r_log2_arg;
   const int lane = threadIdx.x & 63;
   const int tiles_per_job = 2 * q.kv_heads;
   const int64_t tile = int64_t(blockIdx.x) * (QT / 64) + (threadIdx.x >> 6);
@@ -495,7 +510,7 @@ __global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_
       if (sc == 0.f) sc = 1.f;                            // torch.where(scale == 0, 1, scale)
       float qt[8], qm;
       if (__builtin_isfinite(sc)) {
-        const float y = __fdiv_rn(1.f, sc);
+        const float y = rcp_rn_f16_value(sc);   // sc: a positive finite fp16 value
         qm = div_rn_by(mn, sc, y);
 #pragma unroll
         for (int e = 0; e < 8; ++e) qt[e] = div_rn_by_unsigned_zero(xs[e], sc, y);
@@ -718,10 +733,13 @@ int32_t launch_demote(const QuantJobs& q, int n_grid, int32_t warm_format, hipSt
       return check_launch("demote_ref_kernel");
     }
     const dim3 wgrid(static_cast<unsigned>((tiles + QT / 64 - 1) / (QT / 64)));
-    if (nv == 1) hipLaunchKernelGGL(demote_ref_wave_kernel<1>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
-    else if (nv == 2) hipLaunchKernelGGL(demote_ref_wave_kernel<2>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
-    else if (nv == 4) hipLaunchKernelGGL(demote_ref_wave_kernel<4>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
-    else hipLaunchKernelGGL(demote_ref_wave_kernel<8>, wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    // Head dim 128 / 64 with 16-token blocks: 16 / 8 lanes per row.
+    if (nv == 4 && rl == 4) hipLaunchKernelGGL((demote_ref_wave_kernel<4, 4>), wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else if (nv == 2 && rl == 3) hipLaunchKernelGGL((demote_ref_wave_kernel<2, 3>), wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else if (nv == 1) hipLaunchKernelGGL((demote_ref_wave_kernel<1, -1>), wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else if (nv == 2) hipLaunchKernelGGL((demote_ref_wave_kernel<2, -1>), wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else if (nv == 4) hipLaunchKernelGGL((demote_ref_wave_kernel<4, -1>), wgrid, dim3(QT), 0, stream, q, n_grid, rl);
+    else hipLaunchKernelGGL((demote_ref_wave_kernel<8, -1>), wgrid, dim3(QT), 0, stream, q, n_grid, rl);
     return check_launch("demote_ref_wave_kernel");
   }
   return fail(TIERKV_ERR_INVALID, "unknown warm format");

@@ -24,3 +24,17 @@ def test_markstein_correction_equals_ieee_division(tmp_path):
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
     assert res.returncode == 0, res.stdout + res.stderr
     assert res.stdout.strip() == "pairs 2015299584 mismatches 0"
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_reciprocal_newton_step_is_correctly_rounded(tmp_path):
+    """The per-row reciprocal RN(1 / s) the correction above needs comes from
+    the hardware reciprocal (within one ulp) and one FMA Newton step:
+    tests/native/rcp_newton_check.c checks every positive finite fp16 s with
+    each starting value within one ulp."""
+    exe = tmp_path / "rcp_newton_check"
+    src = os.path.join(HERE, "native", "rcp_newton_check.c")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", src, "-o", str(exe), "-lm"], check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert res.stdout.strip() == "cases 95229 mismatches 0"
