@@ -284,6 +284,36 @@ def test_c2_reference_codec_round_trip_bit_exact(device):
     _eq(states.cpu().numpy(), exp_states.numpy(), "C2 promote states")
 
 
+@pytest.mark.parametrize("dim", [128, 64])
+def test_reference_codec_every_scale(device, dim):
+    """One token row per positive finite fp16 maximum M (row minimum 0, so
+    the row's scale is fp16(M / 255)): the quotients of every reachable
+    scale go through the per-row reciprocal (hardware reciprocal plus a
+    Newton step) and the FMA correction on the GPU itself; codes, scales and
+    zero points must equal the oracle's bit for bit."""
+    print(f"[quant] ref_u8 every scale dim={dim}", flush=True)
+    m = np.arange(1, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)   # every positive finite fp16
+    rows = int(np.ceil(m.size / 32)) * 32                                            # whole [2 heads, 16 tokens] tiles
+    m = np.concatenate([m, np.ones(rows - m.size, np.float32)])
+    u = np.random.default_rng(31).random((rows, dim), dtype=np.float32)
+    x = (m[:, None] * u).astype(np.float16)
+    x[:, 0] = 0.0
+    x[:, 1] = m.astype(np.float16)
+    x = torch.from_numpy(x.reshape(rows // 32, 2, 16, dim))
+    n = x.shape[0]
+    idx = torch.arange(n, dtype=torch.int32)
+    warm = torch.zeros((n, 2, 16, dim), dtype=torch.uint8, device=device)
+    meta = [torch.zeros((n, 2, 16, 1), dtype=torch.float16, device=device) for _ in range(4)]
+    xd = x.to(device)
+    kernels.demote_to_warm(xd, xd, idx, idx, torch.full((n,), 16, dtype=torch.int32), warm, warm.clone(), *meta,
+                           warm_format="ref_u8")
+    torch.cuda.synchronize()
+    q, sc, zp = codec.quantize_ref_u8(x.numpy())
+    assert len(np.unique(sc)) > 20000                     # most fp16 scale values are reached
+    _eq(meta[0].cpu().numpy(), sc, "every-scale scales")
+    _eq(meta[1].cpu().numpy(), zp, "every-scale zero points")
+    _eq(warm.cpu().numpy(), q, "every-scale codes")
+
 def test_absmax_promote_bit_exact(device):
     g = torch.Generator().manual_seed(4)
     codes = torch.randint(-127, 128, (5, 2, 16, 128), generator=g, dtype=torch.int8)
