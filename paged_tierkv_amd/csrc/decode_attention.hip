@@ -1285,7 +1285,9 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
 // the blanks and added in integers.  The row is written up to the table
 // stride (zeros past the sequence's block count).
 // --------------------------------------------------------------------------
-constexpr int FIN_THREADS = 512;
+// 1024 threads per row: the row's loads and writes spread over sixteen waves
+// (C4 with scores: 38.8 -> 38.4 us per step against 512 threads).
+constexpr int FIN_THREADS = 1024;
 constexpr int FIN_LDS_BLOCKS = 4096;
 
 // All arguments fit the preloaded kernel-argument registers, so the row's
