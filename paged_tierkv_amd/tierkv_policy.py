@@ -1310,6 +1310,35 @@ class CompactTieredKVTensorPool(_PoolBase):
         if where is not None:
             self._tables.set(self._t_len, where[0], where[1], pos + 1)
 
+    def _fused_inputs_ok(self, query_states, key_states, value_states, new_pairs: int) -> bool:
+        """_decode_step's conditions that do not depend on the block: nothing
+        queued, room in the inline table writes for new_pairs more entries,
+        one contiguous fp16 token per kv head in the pool's geometry."""
+        tables = self._tables
+        if (tables is None or self._depth or self._q_write or self._q_stage or self._q_dem or self._q_pro
+                or len(tables.pending) + new_pairs > _INLINE_PAIRS - 1):
+            return False
+        return not (key_states.dtype != torch.float16 or value_states.dtype != torch.float16 or key_states.ndim != 4
+                    or key_states.shape != value_states.shape or key_states.shape[0] != 1
+                    or key_states.shape[1] != self.kv_heads or key_states.shape[-1] != self.head_dim
+                    or key_states.shape[2] != 1 or not key_states.is_cuda or key_states.device != self.device
+                    or not key_states.is_contiguous() or not value_states.is_contiguous()
+                    or not query_states.is_contiguous())
+
+    def _open_hot(self, physical_idx: int, src_k) -> None:
+        """_write_hot_range's placement of a new block's first token for a
+        decode step that writes the token in its own launch: the HOT slot and
+        the ledger entry (one token), mirrored into the tables as the general
+        path does, with no queued write."""
+        self._adopt_geometry(src_k)
+        held = self.get_physical_state(physical_idx)
+        if held == COLD_STATE:
+            raise KeyError(f"Physical block {physical_idx} is COLD and cannot be promoted.")
+        if held == WARM_STATE:
+            self.promote_to_hot(physical_idx)
+        slot = self._hot.take() if held is None else self._blocks[physical_idx].slot
+        self._record(physical_idx, HOT_STATE, slot, 1)
+
     def _decode_step(self, layer_idx: int, physical_idx: int, pos: int, num_blocks: int, query_states, key_states,
                      value_states, num_key_value_groups: int, scaling: float, cache: dict):
         """_append_token's token write and table update, the queued table
@@ -1322,16 +1351,8 @@ class CompactTieredKVTensorPool(_PoolBase):
         b = self._blocks.get(physical_idx)
         where = self._where.get(physical_idx)
         tables = self._tables
-        if (b is None or b.state != HOT_STATE or where is None or tables is None or self._depth or self._q_write
-                or self._q_stage or self._q_dem or self._q_pro or not 0 <= pos < self.block_size
-                or len(tables.pending) > _INLINE_PAIRS - 1):
-            return None
-        if (key_states.dtype != torch.float16 or value_states.dtype != torch.float16 or key_states.ndim != 4
-                or key_states.shape != value_states.shape or key_states.shape[0] != 1
-                or key_states.shape[1] != self.kv_heads or key_states.shape[-1] != self.head_dim
-                or not key_states.is_cuda or key_states.device != self.device
-                or not key_states.is_contiguous() or not value_states.is_contiguous()
-                or not query_states.is_contiguous()):
+        if (b is None or b.state != HOT_STATE or where is None or not 0 <= pos < self.block_size
+                or not self._fused_inputs_ok(query_states, key_states, value_states, 0)):
             return None
         self._before_decode()
         # The cached launch holds the tensors it was bound to, so a replaced
@@ -1987,10 +2008,10 @@ class TieredKVRuntime:
                           scaling: float):
         """The decode forward's append_to_layer, get_layer_table and
         tierkv_decode_attention (modeling_llama.py:419-456) as one C call,
-        for the steps that are nothing else: the token goes into the layer's
-        open HOT block, no block is allocated, and no policy runs and no
-        scores are collected.  Returns the attention output [1, 1, H, D], or
-        None (nothing done) for any other step, which then takes the general
+        for the steps that are nothing else: one token into the layer's open
+        HOT block or into a block it opens, no policy due and no scores
+        collected.  Returns the attention output [1, 1, H, D], or None
+        (nothing done) for any other step, which then takes the general
         path; both leave the same state."""
         if self._tiered(seq_id) and (self.policy_tick_this_forward or self.score_accumulation_mode == "every_step"):
             return None
@@ -1999,8 +2020,17 @@ class TieredKVRuntime:
             return None
         cursor = self.layer_states[seq_id]
         p = cursor.open_physical_idx
-        if p is None or key_states.shape[-2] != 1 or value_states.shape[-2] != 1:
+        if key_states.shape[-2] != 1 or value_states.shape[-2] != 1:
             return None
+        if p is None:
+            # The token opens a block: placed as append_to_layer places it
+            # (BlockManager id, HOT slot, table entry), unless the allocation
+            # itself is due to run the policy.
+            if self.policy_on_new_block and self._tiered(seq_id):
+                return None
+            if not self.kv_pool._fused_inputs_ok(query_states, key_states, value_states, 4):
+                return None
+            p = self._open_block(seq_id, cursor, key_states)
         out = self.kv_pool._decode_step(seq_id, p, cursor.open_token_count, cursor.num_blocks, query_states,
                                         key_states, value_states, num_key_value_groups, scaling, self._step_cache)
         if out is not None:
@@ -2008,6 +2038,22 @@ class TieredKVRuntime:
             if cursor.open_token_count == self.block_size:
                 cursor.open_physical_idx, cursor.open_token_count = None, 0
         return out
+
+    def _open_block(self, seq_id: int, cursor: LayerRuntimeState, key_states) -> int:
+        """_placements' block opening and append_to_layer's placement of its
+        first token, for a token the decode step's own launch writes: the
+        BlockManager id, the HOT slot (the token counted), the table entry."""
+        p = self.block_manager.allocate_block(seq_id)
+        cursor.open_physical_idx, cursor.open_token_count = p, 0
+        new_logical = cursor.num_blocks
+        if new_logical >= self.max_blocks_per_layer:
+            raise RuntimeError(f"Layer {seq_id} exceeded max_blocks_per_layer={self.max_blocks_per_layer}.")
+        pool = self.kv_pool
+        pool._check_physical_idx(p)
+        pool._open_hot(p, key_states)
+        pool.set_block_entry(seq_id, new_logical, p, HOT_STATE)
+        cursor.num_blocks += 1
+        return p
 
     # -- policy ---------------------------------------------------------------
     def _tiered(self, seq_id: int) -> bool:
