@@ -828,6 +828,12 @@ class _PoolBase(_QueuedStorage):
         self._require_allocated()
         self._tables.set(self._t_state, layer_idx, logical_idx, int(state))
 
+    def _state_settled(self, layer_idx: int, logical_idx: int, physical_idx: int, state: int) -> bool:
+        """Whether retier(physical_idx, state) and set_block_state(layer_idx,
+        logical_idx, state) would both do nothing now (allocated pools)."""
+        return (_RETIER.get((int(state), self.get_physical_state(physical_idx))) is None
+                and int(self._tables.host[layer_idx, self._t_state, logical_idx]) == int(state))
+
     # -- telemetry ----------------------------------------------------------
     def _tensor_bytes_mb(self, names) -> float:
         return sum(self._tensor_mb(getattr(self, n)) for n in names)
@@ -1995,8 +2001,11 @@ class TieredKVRuntime:
         one promote launch, one table push."""
         pool = self.kv_pool
         pairs = zip(self.block_manager.get_physical_indices(seq_id), self.block_manager.get_states(seq_id))
+        settled = pool._state_settled if pool.is_allocated() and pool._tables is not None else None
         with pool._batch():
             for logical_idx, (physical_idx, state) in enumerate(pairs):
+                if settled is not None and settled(seq_id, logical_idx, physical_idx, state):
+                    continue   # both calls below would do nothing
                 pool.retier(physical_idx, state)
                 pool.set_block_state(seq_id, logical_idx, state)
 
