@@ -21,6 +21,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -714,6 +715,28 @@ def c5_generate(model, prompt, cache, steps, runtime=None):
     return torch.cat(toks, dim=1), sec, cache
 
 
+def synced_step_ms(model, prompt, cache, steps):
+    """Prefill, then `steps` greedy decode steps with a device sync after
+    each; returns the wall time of every step in ms (the per-step view of
+    c5_generate's run: which steps cost more, not the pipelined rate)."""
+    import torch
+
+    out_ms = []
+    with torch.no_grad():
+        out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        cache = out.past_key_values
+        tok = out.logits[:, -1].argmax(-1, keepdim=True)
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            out = model(input_ids=tok, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            cache = out.past_key_values
+            tok = out.logits[:, -1].argmax(-1, keepdim=True)
+            torch.cuda.synchronize()
+            out_ms.append((time.perf_counter() - t0) * 1e3)
+    return out_ms
+
+
 REF_METRIC = ("reference-API drop-in end-to-end decode tokens/s, TinyLlama-1.1B shape, batch 1, HOT+WARM, "
               "hot budget 8, policy every 64")
 # The reference's own number for this setting (TierKV Triton path, HOT+WARM,
@@ -768,12 +791,24 @@ def run_ref(args, device):
     tps = steps / sec
     metrics = rt.collect_memory_metrics() if hasattr(rt, "collect_memory_metrics") else {}
     log(f"[ref] drop-in: {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step)")
+    # Per-step view (a sync after every step): plain steps against the policy
+    # steps (every 64th), beside the same view of stock dense.
+    per_step = synced_step_ms(model, prompt, runtime().cache, steps)
+    policy_idx = [i for i in range(steps) if (i + 1) % 64 == 0]
+    plain = [t for i, t in enumerate(per_step) if i not in policy_idx and i > 0]
+    synced = {"drop_in_plain_step_median_ms": round(statistics.median(plain), 3),
+              "drop_in_policy_step_mean_ms": (round(statistics.mean(per_step[i] for i in policy_idx), 3)
+                                              if policy_idx else None),
+              "drop_in_first_step_ms": round(per_step[0], 3)}
     dense = None
     if not args.no_dense_baseline:
         c5_generate(model, prompt[:, :64], DynamicCache(config=cfg), 8)
         _, dsec, _ = c5_generate(model, prompt, DynamicCache(config=cfg), steps)
         dense = {"tokens_per_s": round(steps / dsec, 1), "ms_per_step": round(dsec / steps * 1e3, 3)}
+        synced["dense_step_median_ms"] = round(statistics.median(synced_step_ms(model, prompt,
+                                                                                 DynamicCache(config=cfg), steps)), 3)
         log(f"[ref] dense: {dense['tokens_per_s']} tok/s")
+    log(f"[ref] synced steps: {synced}")
     hf_llama.uninstall()
     tp.reset_global_tierkv()
     pub = REF_PUBLISHED_A10G.get(T)
@@ -783,7 +818,7 @@ def run_ref(args, device):
                   "warm_format": "reference uint8 per-token asymmetric", "cold": "zero_logit",
                   "runtime": "reference-API drop-in (tierkv_policy.TieredKVRuntime) through the HF hooks",
                   "decode_steps_as": "eager"},
-                 dense_hf_baseline=dense,
+                 dense_hf_baseline=dense, synced_steps=synced,
                  reference_published=({"tokens_per_s": pub, "hardware": "NVIDIA A10G",
                                        "source": "FINAL_EVALUATION_RESULTS.md:83-88"} if pub else None))
     line["data"] = "synthetic: random-init weights N(0, 0.02), uniform random prompt ids"
