@@ -49,12 +49,14 @@ constexpr int MAX_LDS_STAGE = 48 * 1024;   // bytes of per-block score statistic
 // Where a score launch stages each block's (max, sum) per head:
 //   STAGE_LDS_BLOCK LDS [G][num_blocks] by logical block (unsplit launches),
 //                   finalised by the workgroup itself;
-//   STAGE_LDS_LIST  LDS [G][stage_cap] by list position, copied to the
+//   STAGE_LDS_LIST  LDS [G][MAX_LIST] by list position, copied to the
 //                   workspace [B][H][num_blocks] at the end of the workgroup
 //                   (split launches);
 //   STAGE_GLOBAL    the workspace, written per tile (rows too long for LDS).
-// The workspace stages (resident blocks only) are finalised by
-// finalize_scores_kernel, launched after the decode kernel.
+// The workspace stages are finalised by finalize_scores_kernel, launched
+// after the decode kernel: one workgroup per (sequence, q head) row spreads
+// that work over the chip, where a unit's last workgroup would read every
+// staged pair of the unit and write its whole score rows from one CU.
 constexpr int STAGE_GLOBAL = 0;
 constexpr int STAGE_LDS_BLOCK = 1;
 constexpr int STAGE_LDS_LIST = 2;
@@ -92,7 +94,6 @@ struct DecodeParams {
   int32_t splits;
   uint32_t split_magic;   // ceil(2^32 / splits) when num_blocks * splits < 2^32, else 0
   int32_t lds_stage;      // where score statistics are staged (STAGE_* below)
-  int32_t stage_cap;      // STAGE_LDS_LIST: entries per head in the LDS stage
   float* ws_acc;      // [units][splits][G][D]
   float* ws_ml;       // [units][splits][G][2]
   float* ws_stage;    // [B][H][num_blocks][2]  per-block (max, sum) (split score launches)
@@ -127,6 +128,15 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
 }
 __device__ __forceinline__ float load_dev(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// waits for the wave's outstanding global stores (on gfx9 they count in the
+// same vector-memory counter as loads), which the score finalisation would
+// otherwise pay for right after the output stores.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // --------------------------------------------------------------------------
@@ -330,7 +340,7 @@ __device__ __forceinline__ void softmax_step(const DecodeParams& p, const float*
       if (s_stage) {
         // LDS stage [G][row] of (max, sum) at this tile's stage index (its
         // logical block or its list position); lane n < G is head n.
-        const int row = (p.lds_stage == STAGE_LDS_LIST) ? p.stage_cap : p.num_blocks;
+        const int row = (p.lds_stage == STAGE_LDS_LIST) ? MAX_LIST : p.num_blocks;
         reinterpret_cast<float2*>(s_stage)[(lane & 15) * row + si] = make_float2(bm, bs);
       } else {
         // Workspace stage, read by the finalisation kernel after this launch.
@@ -546,6 +556,34 @@ __device__ __forceinline__ void wave_combine_ms(float& m, float& s) {
   combine_ms(m, s, xor32_f(m), xor32_f(s));
 }
 
+// One lane's share of a score part (below): its entries j = 0, 1, ...
+// (blocks lo + lane + 64 j) in rounds of FOLD_ROUND; a round is reduced by a
+// balanced binary tree over its FOLD_ROUND slots and the rounds are combined
+// into (m, s) in ascending order.  Slots past the lane's entries, and blocks
+// without a tile (max -inf), are the identity (-inf, 0), which combine_ms
+// leaves exact, so a round reduced over U < FOLD_ROUND slots (U a power of
+// two covering the lane's entries) gives the same bits as the full tree.  The
+// tree's levels are independent combines, where a sequential fold would be
+// one dependent chain of exponentials per lane.
+constexpr int FOLD_ROUND = 16;
+
+template <int U>
+__device__ __forceinline__ void fold_round(const float2* e, int live, float& m, float& s) {
+  static_assert(U <= FOLD_ROUND && (U & (U - 1)) == 0, "a round is a power of two of at most FOLD_ROUND slots");
+  float tm[U], ts[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bool use = u < live && e[u].x != -INFINITY;
+    tm[u] = use ? e[u].x : -INFINITY;
+    ts[u] = use ? e[u].y : 0.f;
+  }
+#pragma unroll
+  for (int w2 = 1; w2 < U; w2 *= 2)
+#pragma unroll
+    for (int u = 0; u < U; u += 2 * w2) combine_ms(tm[u], ts[u], tm[u + w2], ts[u + w2]);
+  combine_ms(m, s, tm[0], ts[0]);
+}
+
 // Staged statistics of a block that no tile visits: (-inf, -len) for a COLD
 // block whose tokens enter the softmax (zero-logit mode), (-inf, 0) for one
 // that contributes nothing.
@@ -564,7 +602,7 @@ __device__ __forceinline__ float block_score(float2 e, float M, float inv_l, flo
 
 // Score reduction tree of a head's row: `parts` contiguous ranges of
 // ceil(nb / parts) blocks, one wave each (lane l folds blocks lo + l,
-// lo + l + 64, ... in ascending order, then wave_combine_ms), the parts
+// lo + l + 64, ... with fold_round, then wave_combine_ms), the parts
 // combined in ascending order.  parts = nw / G when the unit's G heads fit
 // in its nw waves, else 1; the decode workgroup and the finalisation kernel
 // both follow it, so score sums do not depend on the launch's split count.
@@ -625,47 +663,51 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // the first row chunk and applied afterwards.
   const int nb_ld = a_seq_nblocks ? a_seq_nblocks[b] : a_num_blocks;
   // Per-block score statistics (max, sum) per head (STAGE_* modes above).
-  const int stage_mode = p.lds_stage;
-  float* s_stage = (SCORES && stage_mode != STAGE_GLOBAL) ? s_dyn + NW * G * D : nullptr;
-  const bool list_stage = SCORES && stage_mode == STAGE_LDS_LIST;
-  float* const gstage_unit = p.ws_stage + (int64_t(b) * p.num_heads + int64_t(kvh) * G) * p.num_blocks * 2;
-  // A block that no tile will visit gets an entry too (stage_blank), so the
-  // staged statistics describe every block below the row's count (the
-  // finalisation kernel reads the pairs alone): in LDS (block stage) for
-  // every head as the list build classifies it; in the workspace from the
-  // split that owns the block (split s: blocks [s * own, (s + 1) * own), so
-  // a wave's stores are contiguous).  The list build's first pass records
-  // its owned blanks in blank_bits (8 bits per entry: blank, COLD, length)
-  // and they are written at the end of the workgroup, where the stores do
-  // not hold up the tile loads' waits; later passes (rows beyond
-  // PRE_CHUNKS * nthreads blocks) write theirs at once.
+  // Nothing the list build does depends on the stage mode, a kernel argument
+  // outside the preloaded ones whose load would hold the build up.  A block
+  // that no tile will visit gets an entry too (stage_blank), so the staged
+  // statistics describe every block below the row's count.  The list build's
+  // first pass records the blanks of its entries in blank_bits (8 bits per
+  // entry: blank, COLD, length); after the tile loops they go to the LDS
+  // block stage, or to the workspace from the split that owns the block
+  // (split s: blocks [s * own, (s + 1) * own), so a wave's stores are
+  // contiguous).  Later passes (rows beyond PRE_CHUNKS * nthreads blocks;
+  // block and workspace stages only) write theirs at once.
   const int own = (a_num_blocks + splits - 1) / splits;
   uint32_t blank_bits = 0;
-  auto store_blank = [&](int idx, int st, int len) {
-    for (int h = 0; h < G; ++h)
-      *reinterpret_cast<float2*>(gstage_unit + (int64_t(h) * p.num_blocks + idx) * 2) = stage_blank<COLD_ZERO>(st, len);
+  auto stage_base = [&]() -> float* {
+    return p.ws_stage + (int64_t(b) * p.num_heads + int64_t(kvh) * G) * p.num_blocks * 2;
   };
-  // blank: the entry is below the row's count and has no tile.  The stage
-  // mode and the pass are uniform; the first pass's bookkeeping is
-  // branch-free.
+  auto lds_blank = [&](int idx, int st, int len) {
+    float2* const ls = reinterpret_cast<float2*>(s_dyn + NW * G * D);
+    for (int h = 0; h < G; ++h) ls[h * p.num_blocks + idx] = stage_blank<COLD_ZERO>(st, len);
+  };
+  auto store_blank = [&](int idx, int st, int len) {
+    float* const gs = stage_base();
+    for (int h = 0; h < G; ++h)
+      *reinterpret_cast<float2*>(gs + (int64_t(h) * p.num_blocks + idx) * 2) = stage_blank<COLD_ZERO>(st, len);
+  };
+  auto owned = [&](int idx) { return uint32_t(idx - split * own) < uint32_t(own); };
+  // blank: the entry is below the row's count and has no tile.  The pass is
+  // uniform; the first pass's bookkeeping is branch-free.
   auto stage_init = [&](bool blank, int idx, int st, int len, int k, bool first_pass) {
-    if (stage_mode == STAGE_LDS_BLOCK) {
-      if (blank)
-        for (int h = 0; h < G; ++h)
-          reinterpret_cast<float2*>(s_stage)[h * p.num_blocks + idx] = stage_blank<COLD_ZERO>(st, len);
-    } else {
-      const bool mine_blank = blank && uint32_t(idx - split * own) < uint32_t(own);
-      if (first_pass)
-        blank_bits |= mine_blank ? uint32_t(1 | ((st == COLD) ? 2 : 0) | (len << 2)) << (8 * k) : 0u;
-      else if (mine_blank)
-        store_blank(idx, st, len);
+    if (first_pass) {
+      blank_bits |= blank ? uint32_t(1 | ((st == COLD) ? 2 : 0) | (len << 2)) << (8 * k) : 0u;
+    } else if (blank) {
+      if (p.lds_stage == STAGE_LDS_BLOCK) lds_blank(idx, st, len);
+      else if (owned(idx)) store_blank(idx, st, len);
     }
   };
-  auto flush_blanks = [&]() {
+  // The first pass's blanks: all of them into the LDS block stage, or the
+  // owned ones into the workspace stage.
+  auto flush_blanks = [&](bool to_lds) {
 #pragma unroll
     for (int k = 0; k < NLD; ++k) {
       const uint32_t e = (blank_bits >> (8 * k)) & 0xffu;
-      if (e & 1u) store_blank(k * nthreads + tid, (e & 2u) ? COLD : HOT, int(e >> 2));
+      const int idx = k * nthreads + tid;
+      if (!(e & 1u)) continue;
+      if (to_lds) lds_blank(idx, (e & 2u) ? COLD : HOT, int(e >> 2));
+      else if (owned(idx)) store_blank(idx, (e & 2u) ? COLD : HOT, int(e >> 2));
     }
   };
   if (tid == 0) {
@@ -814,7 +856,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
           if (cls[k] != 0 && uint32_t(q) < uint32_t(is_hot ? own_h : own_w)) {
             const int idx = k * nthreads + tid;
             const int pos = is_hot ? q : MAX_LIST - 1 - q;
-            s_list[pos] = make_int4(idx, slot[k], len[k], list_stage ? (is_hot ? q : p.stage_cap - 1 - q) : idx);
+            s_list[pos] = make_int4(idx, slot[k], len[k], pos);
           }
         }
         return;
@@ -825,8 +867,6 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         const int j = uniform(k * nw + w);
         const int hb = seen_hot + __builtin_amdgcn_readlane(ih - ch, j);
         const int wb = seen_warm + __builtin_amdgcn_readlane(iw - cw, j);
-        // .w: the entry's stage index (its list position with list staging,
-        // else its logical block).
         const int idx = c0 + k * nthreads + tid;
         const uint64_t mh = __ballot(cls[k] == 1);
         const uint64_t mw = __ballot(cls[k] == 2);
@@ -837,7 +877,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         int q;
         if (cls[k] != 0 && mine(r, q)) {
           const int pos = is_hot ? q : MAX_LIST - 1 - q;
-          s_list[pos] = make_int4(idx, slot[k], len[k], list_stage ? (is_hot ? q : p.stage_cap - 1 - q) : idx);
+          s_list[pos] = make_int4(idx, slot[k], len[k], pos);
         }
       }
       seen_hot += __builtin_amdgcn_readlane(ih, 63);
@@ -892,13 +932,11 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       seen_warm += cw;
     }
     const uint64_t below = (1ull << lane) - 1ull;
-    // .w: the entry's stage index (its list position with list staging, else
-    // its logical block).
     const int r = hot ? hb + __popcll(mh & below) : wb + __popcll(mw & below);
     int q;
     if ((hot || warm) && mine(r, q)) {
       const int pos = hot ? q : MAX_LIST - 1 - q;
-      s_list[pos] = make_int4(idx, slot, len, list_stage ? (hot ? q : p.stage_cap - 1 - q) : idx);
+      s_list[pos] = make_int4(idx, slot, len, pos);
     }
   }
   if (COLD_ZERO) {
@@ -952,6 +990,12 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // (a position past the end reads one cache line for the whole wave and is
   // never processed) and the loops leave only through their latch, so the
   // compiler's wait counts stay exact across iterations.
+  // Score statistics: staged by list position (.w) with the list stage, else
+  // by logical block (.x).
+  const int stage_mode = SCORES ? p.lds_stage : STAGE_GLOBAL;
+  const bool list_stage = SCORES && stage_mode == STAGE_LDS_LIST;
+  float* const s_stage = (SCORES && stage_mode != STAGE_GLOBAL) ? s_dyn + NW * G * D : nullptr;
+  auto stage_index = [&](const int4& e) { return uniform(list_stage ? e.w : e.x); };
   WaveState<D> st;
 #pragma unroll
   for (int s = 0; s < DS; ++s) st.acc[s] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1016,8 +1060,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
         nl = gi < nwarm;
         if (lw[k])
-          process_warm<D, WF, SCORES>(p, tw[k], uniform(ew[k].w), uniform(ew[k].z), lane, head_ok, b, qh, qv, qsum,
-                                      s_stage, st);
+          process_warm<D, WF, SCORES>(p, tw[k], stage_index(ew[k]), uniform(ew[k].z), lane, head_ok, b, qh, qv,
+                                      qsum, s_stage, st);
       }
     } while (lw[0]);   // buffer 0 holds the next tile; positions are handed out in order
   }
@@ -1034,8 +1078,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         hne = s_list[min(gi, nhot - 1)];
         hnl = gi < nhot;
         if (lh[k])
-          process_hot<D, SCORES>(p, th[k], uniform(eh[k].w), uniform(eh[k].z), lane, head_ok, b, qh, qvh, s_stage,
-                                 st);
+          process_hot<D, SCORES>(p, th[k], stage_index(eh[k]), uniform(eh[k].z), lane, head_ok, b, qh, qvh,
+                                 s_stage, st);
       }
     } while (lh[0]);
   }
@@ -1062,7 +1106,11 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
 #pragma unroll
       for (int s = 0; s < DS; ++s) s_acc[(w * G + n) * D + (4 * g + r) * DS + s] = st.acc[s][r] - corr;
   }
-  if (SCORES) __builtin_amdgcn_s_waitcnt(0);   // this wave's per-block statistics are stored
+  if constexpr (SCORES) {
+    // The first pass's blanks into the LDS block stage.
+    if (stage_mode == STAGE_LDS_BLOCK) flush_blanks(true);
+    __builtin_amdgcn_s_waitcnt(0);   // this wave's per-block statistics are stored
+  }
   __syncthreads();
   float cold_tokens = 0.f;
   if (COLD_ZERO) {
@@ -1107,7 +1155,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // score = bs * 2^(bm - M) / L, or len * 2^-M / L for a COLD block of the
   // zero-logit mode.  A lane's entries of a part (up to 16) are loaded
   // together and, when the wave's only part fits in one such round, kept in
-  // registers for the second pass.
+  // registers for the second pass.  The barrier between the passes orders
+  // LDS only, so that no wave waits there for its output stores.
   auto finalize_scores = [&]() {
     const int stride = int(p.table_stride);
     const int parts = score_parts(G, nw);
@@ -1117,7 +1166,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       return reinterpret_cast<const float2*>(s_stage)[h * p.num_blocks + blk];
     };
     // U entries per lane per round; the caller picks the smallest U that
-    // covers a part in one round (rows up to 64 * U blocks per part).
+    // covers a part in one round (rows up to 64 * U blocks per part), else
+    // U = FOLD_ROUND.
     auto run = [&](auto u_const) {
       constexpr int U = decltype(u_const)::value;
       const bool reuse = ntask <= nw && chunk <= 64 * U;
@@ -1130,9 +1180,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         for (int c0 = lo; c0 < hi; c0 += U * 64) {
 #pragma unroll
           for (int u = 0; u < U; ++u) kept[u] = entry(h, min(c0 + u * 64 + lane, hi - 1));
-#pragma unroll
-          for (int u = 0; u < U; ++u)
-            if (c0 + u * 64 + lane < hi) combine_ms(m, sum, kept[u].x, kept[u].y);
+          fold_round<U>(kept, (hi - c0 - lane + 63) / 64, m, sum);
         }
         wave_combine_ms(m, sum);
         if (lane == 0) {
@@ -1140,7 +1188,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
           s_ts[t] = sum;
         }
       }
-      __syncthreads();
+      lds_barrier();
       for (int t = w; t < ntask; t += nw) {
         const int h = t / parts;
         const int k0 = t - h * parts;
@@ -1172,7 +1220,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     };
     if (chunk <= 128) run(std::integral_constant<int, 2>{});
     else if (chunk <= 256) run(std::integral_constant<int, 4>{});
-    else run(std::integral_constant<int, 16>{});
+    else if (chunk <= 512) run(std::integral_constant<int, 8>{});
+    else run(std::integral_constant<int, FOLD_ROUND>{});
   };
 
   if (splits == 1) {
@@ -1185,7 +1234,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
       out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
     }
     if (SCORES && stage_mode == STAGE_LDS_BLOCK) finalize_scores();
-    if (SCORES && stage_mode != STAGE_LDS_BLOCK) flush_blanks();
+    if (SCORES && stage_mode == STAGE_GLOBAL) flush_blanks(false);
     return;
   }
 
@@ -1210,24 +1259,28 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = last ? 1 : 0;
   }
-  // The statistics this workgroup staged in LDS go to the workspace by
-  // logical block, for the finalisation kernel that runs after this launch
-  // (no wait covers these stores; the last workgroup issues them after its
-  // merge, whose loads would otherwise wait behind them).
+  // Score launches: the statistics this workgroup staged in LDS (by list
+  // position) go to the workspace by logical block, and the blanks of the
+  // blocks it owns with them, for the finalisation kernel that runs after
+  // this launch (no wait covers these stores; the last workgroup issues them
+  // after its merge, whose loads would otherwise wait behind them).
   auto flush_stage = [&]() {
-    const int nlist = nhot + nwarm;
-    for (int i = tid; i < G * nlist; i += nthreads) {
-      const int h = i / nlist;
-      const int j = i - h * nlist;
-      const int4 e = (j < nhot) ? s_list[j] : s_list[MAX_LIST - 1 - (j - nhot)];
-      *reinterpret_cast<float2*>(gstage_unit + (int64_t(h) * p.num_blocks + e.x) * 2) =
-          reinterpret_cast<const float2*>(s_stage)[h * p.stage_cap + e.w];
+    if (list_stage) {
+      float* const gs = stage_base();
+      const int nlist = nhot + nwarm;
+      for (int i = tid; i < G * nlist; i += nthreads) {
+        const int h = i / nlist;
+        const int j = i - h * nlist;
+        const int4 e = (j < nhot) ? s_list[j] : s_list[MAX_LIST - 1 - (j - nhot)];
+        *reinterpret_cast<float2*>(gs + (int64_t(h) * p.num_blocks + e.x) * 2) =
+            reinterpret_cast<const float2*>(s_stage)[h * MAX_LIST + e.w];
+      }
     }
+    if (SCORES) flush_blanks(false);
   };
   __syncthreads();
   if (!s_last) {
-    if (list_stage) flush_stage();
-    if (SCORES) flush_blanks();
+    flush_stage();
     return;
   }
   // Log-sum-exp merge of the splits' partials (tierkv_triton.py:231-264).
@@ -1269,8 +1322,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     cold_adjust<COLD_ZERO>(M, L, f, cold_tokens);
     out[i] = from_f32<QT>((L > 0.f) ? A * f / (L * PBOOST) : 0.f);
   }
-  if (list_stage) flush_stage();
-  if (SCORES) flush_blanks();
+  flush_stage();
 }
 
 // --------------------------------------------------------------------------
@@ -1333,18 +1385,15 @@ __global__ __launch_bounds__(FIN_THREADS) void finalize_scores_kernel(const floa
   const int hi = min(nb, lo + chunk);
   float m = -INFINITY, sum = 0.f;
   int cold = 0;
-  constexpr int U = 8;
+  constexpr int U = FOLD_ROUND;
   for (int c0 = lo; c0 < hi; c0 += U * 64) {
     float2 e[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) e[u] = entry(min(c0 + u * 64 + lane, hi - 1));
+    fold_round<U>(e, (hi - c0 - lane + 63) / 64, m, sum);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (c0 + u * 64 + lane < hi) {
-        combine_ms(m, sum, e[u].x, e[u].y);
-        cold += (COLD_ZERO && e[u].y < 0.f) ? int(-e[u].y) : 0;
-      }
-    }
+    for (int u = 0; u < U; ++u)
+      cold += (COLD_ZERO && c0 + u * 64 + lane < hi && e[u].y < 0.f) ? int(-e[u].y) : 0;
   }
   wave_combine_ms(m, sum);
   if (COLD_ZERO) {
@@ -1588,7 +1637,7 @@ template <int D, int WF, bool SC, bool CZ, typename QT, int NW>
 static void launch_nw(const DecodeParams& p, bool long_rows, int grid, hipStream_t stream) {
   size_t shmem = size_t(NW) * p.groups * D * sizeof(float);
   if (SC && p.lds_stage == STAGE_LDS_BLOCK) shmem += size_t(p.groups) * p.num_blocks * 2 * sizeof(float);
-  if (SC && p.lds_stage == STAGE_LDS_LIST) shmem += size_t(p.groups) * p.stage_cap * 2 * sizeof(float);
+  if (SC && p.lds_stage == STAGE_LDS_LIST) shmem += size_t(p.groups) * MAX_LIST * 2 * sizeof(float);
   const int32_t stride = int32_t(p.table_stride);
   const int32_t kvh_splits = int32_t(uint32_t(p.kv_heads) | (uint32_t(p.splits) << 16));
   if (long_rows)
@@ -1750,15 +1799,12 @@ extern "C" int32_t tierkv_decode_attention(
     // split ones stage them in LDS by list position and copy them to the
     // workspace, where finalize_scores_kernel reads them.
     p.lds_stage = STAGE_GLOBAL;
-    p.stage_cap = 0;
     if (scores) {
       const int64_t pair = 2 * int64_t(sizeof(float));
-      const int cap = std::min<int>(MAX_LIST, (num_blocks + pl.splits - 1) / pl.splits + 1);
       if (pl.splits == 1 && int64_t(p.groups) * num_blocks * pair <= MAX_LDS_STAGE) {
         p.lds_stage = STAGE_LDS_BLOCK;
-      } else if (pl.splits > 1 && int64_t(p.groups) * cap * pair <= MAX_LDS_STAGE) {
+      } else if (pl.splits > 1 && int64_t(p.groups) * MAX_LIST * pair <= MAX_LDS_STAGE) {
         p.lds_stage = STAGE_LDS_LIST;
-        p.stage_cap = cap;
       }
     }
     if (pl.splits > 1 && int64_t(num_blocks) * pl.splits < (int64_t(1) << 32))
@@ -1795,8 +1841,9 @@ extern "C" int32_t tierkv_decode_attention(
       else dispatch_fast<__half>(pc, warm_format, scores, cz, pl.nw, grid, stream);
     }
     const int32_t rc = check_launch("tiered_decode_kernel");
+    // Block stages are finalised inside the decode launch; list and
+    // workspace stages by one workgroup per (sequence, q head) row.
     if (rc != TIERKV_OK || !scores || p.lds_stage == STAGE_LDS_BLOCK) return rc;
-    // One workgroup per (sequence, q head) row.
     const int parts = score_parts(p.groups, pl.nw);
     const int64_t rows = int64_t(batch) * num_heads;
     if (rows > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");

@@ -80,26 +80,49 @@ def test_c4_long_context_full(device):
     _check(W.config4(), "absmax_i8", device, return_scores=True)
 
 
-def test_scores_reproducible(device):
+def _gqa16_long_case():
+    # GQA 16 (four-wave workgroups), rows long enough that three splits stage
+    # their statistics in the workspace (STAGE_GLOBAL) and eight in LDS.
+    return W.make_tiered_case("gqa16_long", 2, 32, 2, 128, 1500, 150, 700, seed=77)
+
+
+@pytest.mark.parametrize("which,fmt,cold,splits_seq,budgets", [
+    ("c3", "absmax_i8", "masked", (None, None, 2, 3, None), (26, 154)),
+    ("c3", "ref_u8", "zero_logit", (None, 2, 3, None), (26, 154)),
+    # C4: one split (workspace stage + finalisation kernel) against five and
+    # eight splits (list stage, finalised by each unit's last workgroup).
+    ("c4", "absmax_i8", "masked", (None, 1, 5, 8, None), (102, 922)),
+    ("c4", "ref_u8", "zero_logit", (None, 1, 5, 8), (102, 922)),
+    ("gqa16", "absmax_i8", "zero_logit", (3, 4, 8, None, 3), (150, 700)),
+])
+def test_scores_reproducible(device, which, fmt, cold, splits_seq, budgets):
     """Score sums (and the labels ranked from them) are the same bits on every
-    launch over the same inputs, whatever the split count or the order in
-    which waves met the tiles; the reference's score pass is a fixed
-    sequential loop (tierkv_triton.py:121-145)."""
+    launch over the same inputs, whatever the split count, the stage (LDS
+    block, LDS list, workspace) and the order in which waves met the tiles;
+    the reference's score pass is a fixed sequential loop
+    (tierkv_triton.py:121-145).  The first launch is also checked against
+    the oracle."""
     from paged_tierkv_amd import kernels
 
-    case = W.config3()
-    warm = oracle_warm(case, "absmax_i8")
+    case = {"c3": W.config3, "c4": W.config4, "gqa16": _gqa16_long_case}[which]()
+    print(f"[scores-repro] case={case.name} fmt={fmt} cold={cold} splits={splits_seq}", flush=True)
+    warm = oracle_warm(case, fmt)
     args = to_gpu_inputs(case, warm, device)
     runs = []
-    for splits in (None, None, 2, 3, None):
-        _, sc = tierkv_decode_attention(**args, return_scores=True, cold_mode="masked", splits=splits)
+    for splits in splits_seq:
+        _, sc = tierkv_decode_attention(**args, return_scores=True, cold_mode=cold, splits=splits)
         scores = kernels.block_scores_from_sums(sc, args["block_lengths"], case.num_blocks)
-        labels = kernels.tier_labels(scores, args["block_states"], 26, 154, mode="hot_warm_cold")
+        labels = kernels.tier_labels(scores, args["block_states"], budgets[0], budgets[1], mode="hot_warm_cold")
         torch.cuda.synchronize()
         runs.append((sc.cpu(), labels.cpu()))
-    for sc, lab in runs[1:]:
-        assert torch.equal(sc.view(torch.int32), runs[0][0].view(torch.int32))
-        assert torch.equal(lab, runs[0][1])
+    assert workspace_error_word(device) == 0
+    seqs = list(range(min(case.batch, 4)))
+    _, exp_sc = oracle_decode(case, warm, fmt, cold, True, seqs=seqs)
+    sc0 = runs[0][0].numpy()
+    report(f"{case.name} {fmt} {cold} score_sums", assert_close(sc0[seqs], exp_sc, what=f"{case.name} score_sums"))
+    for (sc, lab), splits in zip(runs[1:], splits_seq[1:]):
+        assert torch.equal(sc.view(torch.int32), runs[0][0].view(torch.int32)), f"score bits differ at splits={splits}"
+        assert torch.equal(lab, runs[0][1]), f"labels differ at splits={splits}"
 
 
 def test_two_streams_concurrent(device):
