@@ -99,12 +99,15 @@ TIERKV_API int32_t tierkv_decode_attention(
  * loops, harnesses that forbid hipMalloc.  The scratch is a 16 MiB device
  * array in the library (one copy per GPU, held until the process ends; its
  * address is taken and the array zeroed on the first call on each device,
- * with that device current); launches whose tierkv_decode_workspace_bytes
- * exceed 16 MiB fail with TIERKV_ERR_WORKSPACE.  Every call on a GPU shares
- * that GPU's array: calls that overlap on one GPU (different streams, or
- * host threads) race, and the out-of-range error word is not reported (use
- * tierkv_decode_attention for that).  Arguments and results otherwise as
- * tierkv_decode_attention; the stream must belong to the current device. */
+ * with that device current, and that first call waits for the fill, so it
+ * must not be under stream capture); launches whose
+ * tierkv_decode_workspace_bytes exceed 16 MiB fail with TIERKV_ERR_WORKSPACE.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or host threads) race.  Blocks skipped for an
+ * out-of-range slot or state set the array's error word, which
+ * tierkv_decode_noalloc_error_word reads.  Arguments and results otherwise
+ * as tierkv_decode_attention; the stream must belong to the current
+ * device. */
 TIERKV_API int32_t tierkv_decode_attention_noalloc(
     const void* query, int32_t query_dtype, void* out, float* score_sums,
     const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
@@ -115,6 +118,15 @@ TIERKV_API int32_t tierkv_decode_attention_noalloc(
     int32_t warm_format, int32_t cold_mode,
     int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
     float scaling, int32_t splits_hint, void* stream);
+
+/* The error word of the current device's allocation-free scratch (bit 1: a
+ * resident block with an out-of-range slot was skipped; bit 2: a state that
+ * is none of HOT/WARM/COLD), 0 before the first allocation-free launch on
+ * the device; cleared when clear != 0.  Synchronises the device (a copy, no
+ * allocation; not under stream capture).  Accessor of
+ * tierkv_decode_attention_noalloc, likewise without a counterpart in the
+ * reference. */
+TIERKV_API int32_t tierkv_decode_noalloc_error_word(int32_t clear, int32_t* word);
 
 /* Workspace bytes tierkv_decode_attention needs for this shape. */
 TIERKV_API int64_t tierkv_decode_workspace_bytes(
@@ -304,7 +316,9 @@ TIERKV_API int32_t tierkv_scatter_i32_inline(int32_t* dst, int64_t dst_len, cons
 /* One decode step of a layer in one call: the token write of
  * tierkv_write_hot_tokens_inline (n_jobs 0..4), the table writes of
  * tierkv_scatter_i32_inline (n_pairs 0..16), then tierkv_decode_attention,
- * in stream order, each validated as its own entry point validates it.  It
+ * in stream order, each validated as its own entry point validates it; every
+ * check runs before the first launch, so a call that returns an argument
+ * error has queued nothing.  It
  * replaces the three calls the reference's decode forward makes per layer
  * and step (append_to_layer's token write, the table update it queues, and
  * tierkv_decode_attention: modeling_llama.py:419-456, tierkv_policy.py:

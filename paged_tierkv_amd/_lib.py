@@ -75,6 +75,7 @@ SIGNATURES = {
         c_int32, c_int32, c_int32, c_int32, c_int32,
         c_float, c_int32, _P]),
     "tierkv_decode_workspace_bytes": (c_int64, [c_int32] * 8),
+    "tierkv_decode_noalloc_error_word": (c_int32, [c_int32, _P]),
     "tierkv_demote_to_warm": (c_int32, [
         _P, _P, c_int64,
         _P, _P, _P, c_int32,

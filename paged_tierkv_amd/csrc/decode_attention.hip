@@ -1705,19 +1705,19 @@ extern "C" int64_t tierkv_decode_workspace_bytes(int32_t batch, int32_t num_head
   return ws_layout(batch, num_heads, num_kv_heads, num_blocks, block_size, head_dim, with_scores != 0, splits_hint).total;
 }
 
-extern "C" int32_t tierkv_decode_attention(
+// Every argument check of tierkv_decode_attention, before anything is
+// launched (tierkv_decode_step runs it ahead of its token write, so a refused
+// step changes nothing on the device).
+int32_t tierkv::decode_check_args(
     const void* query, int32_t query_dtype, void* out, float* score_sums,
     const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
-    int64_t table_stride, const int32_t* seq_num_blocks, int32_t num_blocks,
+    int64_t table_stride, int32_t num_blocks,
     const void* hot_k, const void* hot_v, int64_t hot_slots,
     const void* warm_k, const void* warm_v, int64_t warm_slots,
     const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
     int32_t warm_format, int32_t cold_mode,
     int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
-    float scaling, int32_t splits_hint,
-    void* workspace, int64_t workspace_bytes, void* stream_) {
-  clear_error();
-  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+    int32_t splits_hint, void* workspace, int64_t workspace_bytes) {
   if (!query || !out || !block_table || !block_states || !block_lengths || !workspace)
     return fail(TIERKV_ERR_INVALID, "null tensor pointer");
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -1742,6 +1742,51 @@ extern "C" int32_t tierkv_decode_attention(
   const bool scores = score_sums != nullptr;
   const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, num_blocks, block_size, head_dim, scores, splits_hint);
   if (workspace_bytes < wl.total) return fail(TIERKV_ERR_WORKSPACE, "workspace too small");
+  const int groups = num_heads / num_kv_heads;
+  if (fast_path_ok(block_size, head_dim, groups) && table_stride <= 0x7fffffff) {
+    const bool aligned = aligned16(hot_k) && aligned16(hot_v) && aligned16(warm_k) && aligned16(warm_v) &&
+                         aligned16(query);
+    if (!aligned) return fail(TIERKV_ERR_INVALID, "query and pool base pointers must be 16-byte aligned");
+    if (warm_format == TIERKV_WARM_REF_U8) {
+      const uintptr_t m = reinterpret_cast<uintptr_t>(k_scale) | reinterpret_cast<uintptr_t>(k_zero) |
+                          reinterpret_cast<uintptr_t>(v_scale) | reinterpret_cast<uintptr_t>(v_zero);
+      if (m & 7u) return fail(TIERKV_ERR_INVALID, "reference-format scale/zero pools must be 8-byte aligned");
+    }
+    const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, groups, splits_hint);
+    if (pl.splits > 0xffff || num_kv_heads > 0xffff)
+      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or splits");
+    int64_t seqs_per_chunk = batch;
+    if (pl.splits > 1) {
+      seqs_per_chunk = MAX_SPLIT_UNITS / num_kv_heads;
+      if (seqs_per_chunk < 1) return fail(TIERKV_ERR_UNSUPPORTED, "too many kv heads for a split launch");
+    }
+    if (std::min<int64_t>(seqs_per_chunk, batch) * num_kv_heads * pl.splits > 0x7fffffff)
+      return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
+    if (scores && int64_t(batch) * num_heads > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
+  }
+  return TIERKV_OK;
+}
+
+extern "C" int32_t tierkv_decode_attention(
+    const void* query, int32_t query_dtype, void* out, float* score_sums,
+    const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
+    int64_t table_stride, const int32_t* seq_num_blocks, int32_t num_blocks,
+    const void* hot_k, const void* hot_v, int64_t hot_slots,
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    int32_t warm_format, int32_t cold_mode,
+    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    float scaling, int32_t splits_hint,
+    void* workspace, int64_t workspace_bytes, void* stream_) {
+  clear_error();
+  hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const int32_t rc0 = decode_check_args(query, query_dtype, out, score_sums, block_table, block_states, block_lengths,
+                                        table_stride, num_blocks, hot_k, hot_v, hot_slots, warm_k, warm_v, warm_slots,
+                                        k_scale, k_zero, v_scale, v_zero, warm_format, cold_mode, batch, num_heads,
+                                        num_kv_heads, block_size, head_dim, splits_hint, workspace, workspace_bytes);
+  if (rc0 != TIERKV_OK) return rc0;
+  const bool scores = score_sums != nullptr;
+  const WsLayout wl = ws_layout(batch, num_heads, num_kv_heads, num_blocks, block_size, head_dim, scores, splits_hint);
 
   DecodeParams p{};
   p.q = query;
@@ -1781,17 +1826,8 @@ extern "C" int32_t tierkv_decode_attention(
   const bool bf16 = query_dtype == TIERKV_DTYPE_BF16;
 
   if (fast_path_ok(block_size, head_dim, p.groups) && table_stride <= 0x7fffffff) {
-    const bool aligned = aligned16(hot_k) && aligned16(hot_v) && aligned16(warm_k) && aligned16(warm_v) &&
-                         aligned16(query);
-    if (!aligned) return fail(TIERKV_ERR_INVALID, "query and pool base pointers must be 16-byte aligned");
-    if (warm_format == TIERKV_WARM_REF_U8) {
-      const uintptr_t m = reinterpret_cast<uintptr_t>(k_scale) | reinterpret_cast<uintptr_t>(k_zero) |
-                          reinterpret_cast<uintptr_t>(v_scale) | reinterpret_cast<uintptr_t>(v_zero);
-      if (m & 7u) return fail(TIERKV_ERR_INVALID, "reference-format scale/zero pools must be 8-byte aligned");
-    }
+    // (alignment and launch limits: decode_check_args)
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, p.groups, splits_hint);
-    if (pl.splits > 0xffff || num_kv_heads > 0xffff)
-      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or splits");
     p.splits = pl.splits;
     p.split_magic = 0;
     // Unsplit score launches keep the per-block statistics in LDS (up to
@@ -1813,13 +1849,7 @@ extern "C" int32_t tierkv_decode_attention(
     // MAX_SPLIT_UNITS units each (the size of the workspace's counter
     // region): each chunk is launched on offset pointers, so the kernel sees
     // a batch of its own.  Unsplit launches need no counters.
-    int64_t seqs_per_chunk = batch;
-    if (pl.splits > 1) {
-      seqs_per_chunk = MAX_SPLIT_UNITS / num_kv_heads;
-      if (seqs_per_chunk < 1) return fail(TIERKV_ERR_UNSUPPORTED, "too many kv heads for a split launch");
-    }
-    if (std::min<int64_t>(seqs_per_chunk, batch) * num_kv_heads * pl.splits > 0x7fffffff)
-      return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
+    const int64_t seqs_per_chunk = pl.splits > 1 ? MAX_SPLIT_UNITS / num_kv_heads : batch;
     const size_t qsz = bf16 ? sizeof(__hip_bfloat16) : sizeof(__half);
     for (int64_t b0 = 0; b0 < batch; b0 += seqs_per_chunk) {
       const int64_t nbat = std::min<int64_t>(seqs_per_chunk, batch - b0);
@@ -1846,7 +1876,6 @@ extern "C" int32_t tierkv_decode_attention(
     if (rc != TIERKV_OK || !scores || p.lds_stage == STAGE_LDS_BLOCK) return rc;
     const int parts = score_parts(p.groups, pl.nw);
     const int64_t rows = int64_t(batch) * num_heads;
-    if (rows > 0x7fffffff) return fail(TIERKV_ERR_UNSUPPORTED, "grid too large");
     const size_t lds = num_blocks <= FIN_LDS_BLOCKS ? size_t(num_blocks) * sizeof(float2) : 0;
     const int32_t stride32 = int32_t(table_stride);
     if (cz)
@@ -1887,11 +1916,12 @@ __global__ void scratch_zero_kernel(uint4* p, int64_t n16) {
 }
 
 // The current device's copy of `scratch`.  The first call on a device takes
-// its address (host code never passes the array's name to a kernel) and
-// zeroes it on `stream` (refused under capture); later calls reuse the
-// address.  The arrival
-// counters and the error word must start at zero; every complete decode
-// launch leaves the counters at zero again.
+// its address (host code never passes the array's name to a kernel), zeroes
+// it on `stream` (refused under capture) and waits for the fill before the
+// address is published, so a later call on any stream finds the array zero;
+// later calls reuse the address.  The arrival counters and the error word
+// must start at zero; every complete decode launch leaves the counters at
+// zero again.
 int32_t device_scratch(hipStream_t stream, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
@@ -1911,6 +1941,10 @@ int32_t device_scratch(hipStream_t stream, void** out) {
                        STATIC_SCRATCH_BYTES / 16);
     const int32_t rc = check_launch("scratch_zero_kernel");
     if (rc != TIERKV_OK) return rc;
+    const hipError_t se = hipStreamSynchronize(stream);
+    if (se != hipSuccess)
+      return fail(TIERKV_ERR_HIP, std::string("tierkv_decode_attention_noalloc: zeroing the scratch array: ") +
+                                      hipGetErrorString(se));
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
@@ -1946,4 +1980,28 @@ extern "C" int32_t tierkv_decode_attention_noalloc(
                                  warm_slots, k_scale, k_zero, v_scale, v_zero, warm_format, cold_mode, batch,
                                  num_heads, num_kv_heads, block_size, head_dim, scaling, splits_hint, ws,
                                  STATIC_SCRATCH_BYTES, stream_);
+}
+
+extern "C" int32_t tierkv_decode_noalloc_error_word(int32_t clear, int32_t* word) {
+  clear_error();
+  if (!word) return fail(TIERKV_ERR_INVALID, "word must not be null");
+  *word = 0;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return fail(TIERKV_ERR_HIP, "tierkv_decode_noalloc_error_word: no usable current device");
+  void* ptr = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev];
+  }
+  if (!ptr) return TIERKV_OK;   // no allocation-free launch on this device yet
+  // The error word is the workspace layout's first word (offset 0).  Every
+  // launch on the device, on any stream, completes before it is read.
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipMemcpy(word, ptr, sizeof(int32_t), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && clear && *word != 0) e = hipMemset(ptr, 0, sizeof(int32_t));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess)
+    return fail(TIERKV_ERR_HIP, std::string("tierkv_decode_noalloc_error_word: ") + hipGetErrorString(e));
+  return TIERKV_OK;
 }

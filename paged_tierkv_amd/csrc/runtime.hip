@@ -773,6 +773,16 @@ extern "C" int32_t tierkv_decode_step(const TierkvDecodeStep* s, void* stream) {
   if (!s) return fail(TIERKV_ERR_INVALID, "null pointer");
   if (s->n_jobs < 0 || s->n_jobs > INLINE_JOBS) return fail(TIERKV_ERR_INVALID, "a step carries 0..4 write jobs");
   if (s->n_pairs < 0 || s->n_pairs > INLINE_PAIRS) return fail(TIERKV_ERR_INVALID, "a step carries 0..16 table writes");
+  // The decode launch's arguments are checked before the token write goes
+  // out, so a refused step leaves the device as it was.
+  {
+    const int32_t rc = decode_check_args(
+        s->query, s->query_dtype, s->out, s->score_sums, s->block_table, s->block_states, s->block_lengths,
+        s->table_stride, s->num_blocks, s->hot_k, s->hot_v, s->hot_slots, s->warm_k, s->warm_v, s->warm_slots,
+        s->k_scale, s->k_zero, s->v_scale, s->v_zero, s->warm_format, s->cold_mode, s->batch, s->num_heads,
+        s->num_kv_heads, s->block_size, s->head_dim, s->splits_hint, s->workspace, s->workspace_bytes);
+    if (rc != TIERKV_OK) return rc;
+  }
   if (s->n_jobs > 0) {
     // The token write and the table writes in one launch: workgroup (0, 0, 0)
     // of the write kernel also applies the pairs.

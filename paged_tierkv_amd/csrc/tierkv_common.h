@@ -34,6 +34,19 @@ inline int32_t check_launch(const char* what) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Every argument check of tierkv_decode_attention (decode_attention.hip),
+// without a launch: TIERKV_OK or the status that call would return.
+int32_t decode_check_args(
+    const void* query, int32_t query_dtype, void* out, float* score_sums,
+    const int32_t* block_table, const int32_t* block_states, const int32_t* block_lengths,
+    int64_t table_stride, int32_t num_blocks,
+    const void* hot_k, const void* hot_v, int64_t hot_slots,
+    const void* warm_k, const void* warm_v, int64_t warm_slots,
+    const void* k_scale, const void* k_zero, const void* v_scale, const void* v_zero,
+    int32_t warm_format, int32_t cold_mode,
+    int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
+    int32_t splits_hint, void* workspace, int64_t workspace_bytes);
+
 // ---- device helpers -------------------------------------------------------
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));

@@ -43,6 +43,7 @@ the kernel skipped a block whose slot or state was out of range.
 
 from __future__ import annotations
 
+import ctypes
 import weakref
 
 import torch
@@ -63,12 +64,15 @@ class DecodeWorkspace:
 
     ``growable=False`` fixes the buffer for the workspace's lifetime: a call
     that needs more raises instead of reallocating.  Captured graphs hold the
-    buffer's address, so a workspace used under capture must be fixed and
-    sized before the capture (``DecodeWorkspace.for_shape``).  A growable
-    workspace replaces its buffer when a call needs more bytes; the error
-    flags set in the old buffer are carried into the new one on the device
-    (no host sync), and the old buffer is released on the stream that used
-    it.  The reference caches one placeholder tensor per device the same way
+    buffer's address, so a workspace used under capture must be sized before
+    the capture (``DecodeWorkspace.for_shape``); the first launch bound to a
+    workspace under capture fixes it, so that no later eager launch can free
+    memory a graph replays on.  A growable workspace replaces its buffer when
+    a call needs more bytes; the error flags set in the old buffer are carried
+    into the new one on the device (no host sync), and the old buffer is
+    recorded on every stream that used it before it is dropped, so the
+    caching allocator reuses it only after their queued work.  The reference
+    caches one placeholder tensor per device the same way
     (tierkv_triton.py:24-40).
     """
 
@@ -76,7 +80,13 @@ class DecodeWorkspace:
         self.device = torch.device(device)
         self.growable = bool(growable)
         self.buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=self.device)
+        self._streams = []   # the streams launches bound to this workspace were issued on
         _LIVE.add(self)
+
+    def note_stream(self, stream) -> None:
+        """Record that launches on ``stream`` (a torch stream) use this workspace."""
+        if self.device.type == "cuda" and all(stream != s for s in self._streams):
+            self._streams.append(stream)
 
     @staticmethod
     def bytes_for(batch: int, num_heads: int, kv_heads: int, num_blocks: int, head_dim: int, *,
@@ -104,18 +114,29 @@ class DecodeWorkspace:
     def data_ptr(self) -> int:
         return self.buf.data_ptr()
 
+    def _capturing(self) -> bool:
+        return self.device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
     def reserve(self, nbytes: int) -> None:
+        capturing = self._capturing()
         if nbytes <= self.nbytes:
+            if capturing:
+                self.growable = False   # a graph holds this buffer's address from now on
             return
-        if not self.growable:
-            raise RuntimeError(f"decode workspace holds {self.nbytes} bytes, the launch needs {int(nbytes)}: "
-                               "size the fixed workspace for the largest launch (DecodeWorkspace.for_shape).")
-        if self.device.type == "cuda" and torch.cuda.is_current_stream_capturing():
+        if capturing:
             raise RuntimeError("the decode workspace cannot grow during HIP graph capture: pass workspace= "
                                "(a DecodeWorkspace sized before the capture), or run the launch once eagerly "
                                "on this stream first.")
+        if not self.growable:
+            raise RuntimeError(f"decode workspace holds {self.nbytes} bytes, the launch needs {int(nbytes)}: "
+                               "size the fixed workspace for the largest launch (DecodeWorkspace.for_shape).")
         new = torch.zeros(int(nbytes), dtype=torch.uint8, device=self.device)
         new[:4].view(torch.int32).bitwise_or_(self.buf[:4].view(torch.int32))
+        if self.device.type == "cuda":
+            current = torch.cuda.current_stream(self.device)
+            for stream in self._streams + [current]:
+                self.buf.record_stream(stream)
+            self._streams = [current]
         self.buf = new
 
     def error_word(self, clear: bool = True) -> int:
@@ -145,19 +166,35 @@ def stream_workspace(device=None) -> DecodeWorkspace:
             raise RuntimeError("no decode workspace exists for the capturing stream: pass workspace= (a "
                                "DecodeWorkspace sized before the capture).")
         ws = DecodeWorkspace(device)
+        ws.note_stream(torch.cuda.current_stream(device))
         _implicit[key] = ws
     return ws
 
 
+def noalloc_error_word(device, clear: bool = True) -> int:
+    """The error flags of the allocation-free entry point's scratch on
+    ``device`` (0 before its first launch there); synchronises the device."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        return 0
+    word = ctypes.c_int32(0)
+    with torch.cuda.device(device):
+        _lib.check(_lib.lib().tierkv_decode_noalloc_error_word(int(bool(clear)), ctypes.addressof(word)),
+                   "tierkv_decode_noalloc_error_word")
+    return int(word.value)
+
+
 def workspace_error_word(device) -> int:
     """Read (and clear) the kernels' error flags of every decode workspace on
-    ``device`` (synchronises)."""
+    ``device`` and of the allocation-free scratch there (synchronises)."""
     device = torch.device(device)
     idx = device.index if device.index is not None else torch.cuda.current_device()
     word = 0
     for ws in list(_LIVE):
         if ws.device.type == device.type and (ws.device.index or 0) == idx:
             word |= ws.error_word()
+    if device.type == "cuda":
+        word |= noalloc_error_word(torch.device("cuda", idx))
     return word
 
 
@@ -414,6 +451,7 @@ def _bind(
         ws = None
     elif workspace is not None:
         ws = workspace
+        ws.note_stream(torch.cuda.current_stream(device))
     elif prepared:
         ws = DecodeWorkspace(device, need, growable=False)
     else:
@@ -448,11 +486,11 @@ def _launch(lib, args, device, ws) -> None:
     if ws is None:
         rc = lib.tierkv_decode_attention_noalloc(*args, _lib.stream_of(device))
         _lib.check(rc, "tierkv_decode_attention_noalloc")
-        return
-    rc = lib.tierkv_decode_attention(*args, _lib.stream_of(device))
-    _lib.check(rc, "tierkv_decode_attention")
+    else:
+        rc = lib.tierkv_decode_attention(*args, _lib.stream_of(device))
+        _lib.check(rc, "tierkv_decode_attention")
     if _lib.env_flag("TIERKV_CHECK_ERRORS"):
-        word = ws.error_word()
+        word = noalloc_error_word(device) if ws is None else ws.error_word()
         if word:
             raise RuntimeError(f"TierKV decode skipped blocks with out-of-range slot/state (flag {word}).")
 

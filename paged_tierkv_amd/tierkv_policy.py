@@ -1403,16 +1403,27 @@ class CompactTieredKVTensorPool(_PoolBase):
         self._blocks[physical_idx] = _Block(HOT_STATE, b.slot, pos + 1)
         tables.set(self._t_len, where[0], where[1], pos + 1)
         pending = tables.pending
-        for i, (flat, value) in enumerate(pending.items()):
+        sent = dict(pending)
+        for i, (flat, value) in enumerate(sent.items()):
             st.pairs[i][0], st.pairs[i][1] = flat, value
-        st.n_pairs = len(pending)
+        st.n_pairs = len(sent)
         pending.clear()
         st.src_k, st.src_v = key_states.data_ptr(), value_states.data_ptr()
         st.src_tokens = key_states.shape[2]
         job[3], job[4] = b.slot, pos
         st.query, st.out, st.num_blocks = query_states.data_ptr(), out.data_ptr(), n
         st.workspace, st.workspace_bytes = ws.data_ptr(), ws.nbytes
-        _lib.check(lib.tierkv_decode_step(st_ref, _lib.stream_of(self.device)), "tierkv_decode_step")
+        rc = lib.tierkv_decode_step(st_ref, _lib.stream_of(self.device))
+        if rc != _lib.TIERKV_OK:
+            # A refused step queued nothing on the device (its checks run
+            # before its first launch): the ledger entry and the block's
+            # length return to what they were, and the table entries go back
+            # to the queue, so host and device tables agree once it is
+            # flushed.
+            self._blocks[physical_idx] = b
+            pending.update(sent)
+            tables.set(self._t_len, where[0], where[1], b.length)
+            _lib.check(rc, "tierkv_decode_step")
         return out
 
     def _write_warm_range(self, physical_idx, src_k, src_v, tok0, length) -> None:

@@ -21,6 +21,12 @@ Outputs small .npz fixtures next to this script:
   operation, SHA-256 digests of every pool tensor at each checkpoint, and
   the final pools and outputs.  The ops list (JSON) is what the test
   replays against the drop-in.
+* runtime_compact_hot_warm_cold_tinyllama.npz -- the same script at
+  TinyLlama's attention geometry (4 kv heads, 32 q heads, head_dim 64,
+  block 16), the shape the decode kernel's fast path serves, so the replay's
+  decode launch over the reference-written pools runs that path.
+
+``--only tinyllama`` writes just the last fixture.
 """
 
 import glob
@@ -40,6 +46,8 @@ REF_BM_DIR = os.path.join(os.path.dirname(os.path.dirname(HERE)), "oracle", "_re
 # code path exercised).
 TRAJ = dict(num_layers=2, kv_heads=2, head_dim=16, block_size=16, heads=4, hot_budget=4, warm_budget=3,
             max_seq_len=320, policy_interval=4, pool_chunk_blocks=16, prefill_tokens=90, steps=40)
+# TinyLlama-1.1B's attention geometry, shorter run.
+TRAJ_TINYLLAMA = dict(TRAJ, kv_heads=4, head_dim=64, heads=32, prefill_tokens=72, steps=24)
 POOL_NAMES = ("hot_k_pool", "hot_v_pool", "warm_k_pool", "warm_v_pool", "k_scale", "k_zero", "v_scale", "v_zero")
 
 
@@ -92,11 +100,10 @@ def runtime_snapshot(rt, layout) -> dict:
     return out
 
 
-def runtime_trajectory(tp, BM, layout, mode, seed):
+def runtime_trajectory(tp, BM, layout, mode, seed, c=TRAJ):
     for key in list(os.environ):
         if key.startswith("TIERKV_"):
             del os.environ[key]
-    c = TRAJ
     g = torch.Generator().manual_seed(seed)
     rt = tp.TieredKVRuntime(block_manager=BM(total_blocks=256), num_layers=c["num_layers"],
                             block_size=c["block_size"], hot_budget=c["hot_budget"], max_seq_len=c["max_seq_len"],
@@ -195,19 +202,28 @@ def codec_vectors(tp):
     return dict(x=x.numpy(), q=q.numpy(), scale=s.numpy(), zero=z.numpy(), deq=d.numpy())
 
 
-def main(ref_root):
+def main(ref_root, only=None):
     sys.path.insert(0, ref_root)
     import tierkv_policy as tp   # the reference module, CPU only
 
-    np.savez_compressed(os.path.join(HERE, "codec_ref_u8.npz"), **codec_vectors(tp))
-    print("wrote codec_ref_u8.npz")
     BM = _ref_block_manager()
-    for seed, (layout, mode) in enumerate([("compact", "hot_warm"), ("compact", "hot_warm_cold"),
-                                           ("dense", "hot_warm"), ("dense", "hot_warm_cold")]):
-        name = f"runtime_{layout}_{mode}.npz"
-        np.savez_compressed(os.path.join(HERE, name), **runtime_trajectory(tp, BM, layout, mode, 100 + seed))
-        print("wrote", name)
+    if only is None:
+        np.savez_compressed(os.path.join(HERE, "codec_ref_u8.npz"), **codec_vectors(tp))
+        print("wrote codec_ref_u8.npz")
+        for seed, (layout, mode) in enumerate([("compact", "hot_warm"), ("compact", "hot_warm_cold"),
+                                               ("dense", "hot_warm"), ("dense", "hot_warm_cold")]):
+            name = f"runtime_{layout}_{mode}.npz"
+            np.savez_compressed(os.path.join(HERE, name), **runtime_trajectory(tp, BM, layout, mode, 100 + seed))
+            print("wrote", name)
+    name = "runtime_compact_hot_warm_cold_tinyllama.npz"
+    np.savez_compressed(os.path.join(HERE, name),
+                        **runtime_trajectory(tp, BM, "compact", "hot_warm_cold", 200, TRAJ_TINYLLAMA))
+    print("wrote", name)
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    only = sys.argv[sys.argv.index("--only") + 1] if "--only" in sys.argv else None
+    if only is not None:
+        args = [a for a in args if a != only]
+    main(args[0] if args else "/root/reference", only)

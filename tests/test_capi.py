@@ -52,6 +52,7 @@ def test_abi_version_and_errors_without_gpu():
     assert lib.tierkv_decode_workspace_bytes(32, 32, 8, 256, 16, 128, 1, 0) > 0
     assert lib.tierkv_tier_labels(None, None, None, 4, 1, 4, 2, 1, 7, 1, None) == _lib.TIERKV_ERR_INVALID
     assert lib.tierkv_block_mass_from_probs(None, None, None, 1, 1, 16, 16, None) == _lib.TIERKV_ERR_INVALID
+    assert lib.tierkv_decode_noalloc_error_word(1, None) == _lib.TIERKV_ERR_INVALID
 
 
 def test_decode_wrapper_contract_on_cpu_tensors():

@@ -366,6 +366,38 @@ def test_all_cold(device):
             np.testing.assert_allclose(s, 1.0, atol=1e-5)
 
 
+def test_growable_workspace_grows_on_a_side_stream(device):
+    """A growable workspace bound to launches on a side stream grows there:
+    before its old buffer is dropped it is recorded on every stream that used
+    it, so the caching allocator hands it out again only after their queued
+    launches; every launch matches the oracle."""
+    from paged_tierkv_amd.tierkv_hip import DecodeWorkspace
+
+    small = W.make_tiered_case("ws_small", 2, 16, 4, 64, 30, 6, 14, seed=81)
+    big = W.make_tiered_case("ws_big", 4, 32, 8, 128, 600, 60, 300, seed=82)
+    runs = [(small, "absmax_i8", "masked", 2), (big, "ref_u8", "zero_logit", 6), (small, "ref_u8", "masked", 1)]
+    prepared = []
+    for case, fmt, cold, splits in runs:
+        warm = oracle_warm(case, fmt)
+        prepared.append((case, warm, fmt, cold, splits, to_gpu_inputs(case, warm, device)))
+    torch.cuda.synchronize()
+    ws = DecodeWorkspace(device)            # 256 bytes: the launches below grow it
+    side = torch.cuda.Stream(device)
+    outs = []
+    with torch.cuda.stream(side):
+        for case, warm, fmt, cold, splits, inputs in prepared:
+            print(f"[ws-side] case={case.name} fmt={fmt} cold={cold} splits={splits} bytes={ws.nbytes}", flush=True)
+            outs.append(tierkv_decode_attention(**inputs, return_scores=True, cold_mode=cold, splits=splits,
+                                                workspace=ws))
+    assert ws.growable and ws.nbytes > 256 and any(s == side for s in ws._streams)
+    side.synchronize()
+    assert ws.error_word() == 0
+    for (case, warm, fmt, cold, splits, _), (out, sc) in zip(prepared, outs):
+        exp_out, exp_sc = oracle_decode(case, warm, fmt, cold, True)
+        assert_close(out[:, 0].float().cpu().numpy(), exp_out, what=f"{case.name} side-stream output")
+        assert_close(sc.cpu().numpy(), exp_sc, what=f"{case.name} side-stream score_sums")
+
+
 def test_invalid_slot_is_skipped_and_flagged(device, monkeypatch):
     case = W.make_tiered_case("badslot", 1, 8, 4, 64, 4, 4, 0, seed=5)
     case.block_table[0, 2] = 10_000   # out of range HOT slot: never dereferenced

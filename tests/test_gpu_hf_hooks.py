@@ -135,6 +135,54 @@ def test_dropin_fused_step_matches_general_path(model, device, monkeypatch):
             (cg.open_physical_idx, cg.open_token_count, cg.num_blocks)
 
 
+def test_dropin_refused_step_keeps_tables_consistent(model, device, monkeypatch):
+    """A one-call decode step that the library refuses (its checks run before
+    its first launch, so nothing reached the device) leaves the drop-in's
+    ledger, block cursor and tables as they were, with the step's table
+    writes queued again: after a flush the device tables equal the host
+    copies.  The same step then goes through."""
+    from paged_tierkv_amd import _lib
+
+    print("[hf] drop-in refused one-call step", flush=True)
+    ids = _tokens(1, device)
+    rt = _dropin_runtime(model, hot_budget=3, policy_interval=10_000, policy_mode="hot_warm",
+                         attention_backend="triton")
+    with torch.no_grad():
+        out = model(input_ids=ids[:, :PROMPT], past_key_values=rt.cache, use_cache=True, logits_to_keep=1)
+        for s in range(3):
+            out = model(input_ids=ids[:, PROMPT + s: PROMPT + s + 1], past_key_values=out.past_key_values,
+                        use_cache=True, logits_to_keep=1)
+    cfg = model.config
+    heads, kvh, dim = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    g = torch.Generator().manual_seed(3)
+    q = torch.randn((1, heads, 1, dim), generator=g).half().to(device)
+    k = torch.randn((1, kvh, 1, dim), generator=g).half().to(device)
+    v = torch.randn((1, kvh, 1, dim), generator=g).half().to(device)
+    pool, layer = rt.kv_pool, 0
+    cursor = rt.layer_states[layer]
+    assert cursor.open_physical_idx is not None
+    before = (cursor.open_physical_idx, cursor.open_token_count, cursor.num_blocks)
+    ledger = dict(pool._blocks)
+
+    def tables_agree():
+        for t in range(pool._tables.shape[1]):
+            host = torch.from_numpy(pool._tables.host[:, t].copy())
+            assert torch.equal(pool._tables.view(t).cpu(), host), t
+
+    tables_agree()
+    monkeypatch.setattr(_lib.lib(), "tierkv_decode_step", lambda *a: _lib.TIERKV_ERR_INVALID)
+    with pytest.raises(ValueError):
+        rt.fused_decode_step(layer, q, k, v, heads // kvh, dim ** -0.5)
+    assert (cursor.open_physical_idx, cursor.open_token_count, cursor.num_blocks) == before
+    assert pool._blocks == ledger
+    tables_agree()
+    monkeypatch.undo()
+    out = rt.fused_decode_step(layer, q, k, v, heads // kvh, dim ** -0.5)
+    assert out is not None and torch.isfinite(out.float()).all()
+    assert cursor.open_token_count == before[1] + 1
+    tables_agree()
+
+
 def test_dropin_policy_ticks_run(model, device):
     print("[hf] drop-in hot_warm_cold with ticks", flush=True)
     ids = _tokens(1, device)

@@ -40,8 +40,12 @@ from helpers import ATOL, RTOL
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+# The last case has TinyLlama's attention geometry (4 kv heads, GQA group 8,
+# head_dim 64, block 16): its decode launch runs the kernel's fast path
+# (tiered_decode_kernel) over pools the reference wrote; the others (head_dim
+# 16) run the generic path.
 CASES = ["runtime_compact_hot_warm", "runtime_compact_hot_warm_cold", "runtime_dense_hot_warm",
-         "runtime_dense_hot_warm_cold"]
+         "runtime_dense_hot_warm_cold", "runtime_compact_hot_warm_cold_tinyllama"]
 
 
 def _golden_module():
@@ -131,8 +135,8 @@ def test_runtime_replays_reference_trajectory(device, name):
     print(f"[dropin] {name}", flush=True)
     rt, cfg = _replay(name, device)
     # Decode over the replayed tables, called the way the HF hook calls it.
-    groups = 2
     kvh, dim = cfg["kv_heads"], cfg["head_dim"]
+    groups = cfg["heads"] // kvh
     gen = torch.Generator().manual_seed(5)
     for layer in range(cfg["num_layers"]):
         q = torch.randn((1, kvh * groups, 1, dim), generator=gen).half().to(device)

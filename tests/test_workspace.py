@@ -3,6 +3,8 @@
 * A fixed workspace never replaces its buffer: a launch that needs more
   raises, so a captured graph can never replay on a released buffer.
 * A growable workspace carries its error flags into the new buffer.
+* A workspace first bound under stream capture becomes fixed, so a later,
+  larger eager launch cannot free memory a captured graph replays on.
 * The batched runtime sizes its fixed workspace once, for ``max_blocks``
   with score sums; every smaller launch of the same geometry (any block
   count, with or without scores) fits in it, so nothing it launches can ask
@@ -37,6 +39,21 @@ def test_growable_workspace_keeps_error_flags():
     assert int(ws.buf[4:].abs().sum()) == 0
     assert ws.error_word() == 2
     assert ws.error_word() == 0
+
+
+def test_capture_pins_a_growable_workspace(monkeypatch):
+    ws = DecodeWorkspace("cpu", 4096)
+    assert ws.growable
+    monkeypatch.setattr(DecodeWorkspace, "_capturing", lambda self: True)
+    ws.reserve(1024)                    # bound under capture: fits, and is fixed from now on
+    assert not ws.growable
+    with pytest.raises(RuntimeError, match="during HIP graph capture"):
+        ws.reserve(8192)
+    monkeypatch.setattr(DecodeWorkspace, "_capturing", lambda self: False)
+    before = ws.data_ptr()
+    with pytest.raises(RuntimeError, match="fixed workspace"):
+        ws.reserve(8192)                # eager growth after the capture is refused
+    assert ws.data_ptr() == before and ws.nbytes == 4096
 
 
 @pytest.mark.parametrize("batch,heads,kv,dim,max_blocks", [

@@ -3,6 +3,10 @@ against tierkv_decode_attention: both called through the C ABI on the same
 bound inputs, two or more calls in a row on the library's one scratch array
 (the later ones smaller), each also checked against the CPU oracle.
 
+Also: the scratch array's error word (tierkv_decode_noalloc_error_word),
+and the first call on a device in a fresh process, which zeroes the array
+before any launch on another stream can use it.
+
 Bar: per-block score sums bit-exact (their reduction order is fixed);
 outputs within the split-invariance bound of each other (each wave's
 running maximum depends on the dynamic tile hand-out) and within 2e-3
@@ -10,13 +14,18 @@ absolute / 1e-2 relative of the oracle."""
 
 from __future__ import annotations
 
+import os
+import subprocess
+import sys
+
 import numpy as np
 import pytest
 import torch
 
 from paged_tierkv_amd import _lib
 from paged_tierkv_amd import workloads as W
-from paged_tierkv_amd.tierkv_hip import NOALLOC, DecodeWorkspace, PreparedDecode, _bind, tierkv_decode_attention
+from paged_tierkv_amd.tierkv_hip import (NOALLOC, DecodeWorkspace, PreparedDecode, _bind, noalloc_error_word,
+                                         tierkv_decode_attention, workspace_error_word)
 
 from helpers import assert_close, oracle_decode, oracle_warm, report, to_gpu_inputs
 
@@ -119,3 +128,68 @@ def test_noalloc_rejects_oversize(device):
                                          workspace=NOALLOC)
         torch.cuda.synchronize()
         assert out.shape == (batch, 1, heads, d)
+
+
+def test_noalloc_error_word(device, monkeypatch):
+    """A block whose slot is out of range is skipped by an allocation-free
+    launch and flagged in the scratch array's error word, which
+    tierkv_decode_noalloc_error_word reads and clears."""
+    case = W.make_tiered_case("noalloc_badslot", 1, 8, 4, 64, 4, 4, 0, seed=5)
+    case.block_table[0, 2] = 10_000   # out-of-range HOT slot: never dereferenced
+    args = to_gpu_inputs(case, oracle_warm(case, "absmax_i8"), device)
+    print("[noalloc] bad slot, error word", flush=True)
+    assert noalloc_error_word(device) == 0
+    tierkv_decode_attention(**args, cold_mode="masked", workspace=NOALLOC)
+    assert noalloc_error_word(device, clear=False) == 1
+    assert workspace_error_word(device) == 1      # read and cleared with the workspaces' words
+    assert noalloc_error_word(device) == 0
+    monkeypatch.setenv("TIERKV_CHECK_ERRORS", "1")
+    with pytest.raises(RuntimeError, match="out-of-range"):
+        tierkv_decode_attention(**args, cold_mode="masked", workspace=NOALLOC)
+    assert noalloc_error_word(device) == 0
+
+
+_FIRST_CALL_SCRIPT = r"""
+import torch
+from paged_tierkv_amd import workloads as W
+from paged_tierkv_amd.tierkv_hip import NOALLOC, tierkv_decode_attention, workspace_error_word
+from helpers import assert_close, oracle_decode, oracle_warm, to_gpu_inputs
+
+dev = torch.device("cuda:0")
+a = W.make_tiered_case("first_a", 1, 16, 4, 64, 20, 6, 10, seed=95)          # unsplit, no scores
+b = W.make_tiered_case("first_b", 4, 32, 8, 128, 512, 60, 300, seed=96)      # split, with scores
+wa, wb = oracle_warm(a, "absmax_i8"), oracle_warm(b, "ref_u8")
+ia, ib = to_gpu_inputs(a, wa, dev), to_gpu_inputs(b, wb, dev)
+torch.cuda.synchronize()
+sa, sb = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+print("first noalloc call on stream A, then at once a split launch on stream B", flush=True)
+with torch.cuda.stream(sa):
+    out_a, _ = tierkv_decode_attention(**ia, cold_mode="masked", splits=1, workspace=NOALLOC)
+with torch.cuda.stream(sb):
+    out_b, sc_b = tierkv_decode_attention(**ib, return_scores=True, cold_mode="zero_logit", splits=4,
+                                          workspace=NOALLOC)
+torch.cuda.synchronize()
+assert workspace_error_word(dev) == 0
+assert_close(out_a[:, 0].float().cpu().numpy(), oracle_decode(a, wa, "absmax_i8", "masked"), what="stream A")
+exp_out, exp_sc = oracle_decode(b, wb, "ref_u8", "zero_logit", True)
+assert_close(out_b[:, 0].float().cpu().numpy(), exp_out, what="stream B output")
+assert_close(sc_b.cpu().numpy(), exp_sc, what="stream B score_sums")
+print("FIRST-CALL OK", flush=True)
+"""
+
+
+def test_noalloc_first_call_then_other_stream(device):
+    """In a fresh process (the scratch array not yet zeroed): the first
+    allocation-free call, on stream A, zeroes the array and waits for it
+    before publishing its address, so a split launch issued right after on
+    stream B -- ordered on the host only -- finds its arrival counters zero.
+    (The first launch is unsplit and without scores: it shares nothing with
+    the second but the error word, so the two may overlap.)"""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([root, os.path.join(root, "tests"),
+                                                       os.environ.get("PYTHONPATH", "")]))
+    print("[noalloc] fresh process: first call on stream A, split launch on stream B", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _FIRST_CALL_SCRIPT], cwd=root, env=env, capture_output=True,
+                          text=True, timeout=300)
+    print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0 and "FIRST-CALL OK" in proc.stdout
