@@ -64,6 +64,9 @@ def parse():
                    help="c5: run decode steps eagerly only (no HIP-graph replay, no eager comparison run)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true",
+                   help="default C3 line: skip the extra decode figures (C3 with scores, C3 in the reference WARM "
+                        "format, C4 with and without scores) timed after the headline")
     p.add_argument("--mode", choices=["bench", "copy", "ceiling"], default="bench",
                    help="copy: time a plain device copy of known size (PMC calibration); ceiling: HBM "
                         "stream-read and 4 KB-tile gather ceilings of the box")
@@ -715,6 +718,35 @@ def c5_generate(model, prompt, cache, steps, runtime=None):
     return torch.cat(toks, dim=1), sec, cache
 
 
+def c5_forced(model, prompt, forced, cache, runtime=None):
+    """Prefill, then feed forced[:, s] for every s (teacher forcing): the
+    last-position logits of the prefill and of every step, fp16
+    [steps + 1, B, V]."""
+    import torch
+
+    from paged_tierkv_amd import hf_llama
+
+    outs = []
+    with torch.no_grad():
+        out = model(input_ids=prompt, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        outs.append(out.logits[:, -1].to(torch.float16, copy=True))
+        cache = out.past_key_values
+        runner = hf_llama.DecodeGraphRunner(model, runtime) if runtime is not None else None
+        for s in range(forced.shape[1]):
+            tok = forced[:, s: s + 1]
+            if runner is not None:
+                logits = runner.step(tok)
+            else:
+                out = model(input_ids=tok, past_key_values=cache, use_cache=True, logits_to_keep=1)
+                cache = out.past_key_values
+                logits = out.logits
+            # A copy: the graph runner returns its static output buffer,
+            # which a later replay overwrites.
+            outs.append(logits[:, -1].to(torch.float16, copy=True))
+    torch.cuda.synchronize()
+    return torch.stack(outs)
+
+
 def synced_step_ms(model, prompt, cache, steps):
     """Prefill, then `steps` greedy decode steps with a device sync after
     each; returns the wall time of every step in ms (the per-step view of
@@ -871,7 +903,7 @@ def run_c5(args, device):
     log(f"[c5] tiered ({mode}): {tps:.1f} tok/s ({sec / steps * 1e3:.2f} ms/step), KV pools "
         f"{metrics['physical_pool_bytes'] / 2**20:.1f} MiB allocated ({metrics['resident_kv_bytes'] / 2**20:.1f} MiB "
         f"resident) vs dense {metrics['dense_equivalent_bytes'] / 2**20:.1f} MiB")
-    dense = None
+    dense = agreement = like_for_like = None
     if not args.no_dense_baseline:
         del rt
         torch.cuda.empty_cache()
@@ -882,10 +914,45 @@ def run_c5(args, device):
         for layer in dcache.layers:
             for t in (layer.keys, layer.values):
                 kv_bytes += t.numel() * t.element_size()
-        agree = (dtoks == toks).float().mean().item()
+        del dcache
         dense = {"tokens_per_s": round(B * steps / dsec, 1), "ms_per_step": round(dsec / steps * 1e3, 3),
-                 "kv_bytes": kv_bytes, "greedy_token_agreement_with_tiered": round(agree, 4)}
-        log(f"[c5] dense: {dense['tokens_per_s']} tok/s, KV {kv_bytes / 2**20:.1f} MiB, token agreement {agree:.3f}")
+                 "kv_bytes": kv_bytes, "decode_steps_as": "eager (stock transformers)"}
+        log(f"[c5] dense: {dense['tokens_per_s']} tok/s, KV {kv_bytes / 2**20:.1f} MiB")
+        if eager is not None:
+            like_for_like = {"tiered_eager_tokens_per_s": eager["tokens_per_s"],
+                             "dense_eager_tokens_per_s": dense["tokens_per_s"],
+                             "ratio": round(eager["tokens_per_s"] / dense["tokens_per_s"], 3)}
+        # Output agreement (random-init logits are nearly flat, so greedy
+        # tokens of a tiered run say nothing): every block HOT, teacher-forced
+        # on the dense run's own greedy tokens, against the dense run's logits.
+        n = min(steps, 32)
+        torch.cuda.empty_cache()
+        log(f"[c5] all-HOT tiered runtime teacher-forced on the dense run's first {n} tokens")
+        dlog = c5_forced(model, prompt, dtoks[:, :n], DynamicCache(config=cfg))
+        # The rounding floor of two correct fp16 attention implementations:
+        # stock transformers' eager attention against its SDPA, same tokens.
+        impl = cfg._attn_implementation
+        cfg._attn_implementation = "eager"
+        try:
+            elog = c5_forced(model, prompt, dtoks[:, :n], DynamicCache(config=cfg))
+        finally:
+            cfg._attn_implementation = impl
+        floor = (elog.float() - dlog.float()).abs()
+        del elog
+        hot_rt = BatchedTieredKVRuntime(cfg.num_hidden_layers, B, cfg.num_key_value_heads, cfg.head_dim,
+                                        T + n + 16, block_size=16, hot_fraction=1.0, warm_fraction=0.0,
+                                        policy_mode="hot_warm", policy_interval=64, device=device)
+        hlog = c5_forced(model, prompt, dtoks[:, :n], hot_rt.cache, runtime=hot_rt)
+        hot_rt.check_errors()
+        err = (hlog.float() - dlog.float()).abs()
+        agreement = {"steps": n, "max_abs_logit_err": round(err.max().item(), 5),
+                     "mean_abs_logit_err": round(err.mean().item(), 6),
+                     "logit_std": round(dlog.float().std().item(), 4),
+                     "argmax_agreement": round((hlog.argmax(-1) == dlog.argmax(-1)).float().mean().item(), 4),
+                     "floor_dense_eager_vs_sdpa": {"max_abs_logit_err": round(floor.max().item(), 5),
+                                                   "mean_abs_logit_err": round(floor.mean().item(), 6)}}
+        log(f"[c5] all-HOT vs dense (teacher-forced): {agreement}")
+        del hot_rt, hlog, dlog
     hf_llama.uninstall()
     line = {
         "metric": C5_METRIC,
@@ -906,6 +973,10 @@ def run_c5(args, device):
                    "cold": "masked", "attention": "tiered HIP decode kernel; prefill via the model's SDPA",
                    "decode_steps_as": mode},
         "tiered_eager_steps": eager,
+        # Eager against eager: the HIP-graph figure above has no stock
+        # counterpart (transformers' decode loop runs eagerly).
+        "like_for_like_eager": like_for_like,
+        "all_hot_vs_dense_teacher_forced": agreement,
         # Headline memory figure: the HBM the tiered pools hold (allocated,
         # free slots included) against the dense fp16 cache; the bytes of the
         # blocks resident at the end beside it.
@@ -1088,7 +1159,66 @@ def run_decode(args, device):
     }
     if ratio is not None:
         line["score_path"] = ratio
+    if (args.workload == "c3" and fmt == "absmax_i8" and args.cold == "masked" and not scores and not args.splits
+            and not args.no_extras):
+        del plans, layers
+        torch.cuda.empty_cache()
+        line["extra_decode_figures"] = extra_decode_figures(args, device, sec)
     print(json.dumps(line), flush=True)
+
+
+def extra_decode_figures(args, device, c3_sec):
+    """The other decode lines of the scope, timed right after the headline C3
+    line and the same way (prepared launches, ``--layers`` rotated buffers,
+    warm-up, then exactly ``--steps`` launches between HIP events): C3 with
+    score sums (the policy step's launch) and its no-score/score ratio, C3 in
+    the reference WARM format with zero-logit COLD (the drop-in's default),
+    and C4 with and without score sums.  Each has its own profile summary
+    under profiles/."""
+    import argparse
+
+    import torch
+
+    from paged_tierkv_amd import workloads as W
+    from paged_tierkv_amd.tierkv_hip import PreparedDecode, workspace_error_word
+
+    def timed(workload, fmt, cold, scores):
+        a = argparse.Namespace(**vars(args))
+        a.workload, a.warm_format, a.cold, a.scores = workload, fmt, cold, scores
+        layers = build_layers(a, device)
+        case = layers[0]["case"]
+        nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim,
+                               warm_format=fmt, return_scores=scores)
+        plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=cold) for L in layers]
+        for i in range(max(args.warmup, 4 * len(plans))):
+            plans[i % len(plans)].launch()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(args.steps):
+            plans[i % len(plans)].launch()
+        e1.record()
+        torch.cuda.synchronize()
+        assert workspace_error_word(device) == 0, "kernel flagged an out-of-range slot"
+        sec = e0.elapsed_time(e1) / 1e3 / args.steps
+        del plans, layers
+        torch.cuda.empty_cache()
+        gbs = nbytes / sec / 1e9
+        out = {"workload": _decode_tag(case.name, fmt, cold, scores), "us_per_layer_step": round(sec * 1e6, 3),
+               "achieved_GBps": round(gbs, 2), "frac": round(gbs / PEAK_HBM_GBS, 4), "ideal_bytes_per_step": nbytes}
+        log(f"[bench] extra {out['workload']}: {out['us_per_layer_step']} us, {gbs / PEAK_HBM_GBS:.1%} of peak")
+        return out, sec
+
+    res = {}
+    c3s, sec = timed("c3", "absmax_i8", "masked", True)
+    c3s["no_score_over_score"] = round(c3_sec / sec, 4)
+    res["c3_scores"] = c3s
+    res["c3_ref_u8_zero_logit"], _ = timed("c3", "ref_u8", "zero_logit", False)
+    res["c4"], c4_sec = timed("c4", "absmax_i8", "masked", False)
+    c4s, sec = timed("c4", "absmax_i8", "masked", True)
+    c4s["no_score_over_score"] = round(c4_sec / sec, 4)
+    res["c4_scores"] = c4s
+    res["reference_no_score_over_score_a10g"] = "0.73-0.86"
+    return res
 
 
 def _decode_tag(name, fmt, cold, scores):
