@@ -64,6 +64,7 @@ constexpr int MAX_SPLIT_UNITS = 1 << 16;   // units per launch when a unit is sp
 constexpr float PBOOST = 64.f;     // P is scaled by 2^6 before its fp16 cast
 constexpr float LAZY_T = 8.f;      // log2 headroom of the running maximum
 constexpr float FOLD_MAX = 2.f;    // WARM V scales above this are applied to V
+constexpr uint32_t FOLD_MAX_F16 = 0x4000u;   // FOLD_MAX as an fp16 bit pattern
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr float BIAS_I8 = 1152.f;  // fp16 value of an int8 code c is 1152 + c
 constexpr float BIAS_U8 = 1024.f;  // fp16 value of a uint8 code u is 1024 + u
@@ -149,9 +150,13 @@ __device__ __forceinline__ void lds_barrier() {
 //      segments);
 //   v: tokens 4g + j (j = 0..3), dims n*D/16 .. +D/16 (row j at v[j*RW]);
 // HOT tiles as fp16 pairs, WARM tiles as 8-bit codes plus metadata
-// (absmax: s_k, s_v; reference format: fp16 pairs of the per-token k scale,
-// k zero, v scale and v zero of tokens 4g .. 4g+3).  The two tiers have their
-// own registers: each tile loop is straight-line code for one tier.
+// (absmax: s_k, s_v, two 4-byte loads).  The reference format's four
+// per-token rows (k scale, k zero, v scale, v zero of the (block, head), 32
+// bytes each) are one load instruction: lane 4q + a of each quad fetches
+// row a's 8 bytes for tokens 4g .. 4g+3, and warm_meta spreads them over
+// the quad with DPP broadcasts when the tile is processed (four separate
+// loads: C3 40.7 us; one: 39.9 us).  The two tiers have their own
+// registers: each tile loop is straight-line code for one tier.
 template <int D>
 struct HotTile {
   static constexpr int RW = D / 32;   // dwords per V row
@@ -162,11 +167,34 @@ struct HotTile {
 template <int D, int WF>
 struct WarmTile {
   static constexpr int RW = D / 64;
-  static constexpr int NM = (WF == TIERKV_WARM_ABSMAX_I8) ? 2 : 8;
+  static constexpr int NR = 2;                                        // metadata dwords as loaded
+  static constexpr int NM = (WF == TIERKV_WARM_ABSMAX_I8) ? 2 : 8;   // after warm_meta
   uint32_t k[D / 16];
   uint32_t v[D / 16];
-  uint32_t m[NM];
+  uint32_t mr[NR];
 };
+
+// Value of lane 4 * (lane / 4) + A (DPP quad_perm [A, A, A, A]).
+template <int A>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), A * 0x55, 0xf, 0xf, false));
+}
+
+// The tile's metadata in every lane: absmax m[0] = s_k, m[1] = s_v;
+// reference format m[0..7] = fp16 pairs of the k scale, k zero, v scale and
+// v zero of tokens 4g .. 4g+3.
+template <int D, int WF>
+__device__ __forceinline__ void warm_meta(const WarmTile<D, WF>& t, uint32_t* m) {
+  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
+    m[0] = t.mr[0];
+    m[1] = t.mr[1];
+  } else {
+    m[0] = quad_bcast<0>(t.mr[0]); m[1] = quad_bcast<0>(t.mr[1]);
+    m[2] = quad_bcast<1>(t.mr[0]); m[3] = quad_bcast<1>(t.mr[1]);
+    m[4] = quad_bcast<2>(t.mr[0]); m[5] = quad_bcast<2>(t.mr[1]);
+    m[6] = quad_bcast<3>(t.mr[0]); m[7] = quad_bcast<3>(t.mr[1]);
+  }
+}
 
 // Tile loads go through buffer resources built per tile in scalar registers
 // (base = the tile's first byte, num_records = its size).  A dead load (a
@@ -195,6 +223,34 @@ constexpr int TILE_CPOL = TIERKV_TILE_CPOL;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, RSRC_WORD3);
+}
+
+// Where a WARM tile's metadata comes from, set up once per workgroup:
+// absmax, one buffer resource per scale array (a tile's scale is an offset
+// into it, and a dead pipeline step's offset is the array's size, which
+// reads nothing); the reference format, this lane's row array (the piece it
+// loads for every tile).  Resources per tile would hold four more scalar
+// registers per tile in flight, which the long-row kernels do not have.
+template <int WF>
+struct WarmMeta {
+  __amdgpu_buffer_rsrc_t ks, vs;   // absmax
+  uint32_t bytes;                  // absmax: size of each scale array
+  const char* row;                 // reference format
+};
+
+template <int WF>
+__device__ __forceinline__ WarmMeta<WF> warm_meta_setup(const DecodeParams& p, int lane) {
+  WarmMeta<WF> m{};
+  if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
+    // The host keeps warm_slots * kv_heads * 4 below 2^32.
+    m.bytes = uint32_t(p.warm_slots * p.kv_heads * 4);
+    m.ks = tile_rsrc(p.k_scale, m.bytes);
+    m.vs = tile_rsrc(p.v_scale, m.bytes);
+  } else {
+    const int a = lane & 3;
+    m.row = static_cast<const char*>(a == 0 ? p.k_scale : a == 1 ? p.k_zero : a == 2 ? p.v_scale : p.v_zero);
+  }
+  return m;
 }
 
 template <int D>
@@ -228,8 +284,8 @@ __device__ __forceinline__ void load_hot(const DecodeParams& p, int kvh, int slo
 }
 
 template <int D, int WF>
-__device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int slot, int lane, WarmTile<D, WF>& t,
-                                          bool live) {
+__device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int slot, int lane, const WarmMeta<WF>& wm,
+                                          WarmTile<D, WF>& t, bool live) {
   const int n = lane & 15;
   const int g = lane >> 4;
   constexpr uint32_t TILE = FBS * D;
@@ -255,25 +311,16 @@ __device__ __forceinline__ void load_warm(const DecodeParams& p, int kvh, int sl
     }
   }
   if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-    const int64_t si = int64_t(slot) * p.kv_heads + kvh;
-    const auto rs = tile_rsrc(reinterpret_cast<const float*>(p.k_scale) + si, live ? 4u : 0u);
-    const auto rz = tile_rsrc(reinterpret_cast<const float*>(p.v_scale) + si, live ? 4u : 0u);
-    t.m[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, 0, 0, 0);
-    t.m[1] = __builtin_amdgcn_raw_buffer_load_b32(rz, 0, 0, 0);
+    const uint32_t so = live ? (uint32_t(slot) * uint32_t(p.kv_heads) + uint32_t(kvh)) * 4u : wm.bytes;
+    t.mr[0] = __builtin_amdgcn_raw_buffer_load_b32(wm.ks, 0, so, 0);
+    t.mr[1] = __builtin_amdgcn_raw_buffer_load_b32(wm.vs, 0, so, 0);
   } else {
-    // Per-token fp16 scale and zero of tokens 4g .. 4g+3 (8-byte aligned).
-    constexpr uint32_t META = FBS * 2;
-    const int mo = 8 * g;
-    const auto r0 = tile_rsrc(reinterpret_cast<const __half*>(p.k_scale) + tile0, live ? META : 0u);
-    const auto r1 = tile_rsrc(reinterpret_cast<const __half*>(p.k_zero) + tile0, live ? META : 0u);
-    const auto r2 = tile_rsrc(reinterpret_cast<const __half*>(p.v_scale) + tile0, live ? META : 0u);
-    const auto r3 = tile_rsrc(reinterpret_cast<const __half*>(p.v_zero) + tile0, live ? META : 0u);
-    const u32x2 ks = __builtin_amdgcn_raw_buffer_load_b64(r0, mo, 0, 0);
-    const u32x2 kz = __builtin_amdgcn_raw_buffer_load_b64(r1, mo, 0, 0);
-    const u32x2 vs = __builtin_amdgcn_raw_buffer_load_b64(r2, mo, 0, 0);
-    const u32x2 vz = __builtin_amdgcn_raw_buffer_load_b64(r3, mo, 0, 0);
-    t.m[0] = ks.x; t.m[1] = ks.y; t.m[2] = kz.x; t.m[3] = kz.y;
-    t.m[4] = vs.x; t.m[5] = vs.y; t.m[6] = vz.x; t.m[7] = vz.y;
+    // One load (the slot of a dead step is a clamped list entry, in range,
+    // so the load needs no guard).
+    // Row a of the (block, head): 16 fp16 values, this lane's tokens 4g .. 4g+3.
+    const u32x2 x = *reinterpret_cast<const u32x2*>(wm.row + (tile0 + 4 * g) * 2);
+    t.mr[0] = x.x;
+    t.mr[1] = x.y;
   }
 }
 
@@ -407,6 +454,8 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
                                              float* s_stage, WaveState<D>& ws) {
   constexpr int DS = D / 16;
   constexpr int RW = WarmTile<D, WF>::RW;
+  uint32_t m[WarmTile<D, WF>::NM];
+  warm_meta<D, WF>(t, m);
   // S^T = (K + offset) Q^T with the codes as exact fp16 integers.
   f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -416,17 +465,17 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
   }
   float x[4], pr[4];
   if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-    const float c1 = p.scale_log2 * __uint_as_float(t.m[0]);
+    const float c1 = p.scale_log2 * __uint_as_float(m[0]);
     const float c0 = -BIAS_I8 * qsum * c1;
 #pragma unroll
     for (int r = 0; r < 4; ++r) x[r] = fmaf(sacc[r], c1, c0);
   } else {
+    // s * (S' - (1024 + z) * qsum): the offset is subtracted before the
+    // scale, so the cancellation happens between two values of one size.
+    const float q1024 = BIAS_U8 * qsum;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float c1 = p.scale_log2 * half_of(&t.m[0], r);
-      const float c0 = -(BIAS_U8 + half_of(&t.m[2], r)) * qsum * c1;
-      x[r] = fmaf(sacc[r], c1, c0);
-    }
+    for (int r = 0; r < 4; ++r)
+      x[r] = (sacc[r] - fmaf(half_of(&m[2], r), qsum, q1024)) * (p.scale_log2 * half_of(&m[0], r));
   }
   mask_tail(x, lane >> 4, len);
   softmax_step<D, SCORES>(p, x, pr, lane, head_ok, b, qh, si, s_stage, ws);
@@ -440,7 +489,7 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
   };
   uint32_t vt[DS];
   if constexpr (WF == TIERKV_WARM_ABSMAX_I8) {
-    const float sv = __uint_as_float(t.m[1]);
+    const float sv = __uint_as_float(m[1]);
     if (sv <= FOLD_MAX) {
       const float f = PBOOST * sv;
       const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * f, pr[1] * f), pack_f16x2(pr[2] * f, pr[3] * f));
@@ -471,26 +520,35 @@ __device__ __forceinline__ void process_warm(const DecodeParams& p, const WarmTi
     }
   } else {
     transpose_v(vt);
-    float sv[4], zv[4];
-    bool big = false;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      sv[r] = half_of(&t.m[4], r);
-      zv[r] = half_of(&t.m[6], r);
-      big = big || (sv[r] > FOLD_MAX);
-    }
-    if (!__any(big)) {
-      const uint32_t p01 = pack_f16x2(pr[0] * (PBOOST * sv[0]), pr[1] * (PBOOST * sv[1]));
-      const uint32_t p23 = pack_f16x2(pr[2] * (PBOOST * sv[2]), pr[3] * (PBOOST * sv[3]));
-      // The offset (1024 + zero) is removed with the fp16 P values the MFMA uses.
-      ws.corr += half_lo(p01) * (BIAS_U8 + zv[0]) + half_hi(p01) * (BIAS_U8 + zv[1]) +
-                 half_lo(p23) * (BIAS_U8 + zv[2]) + half_hi(p23) * (BIAS_U8 + zv[3]);
-      const f16x4 pf = as_f16x4(p01, p23);
+    // A scale above FOLD_MAX (or a negative or non-finite one) takes the
+    // unfolded path: a positive fp16 orders as its bit pattern, and every
+    // other pattern compares above FOLD_MAX's.
+    const uint32_t smax = max(max(m[4] & 0xffffu, m[4] >> 16), max(m[5] & 0xffffu, m[5] >> 16));
+    if (!__any(smax > FOLD_MAX_F16)) {
+      // P * PBOOST rounded to fp16, then times the fp16 scale (packed fp16:
+      // at most a second rounding of 2^-11 on each P).
+      const f16x2 pb01 = as_f16x2(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST));
+      const f16x2 pb23 = as_f16x2(pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
+      const f16x4 pf = as_f16x4(bits_of(pb01 * as_f16x2(m[4])), bits_of(pb23 * as_f16x2(m[5])));
+      // The offset (1024 + zero) is removed with the fp16 P values the MFMA
+      // multiplies: an A operand whose four k values are this lane's tokens'
+      // 1024 + zero (exact fp16 integers) gives sum_t (1024 + zero_t) P_t per
+      // head in every element.
+      const f16x2 b1024 = {_Float16(BIAS_U8), _Float16(BIAS_U8)};
+      const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+      ws.ocorr += __builtin_amdgcn_mfma_f32_16x16x16f16(
+          as_f16x4(bits_of(as_f16x2(m[6]) + b1024), bits_of(as_f16x2(m[7]) + b1024)), pf, zero4, 0, 0, 0)[0];
 #pragma unroll
       for (int s = 0; s < DS; ++s)
         ws.acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(u8x4_plus1024(vt[s]), pf, ws.acc[s], 0, 0, 0);
     } else {
       // (u - zero) * scale per token in fp32, as the reference kernel does.
+      float sv[4], zv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sv[r] = half_of(&m[4], r);
+        zv[r] = half_of(&m[6], r);
+      }
       const f16x4 pf = as_f16x4(pack_f16x2(pr[0] * PBOOST, pr[1] * PBOOST), pack_f16x2(pr[2] * PBOOST, pr[3] * PBOOST));
 #pragma unroll
       for (int s = 0; s < DS; ++s) {
@@ -629,14 +687,29 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   __shared__ float s_ts[16];
 
   const int G = p.groups;
-  // kv heads (low 16 bits) and splits (high 16 bits) share one preloaded
-  // argument, so that the split magic (used by the rank) is preloaded too.
+  // kv heads (bits 0-15), splits (bits 16-30) and the XCD placement flag
+  // (bit 31, below) share one preloaded argument, so that the split magic
+  // (used by the rank) is preloaded too.
   const int a_kv_heads = a_kvh_splits & 0xffff;
-  const int splits = int(uint32_t(a_kvh_splits) >> 16);
-  const int split = blockIdx.x % splits;
-  const int unit = int(blockIdx.x) / splits;
-  const int b = unit / a_kv_heads;
-  const int kvh = unit % a_kv_heads;
+  const int splits = int((uint32_t(a_kvh_splits) >> 16) & 0x7fffu);
+  // Unsplit launches of a batch that is a multiple of the 8 XCDs (bit 31):
+  // the hardware deals consecutive workgroups to the XCDs in turn, so
+  // workgroup i serves sequence 8 * (s / kv_heads) + i % 8 and kv head
+  // s % kv_heads with s = i / 8, and the kv heads of one sequence run on one
+  // XCD.  Their per-token scale / zero rows of the reference WARM format
+  // share cache lines (four heads' 32-byte rows in a 128-byte line), which
+  // that XCD's L2 then fetches once (traffic 1.074x -> 1.002x of ideal at
+  // C3), and the sequence's table row is fetched once per XCD.  The flag is
+  // decided on the host and the mapping has no branch, so nothing delays
+  // the first table loads (a branch here let the compiler place the
+  // parameter-block loads and their wait ahead of them: C4 +0.3 us).
+  const bool xcd_seq = a_kvh_splits < 0;
+  const int u = (int(blockIdx.x) >> (xcd_seq ? 3 : 0)) / splits;   // splits == 1 when xcd_seq
+  const int bq = u / a_kv_heads;
+  const int b = xcd_seq ? 8 * bq + int(blockIdx.x & 7u) : bq;
+  const int kvh = u - bq * a_kv_heads;
+  const int split = int(blockIdx.x) % splits;
+  const int unit = b * a_kv_heads + kvh;
   const int tid = threadIdx.x;
   constexpr int nthreads = NW * 64;
   constexpr int nw = NW;
@@ -1032,6 +1105,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     }
   }
   if (nwarm > 0) {
+    const WarmMeta<WF> wm = warm_meta_setup<WF>(p, lane);
     WarmTile<D, WF> tw[NBW];
     int4 ew[NBW];
     bool lw[NBW];
@@ -1042,7 +1116,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
     for (int k = 0; k < NBW - 1; ++k) {
       ew[k] = ne;
       lw[k] = nl;
-      load_warm<D, WF>(p, kvh, uniform(ne.y), lane, tw[k], nl);
+      load_warm<D, WF>(p, kvh, uniform(ne.y), lane, wm, tw[k], nl);
       __builtin_amdgcn_sched_barrier(0);
       gi = grab(0);
       ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
@@ -1054,7 +1128,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         const int kn = (k + NBW - 1) % NBW;
         ew[kn] = ne;
         lw[kn] = nl;
-        load_warm<D, WF>(p, kvh, uniform(ne.y), lane, tw[kn], nl);
+        load_warm<D, WF>(p, kvh, uniform(ne.y), lane, wm, tw[kn], nl);
         __builtin_amdgcn_sched_barrier(0);
         gi = grab(0);
         ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
@@ -1639,7 +1713,9 @@ static void launch_nw(const DecodeParams& p, bool long_rows, int grid, hipStream
   if (SC && p.lds_stage == STAGE_LDS_BLOCK) shmem += size_t(p.groups) * p.num_blocks * 2 * sizeof(float);
   if (SC && p.lds_stage == STAGE_LDS_LIST) shmem += size_t(p.groups) * MAX_LIST * 2 * sizeof(float);
   const int32_t stride = int32_t(p.table_stride);
-  const int32_t kvh_splits = int32_t(uint32_t(p.kv_heads) | (uint32_t(p.splits) << 16));
+  const bool xcd_seq = p.splits == 1 && p.batch % 8 == 0;   // see tiered_decode_kernel
+  const int32_t kvh_splits =
+      int32_t(uint32_t(p.kv_heads) | (uint32_t(p.splits) << 16) | (xcd_seq ? 0x80000000u : 0u));
   if (long_rows)
     hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, true>), dim3(grid), dim3(NW * 64), shmem, stream,
                        p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, kvh_splits,
@@ -1737,6 +1813,8 @@ int32_t tierkv::decode_check_args(
     return fail(TIERKV_ERR_INVALID, "WARM pools and scales are required (pass 1-slot placeholders when empty)");
   if (warm_format == TIERKV_WARM_REF_U8 && (!k_zero || !v_zero))
     return fail(TIERKV_ERR_INVALID, "reference-format WARM pools need zero points");
+  if (warm_format == TIERKV_WARM_ABSMAX_I8 && warm_slots * num_kv_heads * 4 > int64_t(0xffffffff))
+    return fail(TIERKV_ERR_UNSUPPORTED, "absmax scale arrays of 4 GiB or more");
   if (int64_t(batch) * num_kv_heads > (int64_t(1) << 24))
     return fail(TIERKV_ERR_UNSUPPORTED, "batch * kv_heads too large");
   const bool scores = score_sums != nullptr;
@@ -1753,8 +1831,8 @@ int32_t tierkv::decode_check_args(
       if (m & 7u) return fail(TIERKV_ERR_INVALID, "reference-format scale/zero pools must be 8-byte aligned");
     }
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, groups, splits_hint);
-    if (pl.splits > 0xffff || num_kv_heads > 0xffff)
-      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or splits");
+    if (pl.splits > 0x7fff || num_kv_heads > 0xffff)
+      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or 32767 splits");
     int64_t seqs_per_chunk = batch;
     if (pl.splits > 1) {
       seqs_per_chunk = MAX_SPLIT_UNITS / num_kv_heads;

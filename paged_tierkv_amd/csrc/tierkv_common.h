@@ -50,6 +50,7 @@ int32_t decode_check_args(
 // ---- device helpers -------------------------------------------------------
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
@@ -160,6 +161,9 @@ __device__ __forceinline__ f16x4 as_f16x4(uint32_t lo, uint32_t hi) {
   c.u[1] = hi;
   return c.v;
 }
+
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
+__device__ __forceinline__ uint32_t bits_of(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
   __half2 h = __floats2half2_rn(a, b);
