@@ -658,9 +658,9 @@ def run_c2b(args, device):
            "hot_budget": W.C2B_HOT_BUDGET, "warm_budget": W.C2B_WARM_BUDGET, "prob_buffers_rotated": len(bufs)}
     line = _line(C2B_METRIC, round(sec * 1e6, 3), "µs", steps, 20, sec, "f32", cfg,
                  ideal_bytes_per_step=nbytes, block_mass_us=round(msec * 1e6, 3),
-                 roofline={"kernel": "block_mass_vec4_kernel", "bound": "hbm", "achieved": round(gbs, 2),
+                 roofline={"kernel": "block_mass_staged_kernel", "bound": "hbm", "achieved": round(gbs, 2),
                            "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
-                           "traffic": _profile_traffic("block_mass_vec4_kernel", cfg["workload"])},
+                           "traffic": _profile_traffic("block_mass_staged_kernel", cfg["workload"])},
                  cpu_baseline=cpu)
     line["higher_is_better"] = False
     print(json.dumps(line), flush=True)

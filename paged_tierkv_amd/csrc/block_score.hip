@@ -15,6 +15,8 @@
 
 #include "tierkv_common.h"
 
+#include <algorithm>
+
 namespace tierkv {
 
 __global__ __launch_bounds__(256) void block_mass_kernel(const float* __restrict__ probs,
@@ -41,40 +43,60 @@ __global__ __launch_bounds__(256) void block_mass_kernel(const float* __restrict
   }
 }
 
-// The same reduction with four consecutive tokens per thread (block_size a
-// power of two >= 4, probs 16-byte aligned): each thread keeps up to 32
-// 16-byte head-row loads in flight at once, sums every token over the heads
-// in order, folds its four tokens as (t0 + t1) + (t2 + t3) and the lanes of
-// one block with an xor butterfly -- the same pairwise tree as
-// block_mass_kernel, so the results are bit-identical.
-constexpr int MASS_T = 128;   // threads per workgroup (512 tokens)
-constexpr int MASS_BATCH = 32;   // head rows loaded before they are summed
+// The same reduction for block_size a power of two >= 4 and 16-byte aligned
+// probabilities, staged through LDS.  A workgroup of MASS_T threads covers
+// MASS_Q four-token quads (256 tokens) of one sequence; per round of MASS_HC
+// heads each of its MASS_T / MASS_Q head groups loads MASS_HPG head rows of
+// the quads (16-byte loads, every thread's loads in flight together) into
+// LDS, and the first wave sums every quad's heads in order from there.  The
+// tokens of a quad are folded as (t0 + t1) + (t2 + t3) and the lanes of one
+// block with an xor butterfly -- the same pairwise tree as block_mass_kernel,
+// so the results are bit-identical.  Many small loads per workgroup from
+// all of its waves reach HBM sooner than a few waves with long load queues.
+constexpr int MASS_T = 512;                 // threads per workgroup
+constexpr int MASS_Q = 64;                  // token quads per workgroup
+constexpr int MASS_HC = 32;                 // heads staged per round
+constexpr int MASS_HPG = MASS_HC / (MASS_T / MASS_Q);   // head rows per thread and round
+static_assert(MASS_HPG * (MASS_T / MASS_Q) == MASS_HC, "head groups must tile a round");
 
-__global__ __launch_bounds__(MASS_T) void block_mass_vec4_kernel(const float* __restrict__ probs,
-                                                                  const int32_t* __restrict__ lengths,
-                                                                  float* __restrict__ out, int heads,
-                                                                  int tokens, int bs, int nblk) {
+__global__ __launch_bounds__(MASS_T) void block_mass_staged_kernel(const float* __restrict__ probs,
+                                                                    const int32_t* __restrict__ lengths,
+                                                                    float* __restrict__ out, int heads,
+                                                                    int tokens, int bs, int nblk) {
+  __shared__ f32x4 st[MASS_HC][MASS_Q];
   const int b = blockIdx.y;
-  const int tok0 = (blockIdx.x * MASS_T + threadIdx.x) * 4;
-  const bool in = tok0 < tokens;
+  const int tid = threadIdx.x;
+  const int q = tid % MASS_Q, g = tid / MASS_Q;
+  const int quad0 = blockIdx.x * MASS_Q;
+  const bool in_ld = (quad0 + q) * 4 < tokens;
+  const f32x4* p = reinterpret_cast<const f32x4*>(probs + int64_t(b) * heads * tokens) + quad0 + q;
+  const int64_t row = tokens / 4;
   float a[4] = {0.f, 0.f, 0.f, 0.f};
-  if (in) {
-    const f32x4* p = reinterpret_cast<const f32x4*>(probs + int64_t(b) * heads * tokens + tok0);
-    const int64_t row = tokens / 4;
-    for (int h0 = 0; h0 < heads; h0 += MASS_BATCH) {
-      f32x4 v[MASS_BATCH];
+  for (int h0 = 0; h0 < heads; h0 += MASS_HC) {
+    f32x4 v[MASS_HPG];
 #pragma unroll
-      for (int k = 0; k < MASS_BATCH; ++k)
-        if (h0 + k < heads) v[k] = __builtin_nontemporal_load(p + (h0 + k) * row);
+    for (int k = 0; k < MASS_HPG; ++k) {
+      const int h = h0 + MASS_HPG * g + k;
+      if (in_ld && h < heads) v[k] = __builtin_nontemporal_load(p + h * row);
+    }
+    if (h0 > 0) __syncthreads();   // the previous round's sums have read the stage
 #pragma unroll
-      for (int k = 0; k < MASS_BATCH; ++k) {
-        if (h0 + k < heads) {
+    for (int k = 0; k < MASS_HPG; ++k)
+      if (in_ld && h0 + MASS_HPG * g + k < heads) st[MASS_HPG * g + k][q] = v[k];
+    __syncthreads();
+    if (tid < MASS_Q && in_ld) {
+      const int hn = min(MASS_HC, heads - h0);
+#pragma unroll 8
+      for (int h = 0; h < hn; ++h) {
+        const f32x4 x = st[h][tid];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a[e] += v[k][e];
-        }
+        for (int e = 0; e < 4; ++e) a[e] += x[e];
       }
     }
   }
+  if (tid >= MASS_Q) return;
+  const int tok0 = (quad0 + tid) * 4;
+  const bool in = tok0 < tokens;
   const int blk = in ? tok0 / bs : 0;
   const int pos = tok0 - blk * bs;
   const int len = !in ? 0 : (lengths ? min(max(lengths[int64_t(b) * nblk + blk], 0), bs) : bs);
@@ -103,58 +125,87 @@ __global__ __launch_bounds__(256) void scores_from_sums_kernel(const float* __re
 }
 
 constexpr int LABEL_MAX_BLOCKS = 8192;
-constexpr int LABEL_T = 1024;   // threads per sequence
+constexpr int LABEL_WAVES = 4;                             // waves per workgroup
+constexpr int LABEL_CAND = 4;                              // candidates per wave and pass
+constexpr int LABEL_GROUP = LABEL_WAVES * LABEL_CAND;      // candidates per workgroup and pass
+constexpr int LABEL_MAX_WG = 16;                           // workgroups per sequence
 
-// One workgroup per sequence.  Each candidate's rank is counted by `par`
-// adjacent lanes (par = 1, 2, 4 or 8, as many as the 1024 threads allow),
-// lane k of the group counting the candidates j = 1 + k, 1 + k + par, ...,
-// so the lanes of a wave read consecutive keys; the partial counts are summed
-// over the group with lane shuffles.
-__global__ __launch_bounds__(LABEL_T) void tier_labels_kernel(const float* __restrict__ scores,
-                                                              const int32_t* __restrict__ cur,
-                                                              int32_t* __restrict__ out, int64_t stride,
-                                                              int n, int hot_budget, int warm_budget,
-                                                              int mode, int demoted_state) {
-  __shared__ __align__(16) uint64_t key[LABEL_MAX_BLOCKS];
-  const int b = blockIdx.x;
+__device__ __forceinline__ int tier_label(int rank, bool ranked, int c, int mode, int n, int extra_hot, int warm,
+                                          int demoted_state) {
+  int desired;
+  if (mode == 0) {
+    desired = c;                       // hot_only: enforce_policy returns early
+  } else if (!ranked) {
+    desired = HOT;                     // reserved {0, n-1}; n <= 2 -> all HOT
+  } else if (rank < extra_hot) {
+    desired = HOT;
+  } else if (mode == 2) {
+    desired = (rank < extra_hot + warm) ? WARM : COLD;
+  } else {
+    desired = demoted_state;
+  }
+  if (mode != 0 && n > 2 && c == COLD && desired != COLD) desired = COLD;   // COLD is sticky
+  return desired;
+}
+
+// Workgroups of LABEL_WAVES waves; min(ceil(n / LABEL_GROUP), LABEL_MAX_WG)
+// of them per sequence.  A workgroup stages the sequence's scores in LDS
+// once; each wave then takes LABEL_CAND candidates per pass and counts their
+// ranks with the competitors in its lanes: per 64 competitors and candidate
+// one 64-bit compare against the candidate's key (a wave-uniform value) and
+// the population count of the resulting lane mask.  Spreading the
+// candidates over the chip keeps each wave's count short.
+__global__ __launch_bounds__(64 * LABEL_WAVES) void tier_labels_kernel(const float* __restrict__ scores,
+                                                                       const int32_t* __restrict__ cur,
+                                                                       int32_t* __restrict__ out, int64_t stride,
+                                                                       int n, int hot_budget, int warm_budget,
+                                                                       int mode, int demoted_state) {
+  __shared__ float s_row[LABEL_MAX_BLOCKS];
+  const int b = blockIdx.y;
   const int tid = threadIdx.x;
-  for (int i = tid; i < n; i += LABEL_T) key[i] = label_key(scores[int64_t(b) * n + i], i);
-  __syncthreads();
+  const int lane = tid & 63;
+  const bool rank_needed = mode != 0 && n > 2;
+  if (rank_needed) {
+    for (int i = tid; i < n; i += 64 * LABEL_WAVES) s_row[i] = scores[int64_t(b) * n + i];
+    __syncthreads();
+  }
   const int extra_hot = max(hot_budget - 2, 0);
   const int warm = max(warm_budget, 0);
-  int lpar = 0;
-  while (lpar < 3 && (n << (lpar + 1)) <= LABEL_T) ++lpar;
-  const int par = 1 << lpar;
-  for (int t0 = 0; t0 < n * par; t0 += LABEL_T) {
-    const int t = t0 + tid;
-    const int i = t >> lpar;
-    const int part = t & (par - 1);
-    const bool ranked = i < n && mode != 0 && n > 2 && i != 0 && i != n - 1;
+  for (int c0 = (blockIdx.x * LABEL_WAVES + (tid >> 6)) * LABEL_CAND; c0 < n; c0 += gridDim.x * LABEL_GROUP) {
+    const int ci = c0 + lane;
+    const bool mine = lane < LABEL_CAND && ci < n;
+    const int c = mine ? cur[int64_t(b) * stride + ci] : 0;
     int rank = 0;
-    if (ranked) {
+    if (rank_needed) {
       // rank among the candidates j in [1, n - 1)
-      const uint64_t ki = key[i];
-      int j = 1 + part;
-#pragma unroll 4
-      for (; j < n - 1; j += par) rank += key[j] > ki ? 1 : 0;
-    }
-    for (int m = 1; m < par; m <<= 1) rank += __shfl_xor(rank, m, 64);
-    if (i < n && part == 0) {
-      const int c = cur[int64_t(b) * stride + i];
-      int desired;
-      if (mode == 0) {
-        desired = c;                       // hot_only: enforce_policy returns early
-      } else if (!ranked) {
-        desired = HOT;                     // reserved {0, n-1}; n <= 2 -> all HOT
-      } else if (rank < extra_hot) {
-        desired = HOT;
-      } else if (mode == 2) {
-        desired = (rank < extra_hot + warm) ? WARM : COLD;
-      } else {
-        desired = demoted_state;
+      const uint64_t kmine = label_key(s_row[min(ci, n - 1)], ci);
+      int cnt[LABEL_CAND];
+#pragma unroll
+      for (int k = 0; k < LABEL_CAND; ++k) cnt[k] = 0;
+      for (int j0 = 0; j0 < n; j0 += 256) {
+        uint64_t kj[4];
+        bool vj[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int j = j0 + 64 * e + lane;
+          vj[e] = j >= 1 && j < n - 1;
+          kj[e] = label_key(s_row[min(j, n - 1)], j);
+        }
+#pragma unroll
+        for (int k = 0; k < LABEL_CAND; ++k) {
+          const uint32_t lo = __builtin_amdgcn_readlane(uint32_t(kmine), k);
+          const uint32_t hi = __builtin_amdgcn_readlane(uint32_t(kmine >> 32), k);
+          const uint64_t kc = (uint64_t(hi) << 32) | lo;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) cnt[k] += __popcll(__builtin_amdgcn_ballot_w64(vj[e] && kj[e] > kc));
+        }
       }
-      if (mode != 0 && n > 2 && c == COLD && desired != COLD) desired = COLD;   // COLD is sticky
-      out[int64_t(b) * stride + i] = desired;
+#pragma unroll
+      for (int k = 0; k < LABEL_CAND; ++k) rank = lane == k ? cnt[k] : rank;
+    }
+    if (mine) {
+      const bool ranked = rank_needed && ci != 0 && ci != n - 1;
+      out[int64_t(b) * stride + ci] = tier_label(rank, ranked, c, mode, n, extra_hot, warm, demoted_state);
     }
   }
 }
@@ -175,10 +226,10 @@ extern "C" int32_t tierkv_block_mass_from_probs(const float* probs, const int32_
   if (batch > 65535) return fail(TIERKV_ERR_UNSUPPORTED, "batch too large");
   const int nblk = tokens / block_size;
   if (block_size >= 4 && aligned16(probs)) {
-    dim3 grid((tokens / 4 + MASS_T - 1) / MASS_T, batch);
-    hipLaunchKernelGGL(block_mass_vec4_kernel, grid, dim3(MASS_T), 0, reinterpret_cast<hipStream_t>(stream_),
+    dim3 grid((tokens / 4 + MASS_Q - 1) / MASS_Q, batch);
+    hipLaunchKernelGGL(block_mass_staged_kernel, grid, dim3(MASS_T), 0, reinterpret_cast<hipStream_t>(stream_),
                        probs, lengths, out, num_heads, tokens, block_size, nblk);
-    return check_launch("block_mass_vec4_kernel");
+    return check_launch("block_mass_staged_kernel");
   }
   dim3 grid((tokens + 255) / 256, batch);
   hipLaunchKernelGGL(block_mass_kernel, grid, dim3(256), 0, reinterpret_cast<hipStream_t>(stream_), probs,
@@ -214,7 +265,9 @@ extern "C" int32_t tierkv_tier_labels(const float* scores, const int32_t* cur_st
   if (mode == 1 && demoted_state != WARM && demoted_state != COLD)
     return fail(TIERKV_ERR_INVALID, "demoted_state must be WARM_STATE or COLD_STATE.");
   if (num_blocks > LABEL_MAX_BLOCKS) return fail(TIERKV_ERR_UNSUPPORTED, "too many blocks per sequence for the label kernel");
-  hipLaunchKernelGGL(tier_labels_kernel, dim3(batch), dim3(LABEL_T), 0, reinterpret_cast<hipStream_t>(stream_), scores,
+  if (batch > 65535) return fail(TIERKV_ERR_UNSUPPORTED, "batch too large");
+  const dim3 grid(std::min((num_blocks + LABEL_GROUP - 1) / LABEL_GROUP, LABEL_MAX_WG), batch);
+  hipLaunchKernelGGL(tier_labels_kernel, grid, dim3(64 * LABEL_WAVES), 0, reinterpret_cast<hipStream_t>(stream_), scores,
                      cur_states, new_states, states_stride, num_blocks, hot_budget, warm_budget, mode,
                      demoted_state);
   return check_launch("tier_labels_kernel");

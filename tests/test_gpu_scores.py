@@ -42,6 +42,44 @@ def test_block_mass_with_lengths_bit_exact(device):
         assert np.array_equal(_bits(got), _bits(exp)), f"bs={bs}"
 
 
+@pytest.mark.parametrize("shape", [(2, 40, 336, 16), (3, 71, 80, 4), (1, 1, 4, 4), (2, 33, 1024, 64),
+                                   (2, 32, 832, 8), (1, 96, 512, 32)])
+def test_block_mass_head_rounds_and_ragged_tiles_bit_exact(device, shape):
+    # heads beyond one 32-head LDS round, token counts that leave a partial
+    # 256-token workgroup, and the 4-byte-aligned (scalar) path
+    b, h, t, bs = shape
+    g = torch.Generator().manual_seed(sum(shape))
+    probs = torch.softmax(torch.randn((b, h, t), generator=g) * 2, dim=-1)
+    nblk = t // bs
+    lens = torch.randint(0, bs + 1, (b, nblk), generator=g, dtype=torch.int32)
+    print(f"[scores] block mass shape={shape}", flush=True)
+    for ln in (None, lens):
+        exp = opolicy.block_mass_from_probs(probs.numpy(), bs, None if ln is None else ln.numpy())
+        got = kernels.block_mass_from_probs(probs.to(device), bs, ln).cpu().numpy()
+        assert np.array_equal(_bits(got), _bits(exp)), f"aligned, lengths={ln is not None}"
+        flat = torch.empty(probs.numel() + 1, device=device)
+        un = flat[1:].view(b, h, t)
+        un.copy_(probs.to(device))
+        assert un.data_ptr() % 16 != 0
+        got = kernels.block_mass_from_probs(un, bs, ln).cpu().numpy()
+        assert np.array_equal(_bits(got), _bits(exp)), f"unaligned, lengths={ln is not None}"
+
+
+def test_labels_at_the_block_limit(device):
+    rng = np.random.default_rng(9)
+    n = 8192
+    scores = rng.integers(0, 50, (2, n)).astype(np.float32) / 7      # ties across passes
+    cur = rng.integers(0, 3, (2, n)).astype(np.int32)
+    print(f"[scores] labels n={n}", flush=True)
+    exp = opolicy.tier_labels(scores, cur, 300, 2000, "hot_warm_cold")
+    got = kernels.tier_labels(torch.from_numpy(scores).to(device), torch.from_numpy(cur).to(device), 300, 2000,
+                              "hot_warm_cold").cpu().numpy()
+    assert np.array_equal(got, exp)
+    with pytest.raises(RuntimeError, match="too many blocks"):
+        kernels.tier_labels(torch.zeros((1, n + 1), device=device), torch.zeros((1, n + 1), dtype=torch.int32,
+                                                                                 device=device), 3, 3)
+
+
 def test_c2b_labels_bit_exact(device):
     probs = W.config2b()
     mass = opolicy.block_mass_from_probs(probs.numpy(), 16)
