@@ -64,6 +64,9 @@ def parse():
                    help="c5: run decode steps eagerly only (no HIP-graph replay, no eager comparison run)")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--deterministic", action="store_true",
+                   help="decode workloads: fixed tile shares per wave (TIERKV_DECODE_DETERMINISTIC), so every "
+                        "launch's output is the same bits")
     p.add_argument("--no-extras", action="store_true",
                    help="default C3 line: skip the extra decode figures (C3 with scores, C3 in the reference WARM "
                         "format, C4 with and without scores) timed after the headline")
@@ -1062,8 +1065,8 @@ def run_decode(args, device):
     nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim,
                            warm_format=fmt, return_scores=scores)
 
-    plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=args.cold, splits=args.splits or None)
-             for L in layers]
+    plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=args.cold, splits=args.splits or None,
+                            deterministic=args.deterministic) for L in layers]
     # The first warm-up step of each layer runs before the ceiling
     # measurement: a kernel's first launch in a process loads its code object
     # (milliseconds of host time, the GPU idle meanwhile).
@@ -1092,8 +1095,8 @@ def run_decode(args, device):
         # score latency of the decode launch, 0.73-0.86 on an A10G
         # (main.py:3410-3412).  The same layers without scores, timed the
         # same way right after (clocks already steady).
-        plain = [PreparedDecode(**L["args"], return_scores=False, cold_mode=args.cold, splits=args.splits or None)
-                 for L in layers]
+        plain = [PreparedDecode(**L["args"], return_scores=False, cold_mode=args.cold, splits=args.splits or None,
+                                deterministic=args.deterministic) for L in layers]
         for i in range(max(args.warmup, len(plain))):
             plain[i % len(plain)].launch()
         f0, f1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -1115,8 +1118,10 @@ def run_decode(args, device):
     # HBM bytes per launch of the decode kernel from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE summary of this workload (copy-calibrated).
     traffic = None
-    tag = _decode_tag(case.name, fmt, args.cold, scores)
-    tpath = os.path.join(ROOT, "profiles", f"tiered_decode_kernel_{tag}_traffic.json")
+    tag = _decode_tag(case.name, fmt, args.cold, scores, args.deterministic)
+    # (the deterministic hand-out moves the same bytes: the default launch's profile)
+    tpath = os.path.join(ROOT, "profiles", f"tiered_decode_kernel_{_decode_tag(case.name, fmt, args.cold, scores)}"
+                                           "_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
@@ -1152,7 +1157,7 @@ def run_decode(args, device):
                    "kv_heads": case.kv_heads, "head_dim": case.head_dim, "block_size": case.block_size,
                    "blocks_per_seq": case.num_blocks, "tiers_per_seq": list(case.tier_counts()[0]),
                    "warm_format": fmt_name, "cold": args.cold, "return_scores": scores,
-                   "layers_rotated": args.layers},
+                   "deterministic": bool(args.deterministic), "layers_rotated": args.layers},
         "us_per_layer_step": round(sec * 1e6, 3),
         "tokens_per_s_32_layers": round(case.batch / (32 * sec), 1),
         "ideal_bytes_per_step": nbytes,
@@ -1165,7 +1170,7 @@ def run_decode(args, device):
     if ratio is not None:
         line["score_path"] = ratio
     if (args.workload == "c3" and fmt == "absmax_i8" and args.cold == "masked" and not scores and not args.splits
-            and not args.no_extras):
+            and not args.no_extras and not args.deterministic):
         del plans, layers
         torch.cuda.empty_cache()
         line["extra_decode_figures"] = extra_decode_figures(args, device, sec)
@@ -1178,8 +1183,9 @@ def extra_decode_figures(args, device, c3_sec):
     warm-up, then exactly ``--steps`` launches between HIP events): C3 with
     score sums (the policy step's launch) and its no-score/score ratio, C3 in
     the reference WARM format with zero-logit COLD (the drop-in's default),
-    and C4 with and without score sums.  Each has its own profile summary
-    under profiles/."""
+    C4 with and without score sums (each with its own profile summary under
+    profiles/), and C3 with the deterministic tile hand-out and its time
+    over the default launch's."""
     import argparse
 
     import torch
@@ -1187,14 +1193,14 @@ def extra_decode_figures(args, device, c3_sec):
     from paged_tierkv_amd import workloads as W
     from paged_tierkv_amd.tierkv_hip import PreparedDecode, workspace_error_word
 
-    def timed(workload, fmt, cold, scores):
+    def timed(workload, fmt, cold, scores, det=False):
         a = argparse.Namespace(**vars(args))
         a.workload, a.warm_format, a.cold, a.scores = workload, fmt, cold, scores
         layers = build_layers(a, device)
         case = layers[0]["case"]
         nbytes = W.ideal_bytes(case.block_states, case.num_blocks, case.num_heads, case.kv_heads, case.head_dim,
                                warm_format=fmt, return_scores=scores)
-        plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=cold) for L in layers]
+        plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=cold, deterministic=det) for L in layers]
         # Building the inputs leaves the GPU idle long enough for its clocks
         # to drop: keep it launching for >= 60 ms before the timed launches.
         t0, i = time.perf_counter(), 0
@@ -1215,7 +1221,7 @@ def extra_decode_figures(args, device, c3_sec):
         del plans, layers
         torch.cuda.empty_cache()
         gbs = nbytes / sec / 1e9
-        out = {"workload": _decode_tag(case.name, fmt, cold, scores), "us_per_layer_step": round(sec * 1e6, 3),
+        out = {"workload": _decode_tag(case.name, fmt, cold, scores, det), "us_per_layer_step": round(sec * 1e6, 3),
                "achieved_GBps": round(gbs, 2), "frac": round(gbs / PEAK_HBM_GBS, 4), "ideal_bytes_per_step": nbytes}
         log(f"[bench] extra {out['workload']}: {out['us_per_layer_step']} us, {gbs / PEAK_HBM_GBS:.1%} of peak")
         return out, sec
@@ -1229,11 +1235,14 @@ def extra_decode_figures(args, device, c3_sec):
     c4s, sec = timed("c4", "absmax_i8", "masked", True)
     c4s["no_score_over_score"] = round(c4_sec / sec, 4)
     res["c4_scores"] = c4s
+    c3d, sec = timed("c3", "absmax_i8", "masked", False, True)
+    c3d["over_default"] = round(sec / c3_sec, 4)
+    res["c3_deterministic"] = c3d
     res["reference_no_score_over_score_a10g"] = "0.73-0.86"
     return res
 
 
-def _decode_tag(name, fmt, cold, scores):
+def _decode_tag(name, fmt, cold, scores, det=False):
     """Workload name of a decode bench line (and of its profile files)."""
     tag = name
     if fmt != "absmax_i8":
@@ -1242,6 +1251,8 @@ def _decode_tag(name, fmt, cold, scores):
         tag += "_" + cold
     if scores:
         tag += "_scores"
+    if det:
+        tag += "_deterministic"
     return tag
 
 

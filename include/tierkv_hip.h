@@ -54,6 +54,13 @@ extern "C" {
 #define TIERKV_COLD_ZERO_LOGIT 0 /* reference: COLD tokens enter softmax with K=V=0 */
 #define TIERKV_COLD_MASKED 1     /* COLD blocks contribute nothing */
 
+/* Flag OR'ed into a decode call's splits_hint (whose low bits are the split
+ * factor, 0 = automatic): each wave takes a fixed share of the workgroup's
+ * tiles instead of taking them from a shared counter, so the attention output
+ * is the same bits on every call over the same inputs, as the reference's
+ * Triton kernel is.  Costs about 1-2 % of the launch time. */
+#define TIERKV_DECODE_DETERMINISTIC 0x40000000
+
 /* Message of the last failing call on this thread ("" if none). */
 TIERKV_API const char* tierkv_last_error(void);
 
@@ -80,6 +87,11 @@ TIERKV_API int32_t tierkv_abi_version(void);
  *   (and graph replays) on one stream; launches that share it must not
  *   overlap.
  * scaling  softmax scale (head_dim ** -0.5 in modeling_llama.py:315).
+ * splits_hint  split factor per (sequence, kv head) (0: chosen from the
+ *   launch size), optionally | TIERKV_DECODE_DETERMINISTIC.  Without the
+ *   flag, tiles are handed to waves as they free up: outputs agree with the
+ *   fp32 reference within tolerance but their last bits can differ between
+ *   calls.  Score sums are the same bits either way.
  */
 TIERKV_API int32_t tierkv_decode_attention(
     const void* query, int32_t query_dtype, void* out, float* score_sums,

@@ -31,6 +31,7 @@ WARM_REF_U8 = 0
 WARM_ABSMAX_I8 = 1
 COLD_ZERO_LOGIT = 0
 COLD_MASKED = 1
+DECODE_DETERMINISTIC = 0x40000000   # OR'ed into a decode call's splits hint
 
 _P = c_void_p
 _I32P = POINTER(c_int32)

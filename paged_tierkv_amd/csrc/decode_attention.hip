@@ -95,6 +95,7 @@ struct DecodeParams {
   int32_t splits;
   uint32_t split_magic;   // ceil(2^32 / splits) when num_blocks * splits < 2^32, else 0
   int32_t lds_stage;      // where score statistics are staged (STAGE_* below)
+  int32_t deterministic;  // host only: fixed tile shares per wave (TIERKV_DECODE_DETERMINISTIC)
   float* ws_acc;      // [units][splits][G][D]
   float* ws_ml;       // [units][splits][G][2]
   float* ws_stage;    // [B][H][num_blocks][2]  per-block (max, sum) (split score launches)
@@ -681,6 +682,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   __shared__ int s_wcold[MAX_WAVES];
   __shared__ int s_last;
   __shared__ int s_next[2];                      // next WARM / HOT list position to hand out
+  __shared__ int s_prog[MAX_WAVES];              // deterministic launches: tiles taken per wave
   __shared__ float s_m[MAX_WAVES][16];
   __shared__ float s_l[MAX_WAVES][16];
   __shared__ float s_tm[16];                     // score finalisation: per (head, part) max and sum
@@ -691,7 +693,8 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   // (bit 31, below) share one preloaded argument, so that the split magic
   // (used by the rank) is preloaded too.
   const int a_kv_heads = a_kvh_splits & 0xffff;
-  const int splits = int((uint32_t(a_kvh_splits) >> 16) & 0x7fffu);
+  const int splits = int((uint32_t(a_kvh_splits) >> 16) & 0x3fffu);
+  const bool det = ((uint32_t(a_kvh_splits) >> 30) & 1u) != 0;
   // Unsplit launches of a batch that is a multiple of the 8 XCDs (bit 31):
   // the hardware deals consecutive workgroups to the XCDs in turn, so
   // workgroup i serves sequence 8 * (s / kv_heads) + i % 8 and kv head
@@ -786,6 +789,7 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   if (tid == 0) {
     s_next[0] = 0;
     s_next[1] = 0;
+    for (int i = 0; i < MAX_WAVES; ++i) s_prog[i] = 0;
   }
 
   // ---- query: issued right after the first table loads, converted once the
@@ -1077,86 +1081,112 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
   st.corr = 0.f;
   st.ocorr = 0.f;
 
-  auto grab = [&](int c) -> int {
-    int v = 0;
-    if (lane == 0) v = atomicAdd(&s_next[c], 1);
-    return uniform(v);
-  };
-  constexpr int NBH = TIERKV_NBH;
-  constexpr int NBW = TIERKV_NBW;
-  HotTile<D> th[NBH];
-  int4 eh[NBH];
-  bool lh[NBH];
-  int4 hne = make_int4(0, 0, 0, 0);   // next HOT entry to load and whether it is live
-  bool hnl = false;
-  if (nhot > 0) {
-    int gi = grab(1);
-    hne = s_list[min(gi, nhot - 1)];
-    hnl = gi < nhot;
-#pragma unroll
-    for (int k = 0; k < NBH - 1; ++k) {
-      eh[k] = hne;
-      lh[k] = hnl;
-      load_hot<D>(p, kvh, uniform(hne.y), lane, th[k], hnl);
-      __builtin_amdgcn_sched_barrier(0);
-      gi = grab(1);
+  // Tile hand-out.  By default a wave takes the next list position of the
+  // tier from an LDS counter when it frees up.  Deterministic launches give
+  // wave w the positions w, w + nw, ... of the WARM list and nw - 1 - w,
+  // 2 nw - 1 - w, ... of the HOT list (so that the waves left with one more
+  // WARM tile do not also get one more HOT tile): the order of every wave's
+  // accumulation is then fixed.  The two waves of a SIMD (w and w ^ 4) would
+  // otherwise progress unevenly -- the SIMD's arbiter favours the older one
+  // -- so the one behind raises its issue priority after every hand-out.
+  // The tile loops are instantiated once per hand-out (one uniform branch
+  // here): a check of the mode inside the loops cost the default hand-out
+  // 0.7 us at C3.
+  auto tile_loops = [&](auto DET) {
+    int kc0 = 0, kc1 = 0;
+    auto grab = [&](int c) -> int {
+      if constexpr (decltype(DET)::value) {
+        const int k = c ? kc1++ : kc0++;
+        if constexpr (NW == 8) {
+          if (lane == 0) s_prog[w] = kc0 + kc1;
+          if (uniform(s_prog[w ^ 4]) > kc0 + kc1) __builtin_amdgcn_s_setprio(1);
+          else __builtin_amdgcn_s_setprio(0);
+        }
+        return (c ? nw - 1 - w : w) + nw * k;
+      } else {
+        int v = 0;
+        if (lane == 0) v = atomicAdd(&s_next[c], 1);
+        return uniform(v);
+      }
+    };
+    constexpr int NBH = TIERKV_NBH;
+    constexpr int NBW = TIERKV_NBW;
+    HotTile<D> th[NBH];
+    int4 eh[NBH];
+    bool lh[NBH];
+    int4 hne = make_int4(0, 0, 0, 0);   // next HOT entry to load and whether it is live
+    bool hnl = false;
+    if (nhot > 0) {
+      int gi = grab(1);
       hne = s_list[min(gi, nhot - 1)];
       hnl = gi < nhot;
-    }
-  }
-  if (nwarm > 0) {
-    const WarmMeta<WF> wm = warm_meta_setup<WF>(p, lane);
-    WarmTile<D, WF> tw[NBW];
-    int4 ew[NBW];
-    bool lw[NBW];
-    int gi = grab(0);
-    int4 ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
-    bool nl = gi < nwarm;
 #pragma unroll
-    for (int k = 0; k < NBW - 1; ++k) {
-      ew[k] = ne;
-      lw[k] = nl;
-      load_warm<D, WF>(p, kvh, uniform(ne.y), lane, wm, tw[k], nl);
-      __builtin_amdgcn_sched_barrier(0);
-      gi = grab(0);
-      ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
-      nl = gi < nwarm;
+      for (int k = 0; k < NBH - 1; ++k) {
+        eh[k] = hne;
+        lh[k] = hnl;
+        load_hot<D>(p, kvh, uniform(hne.y), lane, th[k], hnl);
+        __builtin_amdgcn_sched_barrier(0);
+        gi = grab(1);
+        hne = s_list[min(gi, nhot - 1)];
+        hnl = gi < nhot;
+      }
     }
-    do {
+    if (nwarm > 0) {
+      const WarmMeta<WF> wm = warm_meta_setup<WF>(p, lane);
+      WarmTile<D, WF> tw[NBW];
+      int4 ew[NBW];
+      bool lw[NBW];
+      int gi = grab(0);
+      int4 ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
+      bool nl = gi < nwarm;
 #pragma unroll
-      for (int k = 0; k < NBW; ++k) {
-        const int kn = (k + NBW - 1) % NBW;
-        ew[kn] = ne;
-        lw[kn] = nl;
-        load_warm<D, WF>(p, kvh, uniform(ne.y), lane, wm, tw[kn], nl);
+      for (int k = 0; k < NBW - 1; ++k) {
+        ew[k] = ne;
+        lw[k] = nl;
+        load_warm<D, WF>(p, kvh, uniform(ne.y), lane, wm, tw[k], nl);
         __builtin_amdgcn_sched_barrier(0);
         gi = grab(0);
         ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
         nl = gi < nwarm;
-        if (lw[k])
-          process_warm<D, WF, SCORES>(p, tw[k], stage_index(ew[k]), uniform(ew[k].z), lane, head_ok, b, qh, qv,
-                                      qsum, s_stage, st);
       }
-    } while (lw[0]);   // buffer 0 holds the next tile; positions are handed out in order
-  }
-  if (nhot > 0) {
-    do {
+      do {
 #pragma unroll
-      for (int k = 0; k < NBH; ++k) {
-        const int kn = (k + NBH - 1) % NBH;
-        eh[kn] = hne;
-        lh[kn] = hnl;
-        load_hot<D>(p, kvh, uniform(hne.y), lane, th[kn], hnl);
-        __builtin_amdgcn_sched_barrier(0);
-        const int gi = grab(1);
-        hne = s_list[min(gi, nhot - 1)];
-        hnl = gi < nhot;
-        if (lh[k])
-          process_hot<D, SCORES>(p, th[k], stage_index(eh[k]), uniform(eh[k].z), lane, head_ok, b, qh, qvh,
-                                 s_stage, st);
-      }
-    } while (lh[0]);
-  }
+        for (int k = 0; k < NBW; ++k) {
+          const int kn = (k + NBW - 1) % NBW;
+          ew[kn] = ne;
+          lw[kn] = nl;
+          load_warm<D, WF>(p, kvh, uniform(ne.y), lane, wm, tw[kn], nl);
+          __builtin_amdgcn_sched_barrier(0);
+          gi = grab(0);
+          ne = s_list[MAX_LIST - 1 - min(gi, nwarm - 1)];
+          nl = gi < nwarm;
+          if (lw[k])
+            process_warm<D, WF, SCORES>(p, tw[k], stage_index(ew[k]), uniform(ew[k].z), lane, head_ok, b, qh, qv,
+                                        qsum, s_stage, st);
+        }
+      } while (lw[0]);   // buffer 0 holds the next tile; positions are handed out in order
+    }
+    if (nhot > 0) {
+      do {
+#pragma unroll
+        for (int k = 0; k < NBH; ++k) {
+          const int kn = (k + NBH - 1) % NBH;
+          eh[kn] = hne;
+          lh[kn] = hnl;
+          load_hot<D>(p, kvh, uniform(hne.y), lane, th[kn], hnl);
+          __builtin_amdgcn_sched_barrier(0);
+          const int gi = grab(1);
+          hne = s_list[min(gi, nhot - 1)];
+          hnl = gi < nhot;
+          if (lh[k])
+            process_hot<D, SCORES>(p, th[k], stage_index(eh[k]), uniform(eh[k].z), lane, head_ok, b, qh, qvh,
+                                   s_stage, st);
+        }
+      } while (lh[0]);
+    }
+  };
+  if (det) tile_loops(std::true_type{});
+  else tile_loops(std::false_type{});
 
   // Error word: bit 1, a resident block with an out-of-range slot (skipped);
   // bit 2, a state that is none of HOT, WARM, COLD.  Reported after the tile
@@ -1714,8 +1744,8 @@ static void launch_nw(const DecodeParams& p, bool long_rows, int grid, hipStream
   if (SC && p.lds_stage == STAGE_LDS_LIST) shmem += size_t(p.groups) * MAX_LIST * 2 * sizeof(float);
   const int32_t stride = int32_t(p.table_stride);
   const bool xcd_seq = p.splits == 1 && p.batch % 8 == 0;   // see tiered_decode_kernel
-  const int32_t kvh_splits =
-      int32_t(uint32_t(p.kv_heads) | (uint32_t(p.splits) << 16) | (xcd_seq ? 0x80000000u : 0u));
+  const int32_t kvh_splits = int32_t(uint32_t(p.kv_heads) | (uint32_t(p.splits) << 16) |
+                                     (p.deterministic ? 0x40000000u : 0u) | (xcd_seq ? 0x80000000u : 0u));
   if (long_rows)
     hipLaunchKernelGGL((tiered_decode_kernel<D, WF, SC, CZ, QT, NW, true>), dim3(grid), dim3(NW * 64), shmem, stream,
                        p.table, p.states, p.lengths, p.q, p.seq_nblocks, stride, p.num_blocks, kvh_splits,
@@ -1778,7 +1808,8 @@ extern "C" int64_t tierkv_decode_workspace_bytes(int32_t batch, int32_t num_head
                                                  int32_t with_scores, int32_t splits_hint) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 || block_size <= 0 || head_dim <= 0)
     return -1;
-  return ws_layout(batch, num_heads, num_kv_heads, num_blocks, block_size, head_dim, with_scores != 0, splits_hint).total;
+  return ws_layout(batch, num_heads, num_kv_heads, num_blocks, block_size, head_dim, with_scores != 0,
+                   hint_splits(splits_hint)).total;
 }
 
 // Every argument check of tierkv_decode_attention, before anything is
@@ -1794,6 +1825,7 @@ int32_t tierkv::decode_check_args(
     int32_t warm_format, int32_t cold_mode,
     int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t block_size, int32_t head_dim,
     int32_t splits_hint, void* workspace, int64_t workspace_bytes) {
+  splits_hint = hint_splits(splits_hint);
   if (!query || !out || !block_table || !block_states || !block_lengths || !workspace)
     return fail(TIERKV_ERR_INVALID, "null tensor pointer");
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -1831,8 +1863,8 @@ int32_t tierkv::decode_check_args(
       if (m & 7u) return fail(TIERKV_ERR_INVALID, "reference-format scale/zero pools must be 8-byte aligned");
     }
     const Plan pl = plan_launch(batch, num_kv_heads, num_blocks, groups, splits_hint);
-    if (pl.splits > 0x7fff || num_kv_heads > 0xffff)
-      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or 32767 splits");
+    if (pl.splits > 0x3fff || num_kv_heads > 0xffff)
+      return fail(TIERKV_ERR_UNSUPPORTED, "more than 65535 kv heads or 16383 splits");
     int64_t seqs_per_chunk = batch;
     if (pl.splits > 1) {
       seqs_per_chunk = MAX_SPLIT_UNITS / num_kv_heads;
@@ -1858,6 +1890,8 @@ extern "C" int32_t tierkv_decode_attention(
     void* workspace, int64_t workspace_bytes, void* stream_) {
   clear_error();
   hipStream_t stream = reinterpret_cast<hipStream_t>(stream_);
+  const bool det = hint_deterministic(splits_hint);
+  splits_hint = hint_splits(splits_hint);
   const int32_t rc0 = decode_check_args(query, query_dtype, out, score_sums, block_table, block_states, block_lengths,
                                         table_stride, num_blocks, hot_k, hot_v, hot_slots, warm_k, warm_v, warm_slots,
                                         k_scale, k_zero, v_scale, v_zero, warm_format, cold_mode, batch, num_heads,
@@ -1900,6 +1934,7 @@ extern "C" int32_t tierkv_decode_attention(
   p.ws_ml = reinterpret_cast<float*>(ws + wl.ml);
   p.ws_stage = reinterpret_cast<float*>(ws + wl.stage);
   p.score_sums = score_sums;
+  p.deterministic = det ? 1 : 0;
   const bool cz = cold_mode == TIERKV_COLD_ZERO_LOGIT;
   const bool bf16 = query_dtype == TIERKV_DTYPE_BF16;
 

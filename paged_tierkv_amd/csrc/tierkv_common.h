@@ -34,6 +34,10 @@ inline int32_t check_launch(const char* what) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A decode call's splits_hint: the split factor, and the deterministic flag.
+inline bool hint_deterministic(int32_t hint) { return hint > 0 && (hint & TIERKV_DECODE_DETERMINISTIC) != 0; }
+inline int32_t hint_splits(int32_t hint) { return hint > 0 ? (hint & ~TIERKV_DECODE_DETERMINISTIC) : hint; }
+
 // Every argument check of tierkv_decode_attention (decode_attention.hip),
 // without a launch: TIERKV_OK or the status that call would return.
 int32_t decode_check_args(

@@ -128,7 +128,7 @@ class BatchedTieredKVRuntime:
                  block_size: int = 16, hot_fraction: float = 0.15, warm_fraction: float = 0.55,
                  policy_mode: str = "hot_warm_cold", policy_interval: int = 64,
                  warm_format: str = "absmax_i8", cold_mode: str = "masked", device=None,
-                 prefill_scoring: str = "proxy"):
+                 prefill_scoring: str = "proxy", deterministic: bool = True):
         if policy_mode not in _MODES:
             raise ValueError('policy_mode must be "hot_warm" or "hot_warm_cold".')
         if warm_format not in kernels.WARM_FORMATS:
@@ -160,6 +160,10 @@ class BatchedTieredKVRuntime:
         # probabilities: "proxy" = sink + recency (the reference under SDPA),
         # "attention" = the prefill block-score kernel.
         self.prefill_scoring = prefill_scoring
+        # Decode launches with a fixed tile share per wave: every step's
+        # attention output is the same bits on every run (about 1-2 % of the
+        # decode kernel's time, a few microseconds of a model step).
+        self.deterministic = bool(deterministic)
         n = self.max_blocks
         # Capacities per sequence, from the budgets: a tick reuses the slots it
         # frees (demotions take evicted WARM slots, promotions the HOT slots
@@ -430,7 +434,7 @@ class BatchedTieredKVRuntime:
             query_states, st.table, st.states, st.lengths, st.hot_k, st.hot_v, st.warm_k, st.warm_v,
             st.k_scale, st.k_zero, st.v_scale, st.v_zero, bound, num_key_value_groups, scaling,
             return_scores=policy_step, cold_mode=self.cold_mode, seq_num_blocks=st.nblocks,
-            workspace=self.reserve_decode_workspace(query_states.shape[1]))
+            workspace=self.reserve_decode_workspace(query_states.shape[1]), deterministic=self.deterministic)
         if policy_step:
             self.last_score_sums = sums   # the probability sums the tick ranked (kept for inspection)
             self.tick_layer(layer, sums, num_blocks)

@@ -26,6 +26,11 @@ Additive, keyword-only extensions:
   reference's ``TIERKV_SPLIT_DECODE`` switch is not needed: the kernel always
   splits when it pays, and the result equals the single pass up to fp32
   re-association;
+* ``deterministic``: every wave takes a fixed share of its workgroup's tiles
+  instead of taking tiles from a shared counter as it frees up, so the
+  output is the same bits on every call over the same inputs (as the
+  reference's Triton kernel is), for about 1-2 % of the launch time.  The
+  default comes from ``TIERKV_DETERMINISTIC`` (off when unset);
 * ``workspace``: a ``DecodeWorkspace`` the caller owns (a fixed one is
   required under HIP graph capture); by default each (device, stream) pair
   has its own implicit workspace, so launches on different streams never
@@ -44,6 +49,7 @@ the kernel skipped a block whose slot or state was out of range.
 from __future__ import annotations
 
 import ctypes
+import os
 import weakref
 
 import torch
@@ -233,14 +239,17 @@ def tierkv_decode_attention(
     seq_num_blocks=None,
     splits: int | None = None,
     workspace: DecodeWorkspace | None = None,
+    deterministic: bool | None = None,
 ):
     """Decode attention over a tiered paged KV cache (see module docstring)."""
     lib = _lib.lib()  # RuntimeError if the HIP library is not built
     statics = (block_table, block_states, block_lengths, hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool,
                k_scale, k_zero, v_scale, v_zero)
+    det = default_deterministic() if deterministic is None else bool(deterministic)
     simple = workspace is None and seq_num_blocks is None and splits is None
     if simple:
-        hit = _rebind(lib, query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode)
+        hit = _rebind(lib, query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode,
+                      det)
         if hit is not None:
             args, out, score_sums, ws, batched = hit
             _launch(lib, args, query_states.device, ws)
@@ -250,9 +259,9 @@ def tierkv_decode_attention(
     args, out, score_sums, ws, batched, _ = _bind(
         query_states, block_table, block_states, block_lengths, hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool,
         k_scale, k_zero, v_scale, v_zero, num_blocks, num_key_value_groups, scaling, return_scores,
-        cold_mode=cold_mode, seq_num_blocks=seq_num_blocks, splits=splits, workspace=workspace)
+        cold_mode=cold_mode, seq_num_blocks=seq_num_blocks, splits=splits, workspace=workspace, deterministic=det)
     if simple:
-        _remember(query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode,
+        _remember(query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode, det,
                   args, batched)
     _launch(lib, args, query_states.device, ws)
     if score_sums is not None and not batched:
@@ -270,27 +279,34 @@ _REBIND: dict = {}
 _REBIND_MAX = 64
 
 
-def _rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode):
+def default_deterministic() -> bool:
+    """The ``deterministic`` default: ``TIERKV_DETERMINISTIC`` set to a
+    non-zero value."""
+    return os.environ.get("TIERKV_DETERMINISTIC", "0") not in ("", "0")
+
+
+def _rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode, det):
     return (tuple(id(t) for t in statics), query_states.dtype, tuple(query_states.shape), query_states.device,
-            int(num_key_value_groups), float(scaling), bool(return_scores), cold_mode)
+            int(num_key_value_groups), float(scaling), bool(return_scores), cold_mode, det)
 
 
-def _remember(query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode, args,
+def _remember(query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode, det, args,
               batched):
     if len(_REBIND) >= _REBIND_MAX:
         _REBIND.pop(next(iter(_REBIND)))
-    key = _rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode)
+    key = _rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode, det)
     refs = tuple(None if t is None else weakref.ref(t) for t in statics)
     ptrs = tuple(None if t is None else t.data_ptr() for t in statics)
     # args: query, dtype, out, scores | table, states, lengths, stride, None | num_blocks | pools ... splits hint
     _REBIND[key] = (refs, ptrs, args[1], args[4:9], args[10:29], batched, {int(num_blocks): None})
 
 
-def _rebind(lib, query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode):
+def _rebind(lib, query_states, statics, num_blocks, num_key_value_groups, scaling, return_scores, cold_mode, det):
     """The bound arguments of a repeated call, or None (bind in full)."""
     if not _REBIND or not query_states.is_cuda:
         return None
-    e = _REBIND.get(_rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode))
+    e = _REBIND.get(_rebind_key(query_states, statics, num_key_value_groups, scaling, return_scores, cold_mode,
+                                det))
     if e is None:
         return None
     refs, ptrs, dtype_code, mid, tail, batched, needs = e
@@ -368,6 +384,7 @@ def _bind(
     splits: int | None = None,
     workspace: DecodeWorkspace | None = None,
     prepared: bool = False,
+    deterministic: bool | None = None,
 ):
     """Validate one decode launch and bind its C-ABI arguments (all but the
     stream).  ``prepared`` binds a fixed workspace the launch owns unless one
@@ -441,6 +458,10 @@ def _bind(
             raise ValueError("seq_num_blocks needs one entry per sequence.")
 
     splits_hint = int(splits) if splits else 0
+    if not 0 <= splits_hint < _lib.DECODE_DETERMINISTIC:
+        raise ValueError("splits must be a non-negative split factor.")
+    if default_deterministic() if deterministic is None else deterministic:
+        splits_hint |= _lib.DECODE_DETERMINISTIC
     need = lib.tierkv_decode_workspace_bytes(batch, num_heads, kv_heads, int(num_blocks), block_size,
                                              head_dim, int(return_scores), splits_hint)
     if need < 0:

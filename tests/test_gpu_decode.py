@@ -125,6 +125,64 @@ def test_scores_reproducible(device, which, fmt, cold, splits_seq, budgets):
         assert torch.equal(lab, runs[0][1]), f"labels differ at splits={splits}"
 
 
+@pytest.mark.parametrize("which,fmt,cold,scores,splits", [
+    ("c3", "absmax_i8", "masked", False, None),
+    ("c3", "ref_u8", "zero_logit", True, None),
+    ("c4", "absmax_i8", "masked", True, None),       # eight splits per unit: list stage, split merge
+    ("gqa16", "ref_u8", "zero_logit", True, 3),      # four-wave workgroups, workspace stage
+    ("c1", "absmax_i8", "masked", False, None),      # D = 64, many splits of a short row
+])
+def test_deterministic_launches_are_bit_identical(device, which, fmt, cold, scores, splits):
+    """deterministic=True (TIERKV_DECODE_DETERMINISTIC) fixes each wave's share
+    of the tiles, so the attention output is the same bits on every launch,
+    as the reference's Triton kernel's is (tierkv_triton.py:45-145); the
+    output stays within tolerance of the oracle, and the score sums equal the
+    default launch's bit for bit."""
+    case = {"c1": W.config1, "c3": W.config3, "c4": W.config4, "gqa16": _gqa16_long_case}[which]()
+    print(f"[deterministic] case={case.name} fmt={fmt} cold={cold} scores={scores} splits={splits}", flush=True)
+    warm = oracle_warm(case, fmt)
+    args = to_gpu_inputs(case, warm, device)
+    runs = []
+    for _ in range(4):
+        out, sc = tierkv_decode_attention(**args, return_scores=scores, cold_mode=cold, splits=splits,
+                                          deterministic=True)
+        torch.cuda.synchronize()
+        runs.append((out.clone(), None if sc is None else sc.clone()))
+    _, sc_default = tierkv_decode_attention(**args, return_scores=scores, cold_mode=cold, splits=splits)
+    torch.cuda.synchronize()
+    assert workspace_error_word(device) == 0
+    for out, sc in runs[1:]:
+        assert torch.equal(out.view(torch.int16), runs[0][0].view(torch.int16)), "output bits differ between launches"
+        if scores:
+            assert torch.equal(sc.view(torch.int32), runs[0][1].view(torch.int32))
+    if scores:
+        assert torch.equal(runs[0][1].view(torch.int32), sc_default.view(torch.int32)), \
+            "score sums differ from the default launch's"
+    seqs = list(range(min(case.batch, 8)))
+    res = oracle_decode(case, warm, fmt, cold, scores, seqs=seqs)
+    exp_out = res[0] if scores else res
+    got = runs[0][0][seqs, 0].float().cpu().numpy()
+    report(f"{case.name} {fmt} deterministic output", assert_close(got, exp_out, what=f"{case.name} output"))
+
+
+def test_deterministic_flag_from_environment(device, monkeypatch):
+    """TIERKV_DETERMINISTIC=1 makes deterministic launches the default, also
+    for repeated calls that reuse their bound arguments."""
+    case = W.config3(batch=8)
+    warm = oracle_warm(case, "absmax_i8")
+    args = to_gpu_inputs(case, warm, device)
+    monkeypatch.setenv("TIERKV_DETERMINISTIC", "1")
+    outs = []
+    for _ in range(3):
+        out, _ = tierkv_decode_attention(**args, cold_mode="masked")
+        torch.cuda.synchronize()
+        outs.append(out.clone())
+    ref, _ = tierkv_decode_attention(**args, cold_mode="masked", deterministic=True, splits=None)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.equal(o.view(torch.int16), ref.view(torch.int16))
+
+
 def test_two_streams_concurrent(device):
     """Decodes of different shapes in flight on two streams at once: each
     stream has its own implicit workspace (split partials, arrival counters,
