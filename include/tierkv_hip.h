@@ -58,7 +58,8 @@ extern "C" {
  * factor, 0 = automatic): each wave takes a fixed share of the workgroup's
  * tiles instead of taking them from a shared counter, so the attention output
  * is the same bits on every call over the same inputs, as the reference's
- * Triton kernel is.  Costs about 1-2 % of the launch time. */
+ * Triton kernel is.  Costs about 1 % of the launch time (2-3 % with score
+ * sums). */
 #define TIERKV_DECODE_DETERMINISTIC 0x40000000
 
 /* Message of the last failing call on this thread ("" if none). */

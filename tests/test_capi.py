@@ -36,6 +36,28 @@ def test_library_exports_every_declared_symbol():
     assert exported == set(names), exported ^ set(names)
 
 
+def test_python_constants_match_the_header():
+    defines = {m.group(1): int(m.group(2), 0)
+               for m in re.finditer(r"#define\s+(TIERKV_\w+)\s+(0x[0-9a-fA-F]+|\d+)", open(HEADER).read())}
+    pairs = {"TIERKV_OK": _lib.TIERKV_OK, "TIERKV_ERR_INVALID": _lib.TIERKV_ERR_INVALID,
+             "TIERKV_ERR_UNSUPPORTED": _lib.TIERKV_ERR_UNSUPPORTED, "TIERKV_ERR_HIP": _lib.TIERKV_ERR_HIP,
+             "TIERKV_ERR_WORKSPACE": _lib.TIERKV_ERR_WORKSPACE, "TIERKV_ERR_STATE": _lib.TIERKV_ERR_STATE,
+             "TIERKV_DTYPE_F16": _lib.DTYPE_F16, "TIERKV_DTYPE_BF16": _lib.DTYPE_BF16,
+             "TIERKV_WARM_REF_U8": _lib.WARM_REF_U8, "TIERKV_WARM_ABSMAX_I8": _lib.WARM_ABSMAX_I8,
+             "TIERKV_COLD_ZERO_LOGIT": _lib.COLD_ZERO_LOGIT, "TIERKV_COLD_MASKED": _lib.COLD_MASKED,
+             "TIERKV_DECODE_DETERMINISTIC": _lib.DECODE_DETERMINISTIC}
+    for name, value in pairs.items():
+        assert defines[name] == value, name
+
+
+def test_decode_workspace_bytes_ignore_the_deterministic_flag():
+    lib = _lib.lib()
+    for splits in (0, 1, 3, 8):
+        a = lib.tierkv_decode_workspace_bytes(4, 32, 8, 2048, 16, 128, 1, splits)
+        b = lib.tierkv_decode_workspace_bytes(4, 32, 8, 2048, 16, 128, 1, splits | _lib.DECODE_DETERMINISTIC)
+        assert a == b > 0
+
+
 def test_abi_version_and_errors_without_gpu():
     lib = _lib.lib()
     assert lib.tierkv_abi_version() == _lib.ABI_VERSION
