@@ -43,7 +43,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--layers", type=int, default=4)
     p.add_argument("--splits", type=int, default=0)
-    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "promote", "c2b", "c5", "prefill", "ref"],
+    p.add_argument("--workload", choices=["c3", "c1", "c4", "c2a", "promote", "c2b", "c5", "prefill", "ref",
+                                          "microbench"],
                    default="c3",
                    help="c2a / promote / c2b: demotion / promotion / scoring microbenchmarks, c5: end-to-end random-init "
                         "Llama-3-8B decode through the HF hooks (each its own JSON line)")
@@ -785,6 +786,84 @@ REF_METRIC = ("reference-API drop-in end-to-end decode tokens/s, TinyLlama-1.1B 
 REF_PUBLISHED_A10G = {512: 50.15, 1024: 49.22, 1536: 49.63, 1900: 46.51}
 
 
+MICRO_METRIC = ("decode no-score / score latency ratio, the reference's kernel microbenchmark (kv 4, q 8, D 64, "
+                "all-HOT dense pool, 4 / 16 / 64 blocks)")
+
+
+def run_microbench(args, device):
+    """benchmark_no_score_anomaly (tierkv_triton.py:504-673) through the
+    drop-in: a dense ``TieredKVTensorPool`` whose HOT blocks are written with
+    ``write_hot_tokens``, an identity block table, the reference's call, and
+    its timing protocol -- 5 warm-up calls per path, then 50 calls each
+    followed by a host synchronisation, wall clock -- for 4, 16 and 64
+    blocks.  The no-score / score ratio is the reference's only kernel-level
+    figure (0.73-0.86 on an A10G, main.py:3410-3412); its anomaly test is a
+    ratio above 1.05.  Kernel-only times (one prepared launch per step,
+    replayed from a HIP graph, HIP events) are reported beside it.  ``value`` is the ratio at
+    64 blocks; a ratio near 1 means the score pass costs little."""
+    import torch
+
+    from paged_tierkv_amd import tierkv_policy as tp
+    from paged_tierkv_amd.tierkv_hip import PreparedDecode, tierkv_decode_attention
+
+    bs, kvh, qh, D = 16, 4, 8, 64
+    gen = torch.Generator(device=device).manual_seed(5000)
+    rows = []
+    for nb in (4, 16, 64):
+        mb = nb + 4
+        pool = tp.TieredKVTensorPool(num_layers=1, block_size=bs, max_seq_len=mb * bs, max_blocks_per_layer=mb,
+                                     pool_blocks=mb, pool_chunk_blocks=max(nb, 4))
+        for phys in range(nb):
+            k = torch.randn((1, kvh, bs, D), generator=gen, device=device, dtype=torch.float16)
+            v = torch.randn((1, kvh, bs, D), generator=gen, device=device, dtype=torch.float16)
+            pool.write_hot_tokens(phys, 0, k, v)
+        table = torch.full((mb,), -1, device=device, dtype=torch.int32)
+        table[:nb] = torch.arange(nb, device=device, dtype=torch.int32)
+        states = torch.full((mb,), tp.HOT_STATE, device=device, dtype=torch.int32)
+        kw = dict(query_states=torch.randn((1, qh, 1, D), generator=gen, device=device, dtype=torch.float16),
+                  block_table=table, block_states=states, block_lengths=pool.block_lengths,
+                  hot_k_pool=pool.hot_k_pool, hot_v_pool=pool.hot_v_pool, warm_k_pool=pool.warm_k_pool,
+                  warm_v_pool=pool.warm_v_pool, k_scale=pool.k_scale, k_zero=pool.k_zero, v_scale=pool.v_scale,
+                  v_zero=pool.v_zero, num_blocks=nb, num_key_value_groups=qh // kvh, scaling=D ** -0.5)
+        for scores in (True, False):
+            for _ in range(5):
+                tierkv_decode_attention(**kw, return_scores=scores)
+                torch.cuda.synchronize()
+        _, with_sums = tierkv_decode_attention(**kw, return_scores=True)
+        _, without = tierkv_decode_attention(**kw, return_scores=False)
+        torch.cuda.synchronize()
+        row = {"num_blocks": nb, "api_score_returns_tensor": with_sums is not None,
+               "api_no_score_returns_none": without is None}
+        for scores, key in ((True, "score"), (False, "no_score")):
+            t0 = time.perf_counter()
+            for _ in range(50):
+                tierkv_decode_attention(**kw, return_scores=scores)
+                torch.cuda.synchronize()
+            row[f"t_{key}_ms"] = round((time.perf_counter() - t0) / 50 * 1e3, 4)
+        for scores, key in ((True, "score"), (False, "no_score")):
+            # kernel time: one prepared launch replayed from a HIP graph
+            plan = PreparedDecode(**kw, return_scores=scores)
+            sec, _ = graph_timed(lambda i: plan.launch(), 20, 400, 20)
+            row[f"kernel_{key}_us"] = round(sec * 1e6, 3)
+            del plan
+        row["ratio_no_score_over_score"] = round(row["t_no_score_ms"] / row["t_score_ms"], 4)
+        row["kernel_ratio_no_score_over_score"] = round(row["kernel_no_score_us"] / row["kernel_score_us"], 4)
+        row["anomaly_present"] = row["ratio_no_score_over_score"] > 1.05
+        log(f"[microbench] {nb:3d} blocks: no-score {row['t_no_score_ms']:.4f} ms, score {row['t_score_ms']:.4f} ms "
+            f"(ratio {row['ratio_no_score_over_score']:.3f}); kernels {row['kernel_no_score_us']:.2f} / "
+            f"{row['kernel_score_us']:.2f} us")
+        rows.append(row)
+        del pool, kw
+    last = rows[-1]
+    cfg = {"workload": "reference_microbench_no_score_anomaly", "kv_heads": kvh, "num_heads": qh, "head_dim": D,
+           "block_size": bs, "block_counts": [4, 16, 64], "pool": "dense TieredKVTensorPool, all HOT",
+           "timing": "per call: launch + host synchronise, wall clock, 50 calls (the reference's protocol)"}
+    line = _line(MICRO_METRIC, last["ratio_no_score_over_score"], "ratio", 50, 5,
+                 last["t_no_score_ms"] / 1e3, "f16", cfg, per_block_count=rows,
+                 reference_ratio_a10g="0.73-0.86 (main.py:3410-3412)", roofline=None, cpu_baseline=None)
+    print(json.dumps(line), flush=True)
+
+
 def run_ref(args, device):
     """The reference's end-to-end setting through this build's drop-in for
     its Python API: a random-init TinyLlama-1.1B-shaped model (22 layers,
@@ -1024,6 +1103,9 @@ def main():
         return
     if args.workload == "ref":
         run_ref(args, device)
+        return
+    if args.workload == "microbench":
+        run_microbench(args, device)
         return
     if args.workload in ("c2a", "promote"):
         run_c2a(args, device)

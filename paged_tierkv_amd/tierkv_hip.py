@@ -416,8 +416,15 @@ def _bind(
         _lib.require_gpu_tensor(t, name)
         if t.dtype != torch.int32:
             raise ValueError(f"{name} must be int32.")
-        if t.shape != block_table.shape:
-            raise ValueError(f"{name} must have the block table's shape.")
+        # Batched tables share one row stride.  A 1-D table's states and
+        # lengths are read at logical blocks [0, num_blocks) only, as the
+        # reference kernel reads them (tierkv_triton.py:81-83): any length
+        # covering them is accepted, e.g. a dense pool's per-block lengths.
+        if batched or t.ndim != 1:
+            if t.shape != block_table.shape:
+                raise ValueError(f"{name} must have the block table's shape.")
+        elif t.shape[0] < int(num_blocks):
+            raise ValueError(f"{name} must have at least num_blocks entries.")
         if not t.is_contiguous():
             raise ValueError(f"{name} must be contiguous.")
     pools = (hot_k_pool, hot_v_pool, warm_k_pool, warm_v_pool)

@@ -206,3 +206,49 @@ def test_pool_errors_match_reference(device):
     pool.write_hot_tokens(2, 0, k, k)
     with pytest.raises(RuntimeError, match="No HOT slots available"):
         pool.write_hot_tokens(3, 0, k, k)
+
+
+@pytest.mark.parametrize("num_blocks", [4, 16, 64])
+def test_reference_microbenchmark_call(device, num_blocks):
+    """The call of the reference's own kernel microbenchmark
+    (benchmark_no_score_anomaly, tierkv_triton.py:504-673): a dense
+    TieredKVTensorPool with HOT blocks written by write_hot_tokens, a padded
+    identity table, and the pool's per-block lengths (indexed by physical id,
+    not of the table's length) passed as block_lengths.  Both return forms
+    (tensor / None) and the output against fp32 attention over the written
+    K/V."""
+    bs, kvh, qh, d = 16, 4, 8, 64
+    mb = num_blocks + 4
+    gen = torch.Generator(device=device).manual_seed(num_blocks)
+    pool = tp.TieredKVTensorPool(num_layers=1, block_size=bs, max_seq_len=mb * bs, max_blocks_per_layer=mb,
+                                 pool_blocks=mb, pool_chunk_blocks=max(num_blocks, 4))
+    ks, vs = [], []
+    for phys in range(num_blocks):
+        k = torch.randn((1, kvh, bs, d), generator=gen, device=device, dtype=torch.float16)
+        v = torch.randn((1, kvh, bs, d), generator=gen, device=device, dtype=torch.float16)
+        pool.write_hot_tokens(phys, 0, k, v)
+        ks.append(k)
+        vs.append(v)
+    table = torch.full((mb,), -1, device=device, dtype=torch.int32)
+    table[:num_blocks] = torch.arange(num_blocks, device=device, dtype=torch.int32)
+    states = torch.full((mb,), tp.HOT_STATE, device=device, dtype=torch.int32)
+    q = torch.randn((1, qh, 1, d), generator=gen, device=device, dtype=torch.float16)
+    kw = dict(query_states=q, block_table=table, block_states=states, block_lengths=pool.block_lengths,
+              hot_k_pool=pool.hot_k_pool, hot_v_pool=pool.hot_v_pool, warm_k_pool=pool.warm_k_pool,
+              warm_v_pool=pool.warm_v_pool, k_scale=pool.k_scale, k_zero=pool.k_zero, v_scale=pool.v_scale,
+              v_zero=pool.v_zero, num_blocks=num_blocks, num_key_value_groups=qh // kvh, scaling=d ** -0.5)
+    print(f"[dropin] reference microbenchmark call, {num_blocks} blocks, lengths {tuple(pool.block_lengths.shape)}",
+          flush=True)
+    out_s, sums = tierkv_decode_attention(**kw, return_scores=True)
+    out_n, none = tierkv_decode_attention(**kw, return_scores=False)
+    torch.cuda.synchronize()
+    assert none is None and sums is not None and sums.shape == (qh, mb)
+    key = torch.cat(ks, dim=2)[0].float().repeat_interleave(qh // kvh, dim=0)      # [H, T, D]
+    val = torch.cat(vs, dim=2)[0].float().repeat_interleave(qh // kvh, dim=0)
+    p = torch.softmax((q[0].float() @ key.transpose(1, 2)) * d ** -0.5, dim=-1)   # [H, 1, T]
+    ref = (p @ val)[:, 0]
+    for out in (out_s, out_n):
+        torch.testing.assert_close(out[0, 0].float(), ref, atol=ATOL, rtol=RTOL)
+    blocks = p[:, 0].view(qh, num_blocks, bs).sum(-1)
+    torch.testing.assert_close(sums[:, :num_blocks], blocks, atol=ATOL, rtol=RTOL)
+    assert torch.count_nonzero(sums[:, num_blocks:]) == 0
