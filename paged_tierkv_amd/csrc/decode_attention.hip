@@ -4,29 +4,39 @@
 // split/reduce pair (147-264) behind tierkv_decode_attention
 // (tierkv_triton.py:272-465).
 //
-// Fast path (block_size 16, head_dim 64 or 128, GQA group <= 16), one kernel:
+// Fast path (block_size 16, head_dim 64 or 128, GQA group <= 16), one kernel
+// (a second one finalises the score sums of split launches):
 //   * workgroup = (sequence, kv head, split), 8 waves (4 when the GQA group
 //     exceeds 8); the whole GQA group is served by one pass over each K/V
-//     byte;
-//   * every workgroup scans its sequence's table row and keeps the resident
-//     (HOT first, then WARM) blocks whose rank is congruent to its split, so
-//     splits and waves get the same number of tiles and a similar HOT/WARM
-//     mix; COLD blocks cost no bytes;
+//     byte; unsplit launches of a batch that is a multiple of 8 place each
+//     sequence's kv heads on one XCD;
+//   * every workgroup scans its sequence's table row and keeps its share of
+//     the resident blocks, HOT and WARM ranked separately: a contiguous range
+//     of each tier's ranks when the row fits one pass of the build, the ranks
+//     congruent to its split otherwise; COLD blocks cost no bytes;
 //   * one wave handles one 16-token block (tile) at a time with MFMA
 //     16x16x16 f16:  S^T = K Q^T  (A = K rows as loaded, B = Q^T), then
-//     O^T += V^T P^T  (B = P^T is exactly S^T's accumulator layout);
-//   * WARM int8 codes become fp16 by a byte permute under the exponent of
-//     1024 (codes + 1152 exactly); the constant offset is removed once per
-//     head (q . 1152 from the logits, 1152 * sum(P) from the output), and the
-//     absmax scales are folded into the logits (s_k) and into P (s_v);
+//     O^T += V^T P^T  (B = P^T is exactly S^T's accumulator layout); tiles
+//     are handed to waves from LDS counters as they free up, or in fixed
+//     interleaved shares (TIERKV_DECODE_DETERMINISTIC);
+//   * WARM codes become fp16 by a byte permute under the exponent of 1024
+//     (int8 absmax codes + 1152, uint8 reference codes + 1024, exactly); the
+//     constant offset (and the reference format's zero points) is removed
+//     once per head from the logits and by one more MFMA from the output,
+//     and the scales are folded into the logits and into P;
 //   * the next tile is prefetched into a second register buffer (ping-pong),
 //     the tier branch is wave-uniform;
 //   * online softmax in base 2 whose running maximum is re-based only when a
 //     logit exceeds it by more than LAZY_T (P stays <= 2^LAZY_T);
 //   * waves merge in LDS; when a sequence is split over several workgroups
 //     the last one to finish (an atomic counter per (sequence, kv head))
-//     merges the partials (log-sum-exp combine, tierkv_triton.py:231-264)
-//     and finalises the per-block probability sums.
+//     merges the partials (log-sum-exp combine, tierkv_triton.py:231-264);
+//   * score launches stage each visited block's (max, sum) per head and
+//     reduce every head's row along a fixed tree, so the per-block
+//     probability sums (tierkv_triton.py:121-145) are the same bits whatever
+//     the tile order and split count: unsplit launches whose statistics fit
+//     the workgroup's LDS finalise in the workgroup, the others (split
+//     launches, longer rows) in finalize_scores_kernel.
 // Generic path (any block_size <= 64, head_dim <= 256, any group): one wave
 // per (sequence, q head), the reference kernel's structure.
 
