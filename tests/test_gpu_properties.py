@@ -2,7 +2,8 @@
 random tier mixes (hypothesis, derandomized so every run draws the same
 cases): batch, kv heads, GQA group, head_dim, row length, HOT/WARM/COLD
 fractions, ragged block lengths, dense or compact pools, both WARM formats,
-both COLD modes, score sums on or off, and automatic or forced splits; and
+both COLD modes, score sums on or off, automatic or forced splits, and the
+default or the deterministic tile hand-out (two launches, the same bits); and
 rows of the long-row list build (513 to 2600 blocks) at many split counts.
 
 Tolerance: BASELINE's 2e-3 absolute / 1e-2 relative vs the fp32 oracle for
@@ -24,11 +25,26 @@ from helpers import assert_close, oracle_decode, oracle_warm, to_gpu_inputs  # n
 pytestmark = pytest.mark.gpu
 
 
+def _launch(case, warm, device, c):
+    """One launch as the case asks; a deterministic case is launched twice
+    and must give the same output bits."""
+    args = to_gpu_inputs(case, warm, device)
+    kw = dict(return_scores=c["scores"], cold_mode=c["cold"], splits=c["splits"], deterministic=c["det"])
+    out, sums = tierkv_decode_attention(**args, **kw)
+    if c["det"]:
+        again, _ = tierkv_decode_attention(**args, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), again.view(torch.int16)), "deterministic launches differ"
+    torch.cuda.synchronize()
+    assert workspace_error_word(device) == 0
+    return out, sums
+
+
 @st.composite
 def tier_cases(draw):
     batch = draw(st.integers(1, 3))
     kv = draw(st.sampled_from([1, 2, 4]))
-    groups = draw(st.sampled_from([1, 2, 4, 8]))
+    groups = draw(st.sampled_from([1, 2, 4, 8, 16]))
     head_dim = draw(st.sampled_from([64, 128]))
     nb = draw(st.integers(1, 80))
     hot_frac = draw(st.floats(0.0, 1.0))
@@ -47,7 +63,7 @@ def tier_cases(draw):
                               recent_hot=draw(st.integers(0, 2)))
     return dict(case=case, fmt=draw(st.sampled_from(["absmax_i8", "ref_u8"])),
                 cold=draw(st.sampled_from(["masked", "zero_logit"])), scores=draw(st.booleans()),
-                splits=draw(st.sampled_from([None, 1, 2, 3])))
+                splits=draw(st.sampled_from([None, 1, 2, 3])), det=draw(st.booleans()))
 
 
 @settings(max_examples=40, deadline=None, derandomize=True, database=None,
@@ -56,13 +72,10 @@ def tier_cases(draw):
 def test_decode_matches_oracle_on_random_tier_mixes(device, c):
     case = c["case"]
     print(f"[prop] B={case.batch} H={case.num_heads} Hkv={case.kv_heads} D={case.head_dim} nb={case.num_blocks} "
-          f"tiers={case.tier_counts()} fmt={c['fmt']} cold={c['cold']} scores={c['scores']} splits={c['splits']}",
-          flush=True)
+          f"tiers={case.tier_counts()} fmt={c['fmt']} cold={c['cold']} scores={c['scores']} splits={c['splits']} "
+          f"det={c['det']}", flush=True)
     warm = oracle_warm(case, c["fmt"])
-    out, sums = tierkv_decode_attention(**to_gpu_inputs(case, warm, device), return_scores=c["scores"],
-                                        cold_mode=c["cold"], splits=c["splits"])
-    torch.cuda.synchronize()
-    assert workspace_error_word(device) == 0
+    out, sums = _launch(case, warm, device, c)
     res = oracle_decode(case, warm, c["fmt"], c["cold"], c["scores"])
     exp_out, exp_sc = res if c["scores"] else (res, None)
     assert_close(out[:, 0].float().cpu().numpy(), exp_out, what="output")
@@ -90,7 +103,7 @@ def long_row_cases(draw):
                               recent_hot=draw(st.integers(0, 2)))
     return dict(case=case, fmt=draw(st.sampled_from(["absmax_i8", "ref_u8"])),
                 cold=draw(st.sampled_from(["masked", "zero_logit"])), scores=draw(st.booleans()),
-                splits=draw(st.sampled_from([None, 1, 2, 3, 5, 8, 13])))
+                splits=draw(st.sampled_from([None, 1, 2, 3, 5, 8, 13])), det=draw(st.booleans()))
 
 
 @settings(max_examples=16, deadline=None, derandomize=True, database=None,
@@ -99,12 +112,9 @@ def long_row_cases(draw):
 def test_long_rows_match_oracle(device, c):
     case = c["case"]
     print(f"[prop-long] nb={case.num_blocks} tiers={case.tier_counts()} fmt={c['fmt']} cold={c['cold']} "
-          f"scores={c['scores']} splits={c['splits']}", flush=True)
+          f"scores={c['scores']} splits={c['splits']} det={c['det']}", flush=True)
     warm = oracle_warm(case, c["fmt"])
-    out, sums = tierkv_decode_attention(**to_gpu_inputs(case, warm, device), return_scores=c["scores"],
-                                        cold_mode=c["cold"], splits=c["splits"])
-    torch.cuda.synchronize()
-    assert workspace_error_word(device) == 0
+    out, sums = _launch(case, warm, device, c)
     res = oracle_decode(case, warm, c["fmt"], c["cold"], c["scores"])
     exp_out, exp_sc = res if c["scores"] else (res, None)
     assert_close(out[:, 0].float().cpu().numpy(), exp_out, what="output")
