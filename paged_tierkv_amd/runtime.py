@@ -26,6 +26,8 @@ lockstep block count.
 
 from __future__ import annotations
 
+import os
+
 from dataclasses import dataclass
 
 import torch
@@ -128,7 +130,7 @@ class BatchedTieredKVRuntime:
                  block_size: int = 16, hot_fraction: float = 0.15, warm_fraction: float = 0.55,
                  policy_mode: str = "hot_warm_cold", policy_interval: int = 64,
                  warm_format: str = "absmax_i8", cold_mode: str = "masked", device=None,
-                 prefill_scoring: str = "proxy", deterministic: bool = True):
+                 prefill_scoring: str = "proxy", deterministic: bool | None = None):
         if policy_mode not in _MODES:
             raise ValueError('policy_mode must be "hot_warm" or "hot_warm_cold".')
         if warm_format not in kernels.WARM_FORMATS:
@@ -161,8 +163,12 @@ class BatchedTieredKVRuntime:
         # "attention" = the prefill block-score kernel.
         self.prefill_scoring = prefill_scoring
         # Decode launches with a fixed tile share per wave: every step's
-        # attention output is the same bits on every run (about 1-2 % of the
-        # decode kernel's time, a few microseconds of a model step).
+        # attention output is the same bits on every run (about 1-3 % of the
+        # decode kernel's time, a few microseconds of a model step).  On by
+        # default; TIERKV_DETERMINISTIC, when set, decides instead.
+        if deterministic is None:
+            env = os.environ.get("TIERKV_DETERMINISTIC")
+            deterministic = True if env is None else env not in ("", "0")
         self.deterministic = bool(deterministic)
         n = self.max_blocks
         # Capacities per sequence, from the budgets: a tick reuses the slots it
