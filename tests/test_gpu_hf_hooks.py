@@ -94,14 +94,16 @@ def test_dropin_tiered_kernel_matches_eager_backend(model, device):
     assert m["warm_blocks"] > 0 and m["logical_compression_x"] > 1.0
 
 
-def test_dropin_fused_step_matches_general_path(model, device, monkeypatch):
+@pytest.mark.parametrize("deterministic", [False, True])
+def test_dropin_fused_step_matches_general_path(model, device, monkeypatch, deterministic):
     # The one-call decode step (append or block opening, table update and
     # decode launch in tierkv_decode_step) against the general path of three
     # calls: the same logits and HOT pool contents (to the decode kernel's
     # run-to-run rounding, which reaches the later tokens' K/V through the
-    # hidden states), the same tables, WARM pools (written by the prefill)
-    # and block cursors.
-    print("[hf] drop-in fused decode step vs three calls", flush=True)
+    # hidden states; bit for bit with the deterministic tile hand-out), the
+    # same tables, WARM pools (written by the prefill) and block cursors.
+    print(f"[hf] drop-in fused decode step vs three calls, deterministic={deterministic}", flush=True)
+    monkeypatch.setenv("TIERKV_DETERMINISTIC", "1" if deterministic else "0")
     ids = _tokens(1, device)
     kw = dict(hot_budget=3, policy_interval=10_000, policy_mode="hot_warm", attention_backend="triton")
     rt_f = _dropin_runtime(model, **kw)
@@ -122,12 +124,16 @@ def test_dropin_fused_step_matches_general_path(model, device, monkeypatch):
     # prefill exceed the inline writes) takes the one-call path, the step
     # that opens the second decode block included.
     assert sum(taken) >= (STEPS - 1) * model.config.num_hidden_layers, taken
-    torch.testing.assert_close(got, ref, atol=2e-3, rtol=2e-3)
     pf, pg = rt_f.kv_pool, rt_g.kv_pool
+    if deterministic:
+        assert torch.equal(got, ref)
+        assert torch.equal(pf.hot_k_pool, pg.hot_k_pool) and torch.equal(pf.hot_v_pool, pg.hot_v_pool)
+    else:
+        torch.testing.assert_close(got, ref, atol=2e-3, rtol=2e-3)
+        torch.testing.assert_close(pf.hot_k_pool, pg.hot_k_pool, atol=2e-2, rtol=2e-2)
+        torch.testing.assert_close(pf.hot_v_pool, pg.hot_v_pool, atol=2e-2, rtol=2e-2)
     for k in range(pf._tables.shape[1]):
         assert torch.equal(pf._tables.view(k), pg._tables.view(k))
-    torch.testing.assert_close(pf.hot_k_pool, pg.hot_k_pool, atol=2e-2, rtol=2e-2)
-    torch.testing.assert_close(pf.hot_v_pool, pg.hot_v_pool, atol=2e-2, rtol=2e-2)
     assert torch.equal(pf.warm_k_pool, pg.warm_k_pool) and torch.equal(pf.warm_v_pool, pg.warm_v_pool)
     for layer in range(model.config.num_hidden_layers):
         cf, cg = rt_f.layer_states[layer], rt_g.layer_states[layer]

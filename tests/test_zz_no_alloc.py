@@ -193,3 +193,20 @@ def test_noalloc_first_call_then_other_stream(device):
                           text=True, timeout=300)
     print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
     assert proc.returncode == 0 and "FIRST-CALL OK" in proc.stdout
+
+
+def test_noalloc_deterministic_matches_workspace_bits(device):
+    """With the deterministic tile hand-out both entry points compute the
+    same sums in the same order: their outputs are the same bits, on two
+    calls in a row (the second smaller)."""
+    split, small = _cases()
+    for case, fmt, cold in ((split, "absmax_i8", "masked"), (small, "ref_u8", "zero_logit")):
+        print(f"[noalloc] deterministic {case.name} {fmt}", flush=True)
+        warm = oracle_warm(case, fmt)
+        inputs = to_gpu_inputs(case, warm, device)
+        out_w, sc_w = tierkv_decode_attention(**inputs, return_scores=True, cold_mode=cold, deterministic=True)
+        out_n, sc_n = tierkv_decode_attention(**inputs, return_scores=True, cold_mode=cold, deterministic=True,
+                                              workspace=NOALLOC)
+        torch.cuda.synchronize()
+        assert torch.equal(out_w.view(torch.int16), out_n.view(torch.int16))
+        assert torch.equal(sc_w.view(torch.int32), sc_n.view(torch.int32))
