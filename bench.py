@@ -289,6 +289,31 @@ def ceiling(device, c3_bytes=216944640, stream_grids=(1024, 2048, 4096), reps=50
     return res
 
 
+SETTLE_SEC = 0.06   # untimed decode launches before a decode line's warm-up steps
+
+
+def settle(plans, seconds=SETTLE_SEC, at_least=0):
+    """Keep the GPU launching ``plans`` (cycling) for at least ``seconds``
+    and ``at_least`` launches; returns the number of launches.  The clocks
+    follow the load with a lag: after the inputs are built (GPU idle) C3
+    launches run 3-8 % slow for about 20 ms, and right after the ceiling
+    measurement's streaming reads about 1 % slow for several milliseconds
+    (measured on the box: 38.6 against 38.2 us for 20 timed steps).  A decode
+    line's timed steps therefore follow this many untimed launches of the
+    same kernel, so that they see the clocks of a decode loop.  The host
+    synchronises every 200 launches, so the queue stays short."""
+    import torch
+
+    t0, i = time.perf_counter(), 0
+    while i < at_least or time.perf_counter() - t0 < seconds:
+        plans[i % len(plans)].launch()
+        i += 1
+        if i % 200 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return i
+
+
 def graph_timed(fn, n_variants, steps, warmup, passes=1):
     """Average device time of fn(i) over `steps` calls (i cycling over
     n_variants input buffers): the launches of `passes` passes over the
@@ -1120,13 +1145,15 @@ def run_decode(args, device):
     """C3 (default) / C4: one step = one decode-attention launch for one layer
     over the whole batch; ``--layers`` layer buffers rotate.
 
-    Order: the box's HBM ceilings first, then W untimed warm-up steps and
-    exactly K timed steps.  After a few seconds idle the GPU's clocks go
-    through a transient of about 20 ms of sustained load (measured on the
-    box: C3 launches run 3-8 % slow for the first ~400 launches, whatever
-    the kernel that supplies the load); the ceiling measurement (about 0.1 s
-    of streaming and gathering HBM reads) runs immediately before the decode
-    steps, so K timed steps see the steady clocks a serving loop sees.  Every launch is a
+    Order: one launch per layer (code-object load), the box's HBM ceilings,
+    at least 60 ms of untimed decode launches (``settle``; their count is in
+    the line as ``untimed_settle_launches``), then W untimed warm-up steps
+    and exactly K timed steps.  The clocks follow the load with a lag: after
+    a few seconds idle C3 launches run 3-8 % slow for about 20 ms, and right
+    after the ceiling measurement's streaming reads about 1 % slow for
+    several milliseconds, which a short timed run (K = 20) would otherwise
+    fall into; after the settle, K timed steps see the clocks a decode loop
+    sees whatever K is.  Every launch is a
     ``PreparedDecode`` (validated and bound once: one C call per step, a few
     microseconds of host time), and the K timed launches are enqueued while
     the warm-up launches still run, so the timed region holds the K kernels
@@ -1149,18 +1176,18 @@ def run_decode(args, device):
 
     plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=args.cold, splits=args.splits or None,
                             deterministic=args.deterministic) for L in layers]
-    # The first warm-up step of each layer runs before the ceiling
-    # measurement: a kernel's first launch in a process loads its code object
-    # (milliseconds of host time, the GPU idle meanwhile).
-    pre = min(args.warmup, len(plans))
-    for i in range(pre):
-        plans[i].launch()
+    # Each layer's plan is launched once before the ceiling measurement: a
+    # kernel's first launch in a process loads its code object (milliseconds
+    # of host time, the GPU idle meanwhile).
+    for plan in plans:
+        plan.launch()
     # The box's own ceiling for this access pattern: the same bytes gathered
     # as shuffled 4 KB tiles with the decode kernel's load policy, no
     # arithmetic; and a streaming read.
     ceil = ceiling(device, c3_bytes=nbytes, stream_grids=(4096,), reps=400, release=False)
+    settle_launches = settle(plans)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for i in range(pre, args.warmup):
+    for i in range(args.warmup):
         plans[i % len(plans)].launch()
     h0 = time.perf_counter()
     e0.record()
@@ -1244,6 +1271,7 @@ def run_decode(args, device):
         "tokens_per_s_32_layers": round(case.batch / (32 * sec), 1),
         "ideal_bytes_per_step": nbytes,
         "host_enqueue_us_per_launch": round(host * 1e6, 2),
+        "untimed_settle_launches": settle_launches,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": traffic},
         "measured_ceiling": measured_ceiling,
@@ -1285,13 +1313,7 @@ def extra_decode_figures(args, device, c3_sec):
         plans = [PreparedDecode(**L["args"], return_scores=scores, cold_mode=cold, deterministic=det) for L in layers]
         # Building the inputs leaves the GPU idle long enough for its clocks
         # to drop: keep it launching for >= 60 ms before the timed launches.
-        t0, i = time.perf_counter(), 0
-        while i < max(args.warmup, 4 * len(plans)) or time.perf_counter() - t0 < 0.06:
-            plans[i % len(plans)].launch()
-            i += 1
-            if i % 200 == 0:
-                torch.cuda.synchronize()
-        torch.cuda.synchronize()
+        settle(plans, at_least=max(args.warmup, 4 * len(plans)))
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for i in range(args.steps):
