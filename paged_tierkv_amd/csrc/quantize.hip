@@ -393,14 +393,6 @@ __device__ __forceinline__ float div_rn_by(float x, float s, float y) {
   return __builtin_copysignf(__builtin_fmaf(r, y, q0), q0);
 }
 
-// div_rn_by without restoring the sign of a zero quotient (x = -0 gives +0):
-// for the codes, whose next step adds the integer zero point and clamps at
-// 0, the sign of a zero makes no difference.
-__device__ __forceinline__ float div_rn_by_unsigned_zero(float x, float s, float y) {
-  const float q0 = x * y;
-  return __builtin_fmaf(__builtin_fmaf(-q0, s, x), y, q0);
-}
-
 constexpr float kRcp255 = 1.f / 255.f;   // RN(1 / 255)
 
 // RN(1 / s) for s a positive finite fp16 value held as fp32: the hardware
@@ -492,32 +484,40 @@ __global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_
   for (int i = 0; i < NV; ++i) {
     const int vi = i * 64 + lane;
     const int row = vi >> r_log2;
-    float xs[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      xs[2 * k] = half_lo(x[i][k]);
-      xs[2 * k + 1] = half_hi(x[i][k]);
-    }
     float mn, mx;
     row_min_max(x[i], r_log2, mn, mx);
     if (vi < valid_vec) {
-      // The quotients below are correctly rounded without an IEEE division
-      // each (div_rn_by: one reciprocal per row, an FMA correction per
-      // quotient); a non-finite operand takes the plain IEEE result.
+      // The scale is stored, so its quotient is correctly rounded without an
+      // IEEE division (div_rn_by); a non-finite operand takes the plain IEEE
+      // result.  The other quotients only feed round(): for every finite
+      // fp16 x and positive finite fp16 s, rint(RN16(RN32(x * RN32(1 / s))))
+      // equals rint(RN16(RN32(x / s))) (tests/native/quotient_rint_check.c
+      // checks all 2.0e9 pairs, also with the product rounded to fp16 once),
+      // so one multiply per element by the row's correctly rounded reciprocal
+      // gives the reference's integers (y > 0 keeps the sign of a zero).
       const float a = r16(mx - mn);
       float sc = __builtin_isfinite(a) ? div_rn_by(a, 255.f, kRcp255) : a;   // (max - min) / 255.0
       sc = r16(sc);
       if (sc == 0.f) sc = 1.f;                            // torch.where(scale == 0, 1, scale)
-      float qt[8], qm;
+      // The words go through scalars (see row_min_max).
+      const uint32_t ws[4] = {x[i].x, x[i].y, x[i].z, x[i].w};
+      h2 qt[4];
+      float qm;
       if (__builtin_isfinite(sc)) {
         const float y = rcp_rn_f16_value(sc);   // sc: a positive finite fp16 value
-        qm = div_rn_by(mn, sc, y);
+        qm = mn * y;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qt[e] = div_rn_by_unsigned_zero(xs[e], sc, y);
+        for (int k = 0; k < 4; ++k) {
+          const h2 v = __builtin_bit_cast(h2, ws[k]);
+          qt[k] = h2{static_cast<_Float16>(static_cast<float>(v[0]) * y),
+                     static_cast<_Float16>(static_cast<float>(v[1]) * y)};
+        }
       } else {   // a row holding an infinity
         qm = __fdiv_rn(mn, sc);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qt[e] = __fdiv_rn(xs[e], sc);
+        for (int k = 0; k < 4; ++k)
+          qt[k] = h2{static_cast<_Float16>(__fdiv_rn(half_lo(ws[k]), sc)),
+                     static_cast<_Float16>(__fdiv_rn(half_hi(ws[k]), sc))};
       }
       const float zp = r16(-rintf(r16(qm)));              // -round(min / scale)
       // round(x / scale) + zp, clamp(0, 255), in fp16 two at a time.  The
@@ -530,8 +530,7 @@ __global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_
       uint32_t hb[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        h2 t = {static_cast<_Float16>(qt[2 * k]), static_cast<_Float16>(qt[2 * k + 1])};
-        t = __builtin_elementwise_rint(t);
+        h2 t = __builtin_elementwise_rint(qt[k]);
         t = t + h2{zh, zh};
         t = __builtin_elementwise_min(__builtin_elementwise_max(t, h2{0, 0}), h2{255, 255});
         t = t + h2{1024, 1024};

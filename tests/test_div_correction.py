@@ -1,9 +1,11 @@
-"""The reference-format quantizer on the GPU divides each fp16 value by its
-row's scale with one reciprocal per row and Markstein's FMA correction per
-element instead of an IEEE division per element.  This test compiles
-tests/native/div_correction_check.c with gcc and checks, over every finite
-fp16 numerator and every positive finite fp16 scale (2.0e9 pairs), that the
-corrected quotient equals the IEEE quotient bit for bit."""
+"""Exhaustive CPU proofs for the divisions of the reference-format quantizer
+on the GPU, which uses one reciprocal per token row instead of an IEEE
+division per element.  The stored scale's quotient takes Markstein's FMA
+correction (tests/native/div_correction_check.c: equal to the IEEE quotient
+bit for bit over every finite fp16 numerator and positive finite fp16 scale,
+2.0e9 pairs); the reciprocal comes from the hardware estimate and a Newton
+step (tests/native/rcp_newton_check.c); the per-element quotients, which
+only feed round(), take one multiply (tests/native/quotient_rint_check.c)."""
 
 from __future__ import annotations
 
@@ -38,3 +40,19 @@ def test_reciprocal_newton_step_is_correctly_rounded(tmp_path):
     res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert res.returncode == 0, res.stdout + res.stderr
     assert res.stdout.strip() == "cases 95229 mismatches 0"
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_quotient_by_reciprocal_rounds_to_the_same_integer(tmp_path):
+    """The quantizer's per-element quotients only feed round(): the kernel
+    multiplies by the row's correctly rounded reciprocal instead of dividing.
+    tests/native/quotient_rint_check.c checks, over every finite fp16
+    numerator and every positive finite fp16 scale, that
+    rint(RN16(RN32(x * RN32(1 / s)))) -- and the same with the product
+    rounded to fp16 once -- equals the reference's rint(RN16(RN32(x / s)))."""
+    exe = tmp_path / "quotient_rint_check"
+    src = os.path.join(HERE, "native", "quotient_rint_check.c")
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-fopenmp", src, "-o", str(exe), "-lm"], check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert res.stdout.strip() == "pairs 2015299584 mismatches 0 0"
