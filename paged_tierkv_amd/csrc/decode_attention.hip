@@ -924,9 +924,16 @@ __global__ __launch_bounds__(MAX_WAVES * 64) void tiered_decode_kernel(
         // chunks are ranked without branches, so their scalar reads overlap.
         const int tot_h = __builtin_amdgcn_readlane(ih, nj - 1);
         const int tot_w = __builtin_amdgcn_readlane(iw, nj - 1);
-        const int lo_h = div_splits(tot_h * split), lo_w = div_splits(tot_w * split);
-        own_h = div_splits(tot_h * (split + 1)) - lo_h;
-        own_w = div_splits(tot_w * (split + 1)) - lo_w;
+        // x / splits without branches: a row of one pass has num_blocks *
+        // splits < 2^32, so the multiply-high is exact whenever splits > 1.
+        auto div_one = [&](int x) -> int {
+          uint32_t qq = __umulhi(uint32_t(x), a_split_magic);
+          qq -= (qq * uint32_t(splits) > uint32_t(x)) ? 1u : 0u;
+          return splits == 1 ? x : int(qq);
+        };
+        const int lo_h = div_one(tot_h * split), lo_w = div_one(tot_w * split);
+        own_h = div_one(tot_h * (split + 1)) - lo_h;
+        own_w = div_one(tot_w * (split + 1)) - lo_w;
         const int rh = ih - ch - lo_h;
         const int rw = iw - cw - lo_w;
         const int wu = uniform(w);
