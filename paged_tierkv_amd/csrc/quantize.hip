@@ -492,7 +492,8 @@ __global__ __launch_bounds__(QT) void demote_ref_wave_kernel(QuantJobs q, int32_
       // result.  The other quotients only feed round(): for every finite
       // fp16 x and positive finite fp16 s, rint(RN16(RN32(x * RN32(1 / s))))
       // equals rint(RN16(RN32(x / s))) (tests/native/quotient_rint_check.c
-      // checks all 2.0e9 pairs, also with the product rounded to fp16 once),
+      // checks all 2.0e9 pairs, also with the product rounded to fp16 once:
+      // the fp16 quotients differ only below 2^-14, where both round to 0),
       // so one multiply per element by the row's correctly rounded reciprocal
       // gives the reference's integers (y > 0 keeps the sign of a zero).
       const float a = r16(mx - mn);

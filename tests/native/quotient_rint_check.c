@@ -12,10 +12,11 @@
  * this program checks t' == t.  It also checks the form in which the product
  * is rounded to fp16 once, rint(RN16(x * y)) with x * y exact, so the result
  * holds whether or not the compiler fuses the multiply and the conversion.
- * (The fp16 quotients themselves differ in a few thousand pairs; none of them
- * changes the rounded integer.)  RN16 is round-to-nearest-even onto the fp16
- * value set, infinity beyond 65504 + 16; rint rounds half to even.  Prints
- * the pair count and both mismatch counts and exits 1 if either is nonzero.
+ * (The fp16 quotients themselves differ in a few thousand pairs in either
+ * form, all with quotients below 2^-14, the fp16 subnormal range, where rint
+ * gives 0.)  RN16 is round-to-nearest-even onto the fp16 value set, infinity
+ * beyond 65504 + 16; rint rounds half to even.  Prints the pair count and
+ * both mismatch counts and exits 1 if either is nonzero.
  * Build: gcc -O2 -ffp-contract=off -fopenmp quotient_rint_check.c -lm. */
 #include <math.h>
 #include <stdint.h>
