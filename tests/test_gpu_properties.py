@@ -42,11 +42,11 @@ def _launch(case, warm, device, c):
 
 @st.composite
 def tier_cases(draw):
-    batch = draw(st.integers(1, 3))
+    batch = draw(st.integers(1, 6))
     kv = draw(st.sampled_from([1, 2, 4]))
     groups = draw(st.sampled_from([1, 2, 4, 8, 16]))
     head_dim = draw(st.sampled_from([64, 128]))
-    nb = draw(st.integers(1, 80))
+    nb = draw(st.integers(1, 200))
     hot_frac = draw(st.floats(0.0, 1.0))
     warm_frac = draw(st.floats(0.0, 1.0 - hot_frac))
     n_hot = min(nb, int(round(nb * hot_frac)))
@@ -63,7 +63,7 @@ def tier_cases(draw):
                               recent_hot=draw(st.integers(0, 2)))
     return dict(case=case, fmt=draw(st.sampled_from(["absmax_i8", "ref_u8"])),
                 cold=draw(st.sampled_from(["masked", "zero_logit"])), scores=draw(st.booleans()),
-                splits=draw(st.sampled_from([None, 1, 2, 3])), det=draw(st.booleans()))
+                splits=draw(st.sampled_from([None, 1, 2, 3, 4, 7, 16])), det=draw(st.booleans()))
 
 
 @settings(max_examples=40, deadline=None, derandomize=True, database=None,
