@@ -12,7 +12,13 @@ other GPU tests:
 * block mass from probabilities (bit for bit) and tier labels (exactly) over
   random shapes, block sizes, lengths, budgets, modes and score ties
   (compute_block_scores, tierkv_policy.py:1380-1389; enforce_budget /
-  enforce_tiered_budget, 1391-1477).
+  enforce_tiered_budget, 1391-1477);
+* the batched runtime over random scenarios (batch, kv heads, group, head
+  dim, prompt length from one token, steps, tick interval, budgets, policy
+  mode, WARM format, COLD mode): tables, states, lengths and pool contents
+  equal to oracle.runtime after the prefill and after every step, decode
+  outputs within BASELINE's tolerance (the runtime generalises
+  TieredKVRuntime, tierkv_policy.py:1534-1912, to a batch).
 
 The seeds are fixed, so every run draws the same cases."""
 
@@ -24,7 +30,12 @@ import torch
 
 from oracle import codec
 from oracle import policy as opolicy
+from oracle.runtime import BatchedRuntimeOracle
 from paged_tierkv_amd import kernels
+from paged_tierkv_amd.runtime import BatchedTieredKVRuntime
+
+from helpers import assert_close
+from test_gpu_runtime import _compare, _oracle_out
 
 pytestmark = pytest.mark.gpu
 
@@ -142,3 +153,55 @@ def test_block_mass_and_labels_random_shapes(device, seed):
         got = kernels.tier_labels(torch.from_numpy(scores).to(device), torch.from_numpy(cur).to(device), hot, warm,
                                   mode, demoted_state=demoted)
         assert np.array_equal(got.cpu().numpy(), exp), f"labels it={it} n={n} hot={hot} warm={warm} mode={mode}"
+
+
+def test_batched_runtime_random_scenarios(device):
+    rng = np.random.default_rng(5)
+    for sc in range(8):
+        B = int(rng.integers(1, 7))
+        kv = int(rng.choice([1, 2, 4]))
+        G = int(rng.choice([1, 2, 4, 8]))
+        D = int(rng.choice([64, 128]))
+        bs = 16
+        prompt, steps, interval = int(rng.integers(1, 600)), int(rng.integers(5, 70)), int(rng.integers(1, 17))
+        policy_mode = str(rng.choice(["hot_warm_cold", "hot_warm"]))
+        warm_format = str(rng.choice(["absmax_i8", "ref_u8"]))
+        cold_mode = str(rng.choice(["masked", "zero_logit"]))
+        hot_f = float(rng.uniform(0.05, 0.6))
+        warm_f = float(rng.uniform(0.0, 1.0 - hot_f))
+        print(f"[sweep] runtime sc={sc} B={B} kv={kv} G={G} D={D} prompt={prompt} steps={steps} "
+              f"interval={interval} mode={policy_mode} fmt={warm_format} cold={cold_mode}", flush=True)
+        gen = torch.Generator().manual_seed(int(rng.integers(0, 2 ** 31)))
+        rt = BatchedTieredKVRuntime(1, B, kv, D, prompt + steps + 16, block_size=bs, hot_fraction=hot_f,
+                                    warm_fraction=warm_f, policy_mode=policy_mode, policy_interval=interval,
+                                    warm_format=warm_format, cold_mode=cold_mode, device=device)
+        orc = BatchedRuntimeOracle(B, kv, D, bs, rt.max_blocks, rt.hot_slots, rt.warm_slots, policy_mode,
+                                   warm_format)
+        k = torch.randn((B, kv, prompt, D), generator=gen).half()
+        v = torch.randn((B, kv, prompt, D), generator=gen).half()
+        n0 = -(-prompt // bs)
+        scores = torch.rand((B, n0), generator=gen)
+        rt.prefill_layer(0, k.to(device), v.to(device), block_scores=scores)
+        hot_b, warm_b = rt.budgets(n0)
+        orc.prefill(k.numpy(), v.numpy(), scores.numpy(), hot_b, warm_b)
+        torch.cuda.synchronize()
+        _compare(rt, orc, f"sc={sc} prefill")
+        scaling = D ** -0.5
+        for step in range(steps):
+            tick = rt.begin_step()
+            q = torch.randn((B, kv * G, 1, D), generator=gen).half()
+            k1 = torch.randn((B, kv, 1, D), generator=gen).half()
+            v1 = torch.randn((B, kv, 1, D), generator=gen).half()
+            out = rt.decode_layer(0, q.to(device), k1.to(device), v1.to(device), G, scaling, policy_step=tick)
+            orc.append(k1.numpy(), v1.numpy())
+            exp = _oracle_out(rt, orc, q[:, :, 0].numpy(), G, scaling, cold_mode)
+            assert_close(out[:, 0].float().cpu().numpy(), exp, what=f"sc={sc} step {step} output")
+            if tick:
+                hb, wb = rt.budgets(int(orc.nb.max()))
+                orc.tick(rt.last_score_sums.cpu().numpy(), hb, wb)
+            rt.end_step()
+            torch.cuda.synchronize()
+            _compare(rt, orc, f"sc={sc} step {step}{' (tick)' if tick else ''}")
+        rt.check_errors()
+        del rt
+        torch.cuda.empty_cache()
