@@ -18,7 +18,11 @@ other GPU tests:
   mode, WARM format, COLD mode): tables, states, lengths and pool contents
   equal to oracle.runtime after the prefill and after every step, decode
   outputs within BASELINE's tolerance (the runtime generalises
-  TieredKVRuntime, tierkv_policy.py:1534-1912, to a batch).
+  TieredKVRuntime, tierkv_policy.py:1534-1912, to a batch);
+* prefill block scores over random batch, GQA group (1-8), prompt length,
+  head dim, block size, dtype and logit scale, at 1e-4 relative to the
+  float64 oracle (compute_block_scores on the eager prefill attention,
+  tierkv_policy.py:1380-1389).
 
 The seeds are fixed, so every run draws the same cases."""
 
@@ -30,6 +34,7 @@ import torch
 
 from oracle import codec
 from oracle import policy as opolicy
+from oracle.policy import prefill_block_mass as oracle_prefill_mass
 from oracle.runtime import BatchedRuntimeOracle
 from paged_tierkv_amd import kernels
 from paged_tierkv_amd.runtime import BatchedTieredKVRuntime
@@ -205,3 +210,22 @@ def test_batched_runtime_random_scenarios(device):
         rt.check_errors()
         del rt
         torch.cuda.empty_cache()
+
+
+def test_prefill_block_mass_random_shapes(device):
+    rng = np.random.default_rng(2)
+    for it in range(12):
+        hkv = int(rng.choice([1, 2, 4, 8]))
+        g_ = int(rng.integers(1, 9))
+        b, t = int(rng.integers(1, 4)), int(rng.integers(1, 700))
+        d, bs = int(rng.choice([64, 128])), int(rng.choice([16, 32, 64]))
+        dtype = torch.float16 if rng.random() < 0.7 else torch.bfloat16
+        sc = float(rng.uniform(0.3, 3.0))
+        print(f"[sweep] prefill it={it} B={b} H={hkv * g_} Hkv={hkv} T={t} D={d} bs={bs} {dtype} scale={sc:.2f}",
+              flush=True)
+        gen = torch.Generator().manual_seed(100 + it)
+        q = (torch.randn((b, hkv * g_, t, d), generator=gen) * sc).to(dtype)
+        k = (torch.randn((b, hkv, t, d), generator=gen) * sc).to(dtype)
+        got = kernels.prefill_block_mass(q.to(device), k.to(device), bs, d ** -0.5).cpu().numpy()
+        want = oracle_prefill_mass(q.float().numpy(), k.float().numpy(), d ** -0.5, bs)
+        np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-9, err_msg=f"prefill it={it}")
