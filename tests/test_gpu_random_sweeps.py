@@ -1,14 +1,16 @@
 """Seeded random sweeps against the oracle, beyond the fixed shapes of the
 other GPU tests:
 
-* demotion in both WARM formats over random geometry (kv heads 1-8, block
+* demotion in both WARM formats, and promotion of the demoted slots, over
+  random geometry (kv heads 1-8, block
   sizes 1-64, head dims including ones the one-wave kernels do not take),
   job counts, lengths (0 included), the zero-padded tail or not, and value
   mixes chosen to reach the codec's edges: exact ties, subnormals, constant
   rows, all-positive rows (negative zero points) and magnitudes near the
   fp16 maximum (a row whose range overflows to infinity takes the IEEE
-  path).  Codes, scales and zero points bit for bit (quantize_fp16_to_int8,
-  tierkv_policy.py:21-36; BASELINE's absmax codec);
+  path).  Codes, scales, zero points and the promoted fp16 values bit for
+  bit (quantize_fp16_to_int8 / dequantize_int8_to_fp16,
+  tierkv_policy.py:21-44; BASELINE's absmax codec);
 * block mass from probabilities (bit for bit) and tier labels (exactly) over
   random shapes, block sizes, lengths, budgets, modes and score ties
   (compute_block_scores, tierkv_policy.py:1380-1389; enforce_budget /
@@ -72,8 +74,10 @@ def _values(rng, shape):
     return np.clip(v, -65504, 65504).astype(np.float16)
 
 
-# Rows near the fp16 maximum overflow the oracle's fp16 range on purpose.
+# Rows near the fp16 maximum overflow the oracle's fp16 range on purpose (an
+# infinite scale then dequantizes a zero offset to NaN, in both).
 @pytest.mark.filterwarnings("ignore:overflow encountered in cast:RuntimeWarning")
+@pytest.mark.filterwarnings("ignore:invalid value encountered in multiply:RuntimeWarning")
 @pytest.mark.parametrize("seed", [3, 7])
 def test_demotion_random_geometry_bit_exact(device, seed):
     rng = np.random.default_rng(seed)
@@ -121,6 +125,25 @@ def test_demotion_random_geometry_bit_exact(device, seed):
                     q, scale = codec.quantize_absmax_i8(src[s, :, :ln])
                     _eq(codes[d, :, :ln].cpu().numpy(), q, f"codes {what}")
                     _eq(sc[d].cpu().numpy(), scale, f"scale {what}")
+        # Promotion of the same slots back to fp16 into fresh HOT slots:
+        # dequantize_int8_to_fp16 (tierkv_policy.py:39-44) of the stored codes,
+        # or fp16(code * scale) for absmax; tokens past a job's length untouched.
+        hot_k = torch.full((n, heads, bs, dim), 9.0, dtype=torch.float16, device=device)
+        hot_v = hot_k.clone()
+        kernels.promote_to_hot(warm_k, warm_v, ks, kz, vs, vz, torch.from_numpy(dst),
+                               torch.arange(n, dtype=torch.int32), torch.from_numpy(lens), hot_k, hot_v,
+                               warm_format=fmt)
+        torch.cuda.synchronize()
+        for i in range(n):
+            d, ln = int(dst[i]), int(lens[i])
+            for nm, codes, sc, zp, hot in (("k", warm_k, ks, kz, hot_k), ("v", warm_v, vs, vz, hot_v)):
+                c = codes[d, :, :ln].cpu().numpy()
+                if fmt == "ref_u8":
+                    exp = codec.dequantize_ref_u8(c, sc[d, :, :ln].cpu().numpy(), zp[d, :, :ln].cpu().numpy())
+                else:
+                    exp = (c.astype(np.float32) * sc[d].cpu().numpy()[:, None, None]).astype(np.float16)
+                _eq(hot[i, :, :ln].cpu().numpy(), exp, f"promote {nm} it={it} job={i}")
+                assert (hot[i, :, ln:].cpu() == 9.0).all(), f"promote {nm} it={it} job={i}: tail written"
 
 
 @pytest.mark.parametrize("seed", [1, 11])
